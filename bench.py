@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Benchmark of the SimSD matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2]
+
+Workloads (synthetic data, bf16, random-init weights of the named shapes):
+  c2      default: the SDAR-1.7B-shape draft linear set at M=4 -- 28 layers x
+          {qkv 2048->4096, o 2048->2048, gate_up 2048->12288, down 6144->2048},
+          weights ~N(0, 0.02) with a fresh seed per layer, activations ~N(0, 1).
+          One step = the 112 linears once (2.83 GB of weights, > the 256 MB MALL).
+  c1      the merged gate_up 2048->12288 at M=4 alone, cycled over 24 distinct
+          weights (1.2 GB) so the MALL cannot serve repeats.
+  c3m16 / c3m32
+          8B-shape target verify set, 36 layers x {qkv 4096->6144, o 4096->4096,
+          gate_up 4096->24576, down 12288->4096} + lm_head 4096->151936, M=16/32.
+  c4t4 / c4t16 / c4t64
+          MoE step (route top-8 softmax over 256 experts -> align -> grouped
+          gate_up + SiLU.mul -> down -> combine, + one shared expert),
+          H=2048, I=512, T tokens; cycled over 8 distinct layers.
+Each step is captured once in a HIP graph and replayed; the timed region is
+K replays bracketed by synchronisations and HIP events on the replay stream.
+
+value = algorithmic bytes per step / time per step (weights read once +
+activations in + outputs out).  The roofline object is for the dominant
+kernel; every launch in the c1/c2/c3 timed region is that kernel, so its
+average launch duration is the region time / launches.  Per-launch event
+timings of one eager pass are reported alongside (kernel time without the
+inter-launch gaps).  The CPU baseline is the reference's CPU path -- torch
+F.linear in bf16 (its oracle ref_thin_linear) or the stock MoE loop --
+timed on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+sys.path.insert(0, os.path.join(REPO, "simsd-release_amd"))
+
+METRIC = "skinny-GEMM HBM GB/s (% of peak) at M=4/16/32; spec-decode tok/s on 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16 = 2
+
+DRAFT = [("qkv", 2048, 4096), ("o", 2048, 2048), ("gate_up", 2048, 12288), ("down", 6144, 2048)]
+TARGET = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 24576), ("down", 12288, 4096)]
+LM_HEAD_TARGET = ("lm_head", 4096, 151936)
+
+
+def linear_bytes(M, K, N):
+    return N * K * BF16 + M * K * BF16 + M * N * BF16
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ───────────────────────────────────────────────────────────── workloads ───
+def make_linear_calls(torch, dev, workload):
+    """[(op name, x, w)] for one step."""
+    calls = []
+
+    def rand(shape, scale, seed):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * scale).to(torch.bfloat16)
+
+    if workload == "c2":
+        M = 4
+        for layer in range(28):
+            for j, (name, K, N) in enumerate(DRAFT):
+                seed = 1000 + layer * 16 + j
+                calls.append((name, rand((M, K), 1.0, seed), rand((N, K), 0.02, seed + 100000)))
+        return M, calls
+    if workload == "c1":
+        M, K, N = 4, 2048, 12288
+        for i in range(24):
+            calls.append(("gate_up", rand((M, K), 1.0, 50 + i), rand((N, K), 0.02, 5000 + i)))
+        return M, calls
+    if workload in ("c3m16", "c3m32"):
+        M = 16 if workload == "c3m16" else 32
+        for layer in range(36):
+            for j, (name, K, N) in enumerate(TARGET):
+                seed = 2000 + layer * 16 + j
+                calls.append((name, rand((M, K), 1.0, seed), rand((N, K), 0.02, seed + 100000)))
+        name, K, N = LM_HEAD_TARGET
+        calls.append((name, rand((M, K), 1.0, 7), rand((N, K), 0.02, 8)))
+        return M, calls
+    raise ValueError(workload)
+
+
+def cpu_baseline_linear(torch, workload, M):
+    """torch CPU F.linear (bf16) on a bounded sample: 4 distinct layers of the
+    workload's shapes, cycled to one full step."""
+    from oracle.thin_linear import linear_cpu_torch
+
+    shapes = DRAFT if workload in ("c2", "c1") else TARGET
+    n_layers = {"c2": 28, "c1": 0}.get(workload, 36)
+    if workload == "c1":
+        shapes = [("gate_up", 2048, 12288)]
+    g = torch.Generator().manual_seed(0)
+    sample_layers = 4 if workload != "c1" else 8
+    layers = []
+    for _ in range(sample_layers):
+        layers.append([(torch.randn(M, K, generator=g).to(torch.bfloat16),
+                        (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16))
+                       for _, K, N in shapes])
+    per_layer_bytes = sum(linear_bytes(M, K, N) for _, K, N in shapes)
+    step_layers = n_layers if n_layers else 24
+
+    def step():
+        for i in range(step_layers):
+            for x, w in layers[i % sample_layers]:
+                linear_cpu_torch(x, w)
+
+    step()                                  # warmup
+    times = []
+    t_end = time.perf_counter() + 12.0
+    while len(times) < 20 and (time.perf_counter() < t_end or len(times) < 3):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    byts = per_layer_bytes * step_layers
+    return {
+        "value": round(byts / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"torch CPU F.linear bf16 (the reference oracle ref_thin_linear), M={M}, "
+                   f"{sample_layers} distinct layers of {[s[0] for s in shapes]} "
+                   f"({sample_layers * per_layer_bytes / 1e6:.0f} MB of weights) cycled to one "
+                   f"{step_layers}-layer step; median of {len(times)} steps "
+                   f"({med * 1e3:.1f} ms/step); cpu={cpu_model()}; os.cpu_count={os.cpu_count()}"),
+    }
+
+
+def run_linear(args, torch, dev):
+    from kernels.thin_linear_fused import thin_linear
+
+    M, calls = make_linear_calls(torch, dev, args.workload)
+    step_bytes = sum(linear_bytes(M, x.shape[1], w.shape[0]) for _, x, w in calls)
+    launches = len(calls)
+
+    def step():
+        return [thin_linear(x, w) for _, x, w in calls]
+
+    with torch.inference_mode():
+        # eager warmup: allocates the split-K workspace before capture
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        # one eager pass with an event pair around every launch: kernel time
+        # per op without the gaps between launches
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in calls]
+        for (name, x, w), (e0, e1) in zip(calls, evs):
+            e0.record()
+            thin_linear(x, w)
+            e1.record()
+        torch.cuda.synchronize()
+        per_op = {}
+        for (name, x, w), (e0, e1) in zip(calls, evs):
+            us = e0.elapsed_time(e1) * 1e3
+            d = per_op.setdefault(name, {"K": x.shape[1], "N": w.shape[0], "us": [], "bytes": 0})
+            d["us"].append(us)
+            d["bytes"] = linear_bytes(M, x.shape[1], w.shape[0])
+        eager_bytes = sum(d["bytes"] * len(d["us"]) for d in per_op.values())
+        eager_us = sum(sum(d["us"]) for d in per_op.values())
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(args.steps):
+            graph.replay()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    avg_launch_us = ms * 1e3 / launches
+    breakdown = {
+        n: {"K": d["K"], "N": d["N"], "calls": len(d["us"]),
+            "us_per_call": round(statistics.mean(d["us"]), 3),
+            "GB/s": round(d["bytes"] / (statistics.mean(d["us"]) * 1e-6) / 1e9, 1),
+            "frac": round(d["bytes"] / (statistics.mean(d["us"]) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        for n, d in per_op.items()}
+    result = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": {"c2": "draft-linear-set-M4-28L", "c1": "gate_up-2048x12288-M4",
+                                "c3m16": "target-verify-set-M16-36L+lm_head",
+                                "c3m32": "target-verify-set-M32-36L+lm_head"}[args.workload],
+                   "M": M, "launches_per_step": launches, "algorithmic_bytes_per_step": step_bytes,
+                   "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(step_bytes / launches / (avg_launch_us * 1e-6) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(step_bytes / launches / (avg_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "thin_gemm_kernel",
+                     "bytes_per_launch": round(step_bytes / launches),
+                     "avg_launch_us": round(avg_launch_us, 3),
+                     "eager_event_kernel_us": round(eager_us / launches, 3),
+                     "eager_event_GBs": round(eager_bytes / (eager_us * 1e-6) / 1e9, 1)},
+        "breakdown": breakdown,
+        "tflops": round(sum(2 * M * x.shape[1] * w.shape[0] for _, x, w in calls) / (ms * 1e-3) / 1e12, 2),
+    }
+    return result, M
+
+
+# ────────────────────────────────────────────────────────────────── MoE ───
+def run_moe(args, torch, dev):
+    from kernels.moe_dispatch_fused import moe_forward, moe_route
+
+    T = int(args.workload[len("c4t"):])
+    E, k, H, I, L = 256, 8, 2048, 512, 8
+    layers = []
+    for layer in range(L):
+        g = torch.Generator(device=dev).manual_seed(300 + layer)
+        mk = lambda *s: (torch.randn(*s, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+        logits = torch.randn(T, E, device=dev, generator=g)
+        x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+        layers.append((x, logits, mk(E, I, H), mk(E, I, H), mk(E, H, I), (mk(I, H), mk(I, H), mk(H, I))))
+    per_expert = (2 * I * H + H * I) * BF16
+    total_bytes = 0
+    with torch.inference_mode():
+        for x, logits, *_ in layers:
+            ids, _ = moe_route(logits, k, scoring="softmax", renorm=False)
+            n_active = int(torch.unique(ids).numel())
+            total_bytes += (n_active + 1) * per_expert + T * H * BF16 * 2 + T * E * 4 + T * k * 12
+
+    def step():
+        return [moe_forward(x, lg, k, wg, wu, wd, shared=sh, scoring="softmax", renorm=False)
+                for x, lg, wg, wu, wd, sh in layers]
+
+    with torch.inference_mode():
+        step()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms_graph = t0.elapsed_time(t1) / args.steps
+    ms = ms_graph / L
+    gbs = total_bytes / L / (ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"moe-step-T{T}-E{E}-k{k}-H{H}-I{I}+shared", "T": T,
+                   "layers_cycled": L, "algorithmic_bytes_per_step": total_bytes // L,
+                   "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "moe step (5 launches)"},
+    }, T
+
+
+def cpu_baseline_moe(torch, T):
+    """The stock per-expert loop (oracle restatement, fp64 numpy) on one layer."""
+    import numpy as np
+    from oracle import moe as omoe
+
+    E, k, H, I = 256, 8, 2048, 512
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((T, H))
+    logits = rng.standard_normal((T, E))
+    ids, w = omoe.route_topk(logits, k, scoring="softmax", renorm=False)
+    act = np.unique(ids)
+    wg = rng.standard_normal((E, I, H)) * 0.02
+    wu = rng.standard_normal((E, I, H)) * 0.02
+    wd = rng.standard_normal((E, H, I)) * 0.02
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        omoe.dispatch_grouped(x, ids, w, wg, wu, wd, dtype="bf16")
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    byts = (act.size) * (2 * I * H + H * I) * BF16
+    return {"value": round(byts / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle stock per-expert loop (numpy fp64), one layer T={T}, "
+                      f"median of 3 ({med * 1e3:.1f} ms); cpu={cpu_model()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; --gpus must be 1 (the hot path "
+              "needs no communication; multi-GPU sharding is described in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.workload.startswith("c4"):
+        result, T = run_moe(args, torch, dev)
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = cpu_baseline_moe(torch, T)
+    else:
+        result, M = run_linear(args, torch, dev)
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = cpu_baseline_linear(torch, args.workload, M)
+    result["device"] = torch.cuda.get_device_name(dev)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,141 @@
+/*
+ * libsimsd_kernels.so -- C ABI of the SimSD matmul hot path on MI355X (gfx950).
+ *
+ * Plain C: raw device pointers, element strides, sizes, and the HIP stream as
+ * an opaque pointer (hipStream_t, e.g. torch.cuda.current_stream().cuda_stream).
+ * Every entry point is stream-ordered, never synchronises the host, never
+ * allocates device memory, and returns 0 on success or -1 with a message left
+ * in simsd_last_error_string() (per thread).  The caller owns every buffer,
+ * workspaces included.  Launches go to the current HIP device: callers make
+ * the tensors' device current first (the reference's device guard,
+ * kernels/moe_dispatch_fused.py:145-151).
+ *
+ * Reference entry points each function replaces are cited as file:line in the
+ * airevo2/SimSD-release tree.
+ */
+#ifndef SIMSD_KERNELS_H_
+#define SIMSD_KERNELS_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIMSD_ABI_VERSION 1
+
+/* dtype codes */
+#define SIMSD_DTYPE_BF16 0
+#define SIMSD_DTYPE_F16 1
+#define SIMSD_DTYPE_F32 2
+
+/* routing scores */
+#define SIMSD_SCORE_SOFTMAX 0
+#define SIMSD_SCORE_SIGMOID 1
+
+#define SIMSD_MOE_MAX_EXPERTS 1024
+#define SIMSD_MOE_MAX_SLOTS 8192
+
+/* ---- housekeeping ---------------------------------------------------- */
+int simsd_abi_version(void);
+const char* simsd_last_error_string(void);
+
+/* ---- skinny linear ------------------------------------------------------
+ * y[m, n] = sum_k x[m, k] * w[n, k]  (+ bias[n]), fp32 accumulation, y in the
+ * input dtype.  Replaces the launch of _thin_gemv_kernel (+ _thin_gemv_reduce
+ * when SPLIT_K > 1) in thin_linear, kernels/thin_linear_fused.py:321-344, and
+ * the kernels themselves (67-171).
+ *   strides are in elements; any stride works (non-unit K strides and
+ *   unaligned rows take a slower element-wise path);
+ *   block_n: weight rows per workgroup (16 or 32; 0 = 16);
+ *   split_k: workgroups along K (0 = automatic); the split partials are summed
+ *            in index order (deterministic);
+ *   num_waves: waves per workgroup splitting K (2, 4 or 8; 0 = 4);
+ *   workspace: needed only when split_k > 1 (size from
+ *            simsd_thin_linear_workspace_bytes); must be zero-filled once
+ *            before first use -- every call leaves its counters at zero.
+ * K must be >= 1 (the caller handles K == 0). */
+int simsd_thin_linear(const void* x, int64_t stride_xm, int64_t stride_xk,
+                      const void* w, int64_t stride_wn, int64_t stride_wk,
+                      const void* bias, int64_t stride_b,
+                      void* y, int64_t stride_ym, int64_t stride_yn,
+                      int64_t M, int64_t N, int64_t K, int dtype,
+                      int block_n, int split_k, int num_waves,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes simsd_thin_linear needs for this shape/config (0 if none).
+ * Plays the role of _partials(), kernels/thin_linear_fused.py:177-185. */
+int64_t simsd_thin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype,
+                                          int block_n, int split_k, int num_waves);
+
+/* The launch geometry simsd_thin_linear picks: out4 = {rows per workgroup,
+ * columns per block, waves per workgroup, split_k}.  Counterpart of
+ * pick_config / _heuristic_config, kernels/thin_linear_fused.py:217-262. */
+int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype, int block_n,
+                           int split_k, int num_waves, int* out4);
+
+/* ---- MoE: routing ------------------------------------------------------
+ * ids_out[t, j] (int64) = index of the j-th largest logit of row t (ties to
+ * the lower index); w_out[t, j] (fp32) = score of that expert, where score is
+ * softmax over all E logits or sigmoid of the logit, renormalised over the k
+ * picks when renorm != 0 and k > 1 (denominator + 1e-20), times scale.
+ * Not part of the reference operator (the gate is remote LLaDA2 code); the
+ * sigmoid/renorm/scale rule restates _routing,
+ * kernels/workspace/moe_dispatch/build_oracle.py:71-90.  k <= 64, E <= 1024. */
+int simsd_moe_route_topk(const float* logits, int64_t T, int64_t E, int64_t stride_t, int k,
+                         int scoring, int renorm, float scale, int64_t* ids_out, float* w_out,
+                         void* stream);
+
+/* ---- MoE: align -------------------------------------------------------
+ * Worst-case tile count min(E, M) + ceil(M / 16) for M = T*k slots.
+ * _num_tiles, kernels/moe_dispatch_fused.py:135-137. */
+int simsd_moe_num_tiles(int64_t M, int64_t E);
+
+/* Sort the M = T*k flat slots by expert (stable) and lay each expert's group
+ * out on 16-row boundaries.  Replaces _align, kernels/moe_dispatch_fused.py:93-132.
+ *   counts[E]          slots per expert
+ *   offsets[E+1]       exclusive scan of counts (offsets[E] = valid slots)
+ *   pad_offsets[E+1]   exclusive scan of counts rounded up to 16
+ *   perm[M]            slot ids in sorted order (argsort(ids, stable=True));
+ *                      ids outside [0, E) sort last, in slot order
+ *   slots[16*num_tiles] slot id per padded row, -1 for padding
+ *   tile_expert[num_tiles] expert of each 16-row tile, E past the used range
+ * One workgroup; E <= 1024, M <= 8192. */
+int simsd_moe_align(const int64_t* ids, int64_t M, int64_t E, int num_tiles,
+                    int32_t* counts, int32_t* offsets, int32_t* pad_offsets, int32_t* perm,
+                    int32_t* slots, int32_t* tile_expert, void* stream);
+
+/* ---- MoE: grouped expert FFN + combine ----------------------------------
+ * out[t] = dtype( sum_j fp32(down_e(silu(gate_e(x_t)) * up_e(x_t))) * w[t, j] )
+ * with e = ids[t, j], then, when a shared expert is given,
+ * out[t] = dtype(out[t] + shared(x_t)).  Rounding points follow the reference
+ * (g, u, silu(g), h and each expert output rounded to the dtype; weighting and
+ * the sum over j in fp32).  Replaces the three _gemm launches, the SiLU.mul and
+ * the combine of moe_dispatch, kernels/moe_dispatch_fused.py:140-192; the
+ * shared-expert addition is the remote LLaDA2 forward's, fused in.
+ *   w_gate/w_up [E, I, H], w_down [E, H, I] (element strides per dim);
+ *   sh_gate/sh_up [Is, H], sh_down [H, Is] or all NULL;
+ *   slots/tile_expert/num_tiles from simsd_moe_align;
+ *   ids with out-of-range experts contribute nothing;
+ *   workspace: simsd_moe_workspace_bytes(T, k, H, I, Is, dtype) bytes. */
+int64_t simsd_moe_workspace_bytes(int64_t T, int k, int64_t H, int64_t I, int64_t Is, int dtype);
+
+int simsd_moe_grouped_ffn(const void* x, int64_t stride_xt, int64_t stride_xh,
+                          const void* w_gate, int64_t sge, int64_t sgi, int64_t sgh,
+                          const void* w_up, int64_t sue, int64_t sui, int64_t suh,
+                          const void* w_down, int64_t sde, int64_t sdh, int64_t sdi,
+                          const void* sh_gate, int64_t shg_i, int64_t shg_h,
+                          const void* sh_up, int64_t shu_i, int64_t shu_h,
+                          const void* sh_down, int64_t shd_h, int64_t shd_i, int64_t Is,
+                          const int32_t* slots, const int32_t* tile_expert, int num_tiles,
+                          const int64_t* topk_ids, int64_t stride_idt, int64_t stride_idk,
+                          const float* topk_w, int64_t stride_wt, int64_t stride_wk,
+                          void* out, int64_t stride_ot, int64_t stride_oh,
+                          int64_t T, int k, int64_t E, int64_t H, int64_t I, int dtype,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIMSD_KERNELS_H_ */

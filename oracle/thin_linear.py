@@ -1,0 +1,60 @@
+"""Oracle of the skinny linear (test infrastructure only).
+
+The reference's correctness target is ``torch.nn.functional.linear``
+(``ref_thin_linear``, kernels/workspace/thin_linear/CONTRACT.md:31-38): for
+bf16/fp16 inputs an fp32-accumulated product rounded once to the input dtype,
+plus bias (``y += bias`` after the GEMM, kernels/thin_linear_fused.py:343-344).
+
+``linear_exact``      y = dtype( sum_k x[m,k] w[n,k] ) with the sum in fp64
+                      (exact for fixture-sized integer data, within fp64
+                      rounding otherwise) -- the closed form.
+``linear_cpu_torch``  torch's CPU ``F.linear`` in the input dtype -- the
+                      reference's own oracle run on the host; also the timed
+                      CPU path of the benchmark.
+``tolerance``         the reference's bounds (thin_linear_fused_test.py:28-32).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .numerics import ROUNDERS
+
+
+def linear_exact(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None,
+                 dtype: str = "bf16") -> np.ndarray:
+    """x [M, K], w [N, K] (values already representable in `dtype`) -> [M, N].
+
+    Follows kernels/thin_linear_fused.py:265-345: flatten handled by the
+    caller, product then bias, result in the input dtype.
+    """
+    x64 = np.asarray(x, dtype=np.float64)
+    w64 = np.asarray(w, dtype=np.float64)
+    y = ROUNDERS[dtype](x64 @ w64.T)
+    if bias is not None:
+        y = ROUNDERS[dtype](y + np.asarray(bias, dtype=np.float64)[None, :])
+    return y
+
+
+def linear_cpu_torch(x, w, bias=None):
+    """torch CPU ``F.linear`` (the reference oracle ``ref_thin_linear``)."""
+    import torch
+    import torch.nn.functional as F
+
+    with torch.inference_mode():
+        return F.linear(x, w, bias)
+
+
+def tolerance(ref_absmax: float, dtype: str) -> float:
+    """Pointwise bound vs the reference: bf16/fp16 2^-7*max|ref| + 1e-3,
+    fp32 1e-5*max(1, max|ref|) (kernels/thin_linear_fused_test.py:28-32)."""
+    if dtype == "fp32":
+        return 1e-5 * max(1.0, ref_absmax)
+    return 2 ** -7 * ref_absmax + 1e-3
+
+
+def max_abs_rel(got: np.ndarray, ref: np.ndarray) -> float:
+    """max|got - ref| / max|ref| (the BASELINE bar is <= 1e-2)."""
+    ref = np.asarray(ref, dtype=np.float64)
+    den = float(np.abs(ref).max()) if ref.size else 0.0
+    err = float(np.abs(np.asarray(got, dtype=np.float64) - ref).max()) if ref.size else 0.0
+    return err / den if den > 0 else err

@@ -1,0 +1,68 @@
+"""Build libsimsd_kernels.so (HIP, gfx950) in-tree, next to the Python package.
+
+    python simsd-release_amd/build_lib.py            # build
+    python simsd-release_amd/build_lib.py --verbose  # echo the hipcc line
+
+The library is compiled ahead of time, so nothing JIT-compiles at import or
+inside a captured graph.  All device code is built with packed-fp32 ops
+disabled (the compiler would otherwise form v_pk_*_f32 from plain float code).
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(REPO, "include")
+OUT = os.path.join(HERE, "kernels", "libsimsd_kernels.so")
+
+SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip"]
+ARCH = os.environ.get("SIMSD_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def command(out: str = OUT, extra=()) -> list[str]:
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    return [
+        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument",
+        "-I", INCLUDE, "-I", CSRC, *extra, "-o", out, *srcs,
+    ]
+
+
+def build(verbose: bool = False, out: str = OUT) -> str:
+    cmd = command(out)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    tmp = out + ".tmp"
+    cmd[cmd.index("-o") + 1] = tmp
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # The host pass does not know the packed-fp32 feature and says so; that
+    # line is expected.  Anything else on stderr is shown.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    errs = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{errs}")
+    if errs.strip() and verbose:
+        print(errs, file=sys.stderr)
+    os.replace(tmp, out)
+    return out
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(verbose=args.verbose))

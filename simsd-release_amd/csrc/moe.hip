@@ -1,0 +1,558 @@
+// Fused MoE step for gfx950: route top-k -> align -> grouped gate_up (+SiLU.mul)
+// -> grouped down -> fp32 weighted combine (+ shared expert).
+//
+// Replaces kernels/moe_dispatch_fused.py:32-192 (reference): the Triton
+// _grouped_gemm_kernel, the ~10 torch launches of _align (93-132) and the
+// SiLU.mul / combine glue (182-192).  The routing gate itself is not in the
+// reference operator; its semantics follow
+// kernels/workspace/moe_dispatch/build_oracle.py:71-90 (top-k on the logits,
+// sigmoid or softmax scores, optional renormalisation, routed scaling).
+//
+// Every launch has a grid fixed by (T, k, E, H, I) alone: tiles that the
+// routing leaves empty exit at once, so the whole step can be captured in a
+// hipGraph and replayed with new routings.
+#include <math.h>
+
+#include "simsd_common.hpp"
+#include "simsd_kernels.h"
+
+namespace simsd {
+
+constexpr int kTile = 16;   // slots per tile (the reference's BLOCK_M)
+
+// ============================================================ route top-k ===
+// One wave per token; the E logits are spread over the 64 lanes.  Selection
+// order is value descending, ties to the lower expert index.
+template <int PL>
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int64_t T,
+                                                        int E, int64_t stride_t, int k, int scoring,
+                                                        int renorm, float scale,
+                                                        int64_t* __restrict__ ids,
+                                                        float* __restrict__ wout) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + t * stride_t;
+  float v[PL];
+  uint32_t used = 0u;   // bit i: entry i taken, or past E
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? row[e] : -INFINITY;
+    if (e >= E) used |= 1u << i;
+  }
+  float mx = 0.f, denom = 1.f;
+  if (scoring == SIMSD_SCORE_SOFTMAX) {
+    mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PL; ++i)
+      if (!((used >> i) & 1u)) mx = fmaxf(mx, v[i]);
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i)
+      if (!((used >> i) & 1u)) s += expf(v[i] - mx);
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    denom = s;
+  }
+  constexpr int kNone = 0x7fffffff;
+  float my_v = 0.f;
+  int my_i = 0;
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY;
+    int bi = kNone;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      if (!((used >> i) & 1u) && (bi == kNone || v[i] > bv)) {
+        bv = v[i];
+        bi = lane + 64 * i;
+      }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const int oi = __shfl_xor(bi, off);
+      const bool take = oi != kNone && (bi == kNone || ov > bv || (ov == bv && oi < bi));
+      if (take) { bv = ov; bi = oi; }
+    }
+    if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+    if (lane == j) { my_v = bv; my_i = bi; }
+  }
+  float s = 0.f;
+  if (lane < k) {
+    s = scoring == SIMSD_SCORE_SOFTMAX ? expf(my_v - mx) / denom : 1.f / (1.f + expf(-my_v));
+  }
+  if (renorm && k > 1) {
+    float tot = lane < k ? s : 0.f;
+    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off);
+    s = s / (tot + 1e-20f);
+  }
+  if (lane < k) {
+    ids[t * k + lane] = (int64_t)my_i;
+    wout[t * k + lane] = s * scale;
+  }
+}
+
+// ================================================================== align ===
+// One workgroup.  counts by LDS histogram; exclusive scans of counts and of
+// counts padded to 16; a stable counting sort walked by one wave in slot
+// order (ballot-matched equal keys, rank = popcount of lower lanes); then the
+// padded slot table and per-tile expert ids of kernels/moe_dispatch_fused.py:93-132.
+constexpr int kAlignThreads = 1024;
+
+SIMSD_DEV void block_exclusive_scan2(int a, int b, int& ea, int& eb, int& ta, int& tb,
+                                     int* s_wa /* [32] */, int* s_wb /* [32] */) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  int ia = a, ib = b;
+  for (int off = 1; off < 64; off <<= 1) {
+    const int ua = __shfl_up(ia, off), ub = __shfl_up(ib, off);
+    if (lane >= off) { ia += ua; ib += ub; }
+  }
+  if (lane == 63) { s_wa[wv] = ia; s_wb[wv] = ib; }
+  __syncthreads();
+  if (wv == 0) {
+    int xa = lane < nw ? s_wa[lane] : 0, xb = lane < nw ? s_wb[lane] : 0;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int ua = __shfl_up(xa, off), ub = __shfl_up(xb, off);
+      if (lane >= off) { xa += ua; xb += ub; }
+    }
+    if (lane < nw) { s_wa[lane] = xa; s_wb[lane] = xb; }
+  }
+  __syncthreads();
+  const int base_a = wv > 0 ? s_wa[wv - 1] : 0, base_b = wv > 0 ? s_wb[wv - 1] : 0;
+  ea = base_a + ia - a;
+  eb = base_b + ib - b;
+  ta = s_wa[nw - 1];
+  tb = s_wb[nw - 1];
+}
+
+// first e in [0, n) with arr[e] > val, or n
+SIMSD_DEV int upper_bound_lds(const int* arr, int n, int val) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (arr[mid] > val) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int64_t* __restrict__ ids, int M, int E, int num_tiles, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
+  __shared__ int s_pos[SIMSD_MOE_MAX_EXPERTS + 1];   // histogram, then running position
+  __shared__ int s_off[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of counts
+  __shared__ int s_pad[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of padded counts
+  __shared__ int s_perm[SIMSD_MOE_MAX_SLOTS];
+  __shared__ int s_wa[32], s_wb[32];
+  const int tid = threadIdx.x;
+  for (int e = tid; e <= E; e += kAlignThreads) s_pos[e] = 0;
+  __syncthreads();
+  // 1. histogram; ids outside [0, E) go to bucket E (kept out of every group)
+  for (int i = tid; i < M; i += kAlignThreads) {
+    const int64_t e = ids[i];
+    atomicAdd(&s_pos[(e >= 0 && e < E) ? (int)e : E], 1);
+  }
+  __syncthreads();
+  // 2. scans (E <= 1024: one expert per thread)
+  const int c = tid < E ? s_pos[tid] : 0;
+  const int pc = (c + kTile - 1) / kTile * kTile;
+  int ec, epc, tc, tpc;
+  block_exclusive_scan2(c, pc, ec, epc, tc, tpc, s_wa, s_wb);
+  if (tid < E) {
+    s_off[tid] = ec;
+    s_pad[tid] = epc;
+    counts[tid] = c;
+    offsets[tid] = ec;
+    pad_offsets[tid] = epc;
+  }
+  if (tid == 0) {
+    s_off[E] = tc;
+    s_pad[E] = tpc;
+    offsets[E] = tc;
+    pad_offsets[E] = tpc;
+  }
+  __syncthreads();
+  // 3. stable scatter, one wave, 64 slots at a time in slot order
+  if (tid < 64) {
+    const int lane = tid;
+    for (int e = lane; e <= E; e += 64) s_pos[e] = s_off[e];   // bucket E starts at tc
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int key_bits = 1;
+    while ((1 << key_bits) <= E + 1) ++key_bits;
+    for (int base = 0; base < M; base += 64) {
+      const int i = base + lane;
+      int key = 0;   // 0: no slot; else expert + 1 (E + 1 = out of range)
+      if (i < M) {
+        const int64_t e = ids[i];
+        key = ((e >= 0 && e < E) ? (int)e : E) + 1;
+      }
+      uint64_t same = ~0ull;
+      for (int b = 0; b < key_bits; ++b) {
+        const bool bit = (key >> b) & 1;
+        const uint64_t bb = __ballot(bit);
+        same &= bit ? bb : ~bb;
+      }
+      const int rank = __popcll(same & lt_mask);
+      const int leader = __ffsll((unsigned long long)same) - 1;
+      int p = 0;
+      if (key > 0) p = s_pos[key - 1] + rank;
+      if (key > 0 && lane == leader) s_pos[key - 1] = p + __popcll(same);
+      if (key > 0) s_perm[p] = i;
+    }
+  }
+  __syncthreads();
+  // 4. outputs
+  for (int p = tid; p < M; p += kAlignThreads) perm[p] = s_perm[p];
+  const int total_rows = num_tiles * kTile;
+  for (int q = tid; q < total_rows; q += kAlignThreads) {
+    const int e = upper_bound_lds(s_pad + 1, E, q);
+    int slot = -1;
+    if (e < E) {
+      const int r = q - s_pad[e];
+      if (r < s_off[e + 1] - s_off[e]) slot = s_perm[s_off[e] + r];
+    }
+    slots[q] = slot;
+  }
+  for (int t = tid; t < num_tiles; t += kAlignThreads)
+    tile_expert[t] = upper_bound_lds(s_pad + 1, E, t * kTile);
+}
+
+// ======================================================== grouped FFN ======
+struct MoeArgs {
+  const char* x;
+  int64_t sxt, sxh;
+  const char* wg;
+  int64_t sge, sgi, sgh;
+  const char* wu;
+  int64_t sue, sui, suh;
+  const char* wd;
+  int64_t sde, sdh, sdi;
+  // shared expert (nullable): gate/up [Is, H], down [H, Is]
+  const char* shg;
+  int64_t shg_i, shg_h;
+  const char* shu;
+  int64_t shu_i, shu_h;
+  const char* shd;
+  int64_t shd_h, shd_i;
+  const int32_t* slots;
+  const int32_t* tile_expert;
+  const int64_t* ids;
+  const float* topk_w;
+  int64_t sidt, sidk, swt, swk;
+  char* h;    // [M, I]  slot-major
+  char* hs;   // [T, Is]
+  char* y;    // [M, H]
+  char* ys;   // [T, H]
+  char* out;
+  int64_t sot, soh;
+  int64_t T, H, I, Is;
+  int k, E, num_tiles, shared_tiles;
+};
+
+// Decode which rows a tile feeds: a routed tile (expert e, gathered slots) or a
+// shared-expert tile (16 consecutive tokens).  Returns false for an empty tile.
+struct TileRows {
+  int e;          // expert, or -1 for the shared expert
+  int64_t slot;   // this lane's slot (routed) or token (shared); -1 if none
+  int64_t token;  // row of x
+};
+
+SIMSD_DEV bool decode_tile(const MoeArgs& a, int t, int r, TileRows& tr) {
+  if (t < a.num_tiles) {
+    const int e = a.tile_expert[t];
+    if (e < 0 || e >= a.E) return false;
+    const int s = a.slots[(int64_t)t * kTile + r];
+    tr.e = e;
+    tr.slot = s;
+    tr.token = s >= 0 ? s / a.k : -1;
+  } else {
+    const int64_t tok = (int64_t)(t - a.num_tiles) * kTile + r;
+    tr.e = -1;
+    tr.slot = tok < a.T ? tok : -1;
+    tr.token = tr.slot;
+  }
+  return true;
+}
+
+SIMSD_DEV float silu_f32(float v) { return v / (1.f + expf(-v)); }
+
+// gate_up: one workgroup = one tile x 16 intermediate columns; rows of W_gate
+// and W_up are the two A blocks, the tile's 16 gathered x rows the B block;
+// 4 waves split H.  Epilogue h = silu(g) * u with the reference's rounding
+// points (g, u, silu(g) and h each rounded to the storage dtype).
+template <int DT, bool FAST>
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int KS = 4, U = 4;
+  const int lane = threadIdx.x & 63, wk = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int t = blockIdx.x;
+  const int64_t i0 = (int64_t)blockIdx.y * 16;
+  TileRows tr;
+  if (!decode_tile(a, t, r, tr)) return;
+  const bool shared = tr.e < 0;
+  const int64_t II = shared ? a.Is : a.I;
+  if (i0 >= II) return;
+  const int64_t i_row = min(i0 + r, II - 1);
+  const char* arow[2];
+  int64_t a_sk[2];
+  if (shared) {
+    arow[0] = a.shg + i_row * a.shg_i * ES;
+    arow[1] = a.shu + i_row * a.shu_i * ES;
+    a_sk[0] = a.shg_h * ES;
+    a_sk[1] = a.shu_h * ES;
+  } else {
+    arow[0] = a.wg + ((int64_t)tr.e * a.sge + i_row * a.sgi) * ES;
+    arow[1] = a.wu + ((int64_t)tr.e * a.sue + i_row * a.sui) * ES;
+    a_sk[0] = a.sgh * ES;
+    a_sk[1] = a.suh * ES;
+  }
+  const char* brow[1] = {tr.token >= 0 ? a.x + tr.token * a.sxt * ES : nullptr};
+  const int steps = (int)((a.H * ES + kStepBytes - 1) / kStepBytes);
+  const int per_w = (steps + KS - 1) / KS;
+  const int w0 = wk * per_w, w1 = min(steps, w0 + per_w);
+  f32x4_t acc[2][1] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}}, {f32x4_t{0.f, 0.f, 0.f, 0.f}}};
+  if (FAST) {
+    accum_fast<DT, 2, 1, U>(arow, brow, w0, w1, g * kLaneBytes, a.H * ES, acc);
+  } else {
+    // both A blocks share one k-stride in the generic gather; use per-block calls
+    const char* a0[1] = {arow[0]};
+    const char* a1[1] = {arow[1]};
+    f32x4_t c0[1][1] = {{acc[0][0]}}, c1[1][1] = {{acc[1][0]}};
+    accum_generic<DT, 1, 1>(a0, a_sk[0], brow, a.sxh * ES, w0, w1, g, a.H, c0);
+    accum_generic<DT, 1, 1>(a1, a_sk[1], brow, a.sxh * ES, w0, w1, g, a.H, c1);
+    acc[0][0] = c0[0][0];
+    acc[1][0] = c1[0][0];
+  }
+  __shared__ float red[(KS - 1) * 2 * 4 * 64];
+  reduce_waves<KS, 2>(reinterpret_cast<f32x4_t(&)[2]>(acc), wk, lane, red);
+  if (wk != 0 || tr.slot < 0) return;
+  char* orow = shared ? a.hs + tr.slot * a.Is * ES : a.h + tr.slot * a.I * ES;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = i0 + 4 * g + j;
+    if (i < II) {
+      const float gv = round_to<DT>(acc[0][0][j]);
+      const float uv = round_to<DT>(acc[1][0][j]);
+      const float sv = round_to<DT>(silu_f32(gv));
+      store_elem<DT>(orow, i, sv * uv);
+    }
+  }
+}
+
+// down: one workgroup = one tile x 64 output features; each of the 4 waves owns
+// 16 rows of W_down over the whole I.
+template <int DT, bool FAST>
+__global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int U = 8;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int t = blockIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.y * 64 + wv * 16;
+  TileRows tr;
+  if (!decode_tile(a, t, r, tr)) return;
+  const bool shared = tr.e < 0;
+  if (n0 >= a.H) return;
+  const int64_t II = shared ? a.Is : a.I;
+  const int64_t n_row = min(n0 + r, a.H - 1);
+  const char* arow[1];
+  int64_t a_sk;
+  if (shared) {
+    arow[0] = a.shd + n_row * a.shd_h * ES;
+    a_sk = a.shd_i * ES;
+  } else {
+    arow[0] = a.wd + ((int64_t)tr.e * a.sde + n_row * a.sdh) * ES;
+    a_sk = a.sdi * ES;
+  }
+  const char* brow[1] = {nullptr};
+  if (tr.slot >= 0) brow[0] = shared ? a.hs + tr.slot * a.Is * ES : a.h + tr.slot * a.I * ES;
+  const int steps = (int)((II * ES + kStepBytes - 1) / kStepBytes);
+  f32x4_t acc[1][1] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}}};
+  if (FAST) accum_fast<DT, 1, 1, U>(arow, brow, 0, steps, g * kLaneBytes, II * ES, acc);
+  else accum_generic<DT, 1, 1>(arow, a_sk, brow, ES, 0, steps, g, II, acc);
+  if (tr.slot < 0) return;
+  char* orow = shared ? a.ys + tr.slot * a.H * ES : a.y + tr.slot * a.H * ES;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = n0 + 4 * g + j;
+    if (n < a.H) store_elem<DT>(orow, n, acc[0][0][j]);
+  }
+}
+
+// combine: out[t] = dtype( sum_j fp32(y[t*k+j]) * w[t,j] ), summed in j order,
+// then (shared expert) out = dtype(out + ys[t]).
+template <int DT>
+__global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const int64_t t = blockIdx.y;
+  const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (h >= a.H) return;
+  float acc = 0.f;
+  for (int j = 0; j < a.k; ++j) {
+    const int64_t e = a.ids[t * a.sidt + j * a.sidk];
+    if (e < 0 || e >= a.E) continue;
+    const float yv = load_elem<DT>(a.y, (t * a.k + j) * a.H + h);
+    acc = __fadd_rn(acc, __fmul_rn(yv, a.topk_w[t * a.swt + j * a.swk]));
+  }
+  float o = round_to<DT>(acc);
+  if (a.shared_tiles > 0) o = o + load_elem<DT>(a.ys, t * a.H + h);
+  store_elem<DT>(a.out, t * a.sot + h * a.soh, o);
+}
+
+// ------------------------------------------------------------------ host side
+namespace {
+
+inline int esize_of(int dtype) { return dtype == kF32 ? 4 : 2; }
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool row_ok(const void* base, int64_t row_stride, int64_t k_stride, int64_t K, int es) {
+  return base != nullptr && al16(base) && k_stride == 1 && (row_stride * es) % 16 == 0 &&
+         (K * es) % 16 == 0;
+}
+inline int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+
+struct MoeLayout {
+  int64_t h, hs, y, ys, total;
+};
+
+MoeLayout moe_layout(int64_t T, int k, int64_t H, int64_t I, int64_t Is, int es) {
+  MoeLayout L{};
+  const int64_t M = T * k;
+  L.h = 0;
+  L.hs = L.h + align256(M * I * es);
+  L.y = L.hs + align256(T * Is * es);
+  L.ys = L.y + align256(M * H * es);
+  L.total = L.ys + align256(T * H * es);
+  return L;
+}
+
+template <int DT>
+void launch_ffn(const MoeArgs& a, bool fast_gu, bool fast_dn, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  const int tiles = a.num_tiles + a.shared_tiles;
+  const int64_t imax = a.I > a.Is ? a.I : a.Is;
+  dim3 g1((unsigned)tiles, (unsigned)((imax + 15) / 16));
+  if (fast_gu) hipLaunchKernelGGL((moe_gate_up_kernel<DT, true>), g1, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((moe_gate_up_kernel<DT, false>), g1, dim3(256), 0, stream, a);
+  dim3 g2((unsigned)tiles, (unsigned)((a.H + 63) / 64));
+  if (fast_dn) hipLaunchKernelGGL((moe_down_kernel<DT, true>), g2, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((moe_down_kernel<DT, false>), g2, dim3(256), 0, stream, a);
+  dim3 g3((unsigned)((a.H + 255) / 256), (unsigned)a.T);
+  hipLaunchKernelGGL((moe_combine_kernel<DT>), g3, dim3(256), 0, stream, a);
+}
+
+}  // namespace
+}  // namespace simsd
+
+using namespace simsd;
+
+extern "C" int simsd_moe_route_topk(const float* logits, int64_t T, int64_t E, int64_t stride_t,
+                                    int k, int scoring, int renorm, float scale, int64_t* ids_out,
+                                    float* w_out, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (T < 0 || E <= 0 || E > SIMSD_MOE_MAX_EXPERTS)
+    return set_error("moe_route_topk: need 0 < E <= %d (E=%lld)", SIMSD_MOE_MAX_EXPERTS, (long long)E);
+  if (k <= 0 || k > 64 || k > E) return set_error("moe_route_topk: need 0 < k <= min(64, E) (k=%d)", k);
+  if (scoring != SIMSD_SCORE_SOFTMAX && scoring != SIMSD_SCORE_SIGMOID)
+    return set_error("moe_route_topk: unknown scoring %d", scoring);
+  if (T == 0) return 0;
+  if (logits == nullptr || ids_out == nullptr || w_out == nullptr)
+    return set_error("moe_route_topk: null pointer");
+  if (T > (int64_t)0x7fffffff * 4) return set_error("moe_route_topk: T too large");
+  dim3 grid((unsigned)((T + 3) / 4));
+  if (E <= 64) hipLaunchKernelGGL((moe_route_kernel<1>), grid, dim3(256), 0, stream, logits, T, (int)E, stride_t, k, scoring, renorm, scale, ids_out, w_out);
+  else if (E <= 256) hipLaunchKernelGGL((moe_route_kernel<4>), grid, dim3(256), 0, stream, logits, T, (int)E, stride_t, k, scoring, renorm, scale, ids_out, w_out);
+  else hipLaunchKernelGGL((moe_route_kernel<16>), grid, dim3(256), 0, stream, logits, T, (int)E, stride_t, k, scoring, renorm, scale, ids_out, w_out);
+  return check_launch("moe_route_topk");
+}
+
+extern "C" int simsd_moe_num_tiles(int64_t M, int64_t E) {
+  return (int)((M < E ? M : E) + (M + kTile - 1) / kTile);
+}
+
+extern "C" int simsd_moe_align(const int64_t* ids, int64_t M, int64_t E, int num_tiles,
+                               int32_t* counts, int32_t* offsets, int32_t* pad_offsets,
+                               int32_t* perm, int32_t* slots, int32_t* tile_expert,
+                               void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (E <= 0 || E > SIMSD_MOE_MAX_EXPERTS)
+    return set_error("moe_align: need 0 < E <= %d", SIMSD_MOE_MAX_EXPERTS);
+  if (M < 0 || M > SIMSD_MOE_MAX_SLOTS)
+    return set_error("moe_align: need 0 <= T*k <= %d (got %lld)", SIMSD_MOE_MAX_SLOTS, (long long)M);
+  if (num_tiles < 0 || (int64_t)num_tiles * kTile > ((int64_t)1 << 30))
+    return set_error("moe_align: bad num_tiles %d", num_tiles);
+  if (counts == nullptr || offsets == nullptr || pad_offsets == nullptr || slots == nullptr ||
+      tile_expert == nullptr || (M > 0 && (ids == nullptr || perm == nullptr)))
+    return set_error("moe_align: null pointer");
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, ids, (int)M, (int)E,
+                     num_tiles, counts, offsets, pad_offsets, perm, slots, tile_expert);
+  return check_launch("moe_align");
+}
+
+extern "C" int64_t simsd_moe_workspace_bytes(int64_t T, int k, int64_t H, int64_t I, int64_t Is,
+                                             int dtype) {
+  return moe_layout(T, k, H, I, Is, esize_of(dtype)).total;
+}
+
+extern "C" int simsd_moe_grouped_ffn(
+    const void* x, int64_t sxt, int64_t sxh, const void* w_gate, int64_t sge, int64_t sgi,
+    int64_t sgh, const void* w_up, int64_t sue, int64_t sui, int64_t suh, const void* w_down,
+    int64_t sde, int64_t sdh, int64_t sdi, const void* sh_gate, int64_t shg_i, int64_t shg_h,
+    const void* sh_up, int64_t shu_i, int64_t shu_h, const void* sh_down, int64_t shd_h,
+    int64_t shd_i, int64_t Is, const int32_t* slots, const int32_t* tile_expert, int num_tiles,
+    const int64_t* topk_ids, int64_t sidt, int64_t sidk, const float* topk_w, int64_t swt,
+    int64_t swk, void* out, int64_t sot, int64_t soh, int64_t T, int k, int64_t E, int64_t H,
+    int64_t I, int dtype, void* workspace, int64_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
+    return set_error("moe_grouped_ffn: unsupported dtype code %d", dtype);
+  if (T < 0 || k <= 0 || E <= 0 || H <= 0 || I <= 0)
+    return set_error("moe_grouped_ffn: bad sizes T=%lld k=%d E=%lld H=%lld I=%lld", (long long)T, k,
+                     (long long)E, (long long)H, (long long)I);
+  if (T == 0) return 0;
+  const bool has_shared = sh_gate != nullptr;
+  if (has_shared && (sh_up == nullptr || sh_down == nullptr || Is <= 0))
+    return set_error("moe_grouped_ffn: shared expert needs gate, up, down and Is > 0");
+  if (!has_shared) Is = 0;
+  const int es = esize_of(dtype);
+  const MoeLayout L = moe_layout(T, k, H, I, Is, es);
+  if (workspace == nullptr || workspace_bytes < L.total || !al16(workspace))
+    return set_error("moe_grouped_ffn: needs a 16-byte aligned %lld-byte workspace (got %lld)",
+                     (long long)L.total, (long long)workspace_bytes);
+  if (x == nullptr || w_gate == nullptr || w_up == nullptr || w_down == nullptr || slots == nullptr ||
+      tile_expert == nullptr || topk_ids == nullptr || topk_w == nullptr || out == nullptr)
+    return set_error("moe_grouped_ffn: null pointer");
+  const int64_t shared_tiles = has_shared ? (T + kTile - 1) / kTile : 0;
+  if (num_tiles + shared_tiles > 0x7fffffff) return set_error("moe_grouped_ffn: too many tiles");
+  MoeArgs a{};
+  a.x = static_cast<const char*>(x); a.sxt = sxt; a.sxh = sxh;
+  a.wg = static_cast<const char*>(w_gate); a.sge = sge; a.sgi = sgi; a.sgh = sgh;
+  a.wu = static_cast<const char*>(w_up); a.sue = sue; a.sui = sui; a.suh = suh;
+  a.wd = static_cast<const char*>(w_down); a.sde = sde; a.sdh = sdh; a.sdi = sdi;
+  a.shg = static_cast<const char*>(sh_gate); a.shg_i = shg_i; a.shg_h = shg_h;
+  a.shu = static_cast<const char*>(sh_up); a.shu_i = shu_i; a.shu_h = shu_h;
+  a.shd = static_cast<const char*>(sh_down); a.shd_h = shd_h; a.shd_i = shd_i;
+  a.slots = slots; a.tile_expert = tile_expert;
+  a.ids = topk_ids; a.sidt = sidt; a.sidk = sidk;
+  a.topk_w = topk_w; a.swt = swt; a.swk = swk;
+  char* ws = static_cast<char*>(workspace);
+  a.h = ws + L.h; a.hs = ws + L.hs; a.y = ws + L.y; a.ys = ws + L.ys;
+  a.out = static_cast<char*>(out); a.sot = sot; a.soh = soh;
+  a.T = T; a.H = H; a.I = I; a.Is = Is;
+  a.k = k; a.E = (int)E; a.num_tiles = num_tiles; a.shared_tiles = (int)shared_tiles;
+  // 16-byte paths: every operand row K-contiguous, 16-byte aligned, K*es % 16 == 0.
+  bool fast_gu = row_ok(x, sxt, sxh, H, es) && row_ok(w_gate, sgi, sgh, H, es) &&
+                 row_ok(w_up, sui, suh, H, es) && (sge * es) % 16 == 0 && (sue * es) % 16 == 0;
+  bool fast_dn = row_ok(w_down, sdh, sdi, I, es) && (sde * es) % 16 == 0;
+  if (has_shared) {
+    fast_gu = fast_gu && row_ok(sh_gate, shg_i, shg_h, H, es) && row_ok(sh_up, shu_i, shu_h, H, es);
+    fast_dn = fast_dn && row_ok(sh_down, shd_h, shd_i, Is, es);
+  }
+  switch (dtype) {
+    case kBF16: launch_ffn<kBF16>(a, fast_gu, fast_dn, stream); break;
+    case kF16: launch_ffn<kF16>(a, fast_gu, fast_dn, stream); break;
+    default: launch_ffn<kF32>(a, fast_gu, fast_dn, stream); break;
+  }
+  return check_launch("moe_grouped_ffn");
+}

@@ -1,0 +1,166 @@
+"""Opt-in switch routing a model's ``nn.Linear`` / MoE calls through the MI355X kernels.
+
+Same API and behaviour as kernels/fused_toggle.py (reference, lines 30-202):
+``DEFAULT_TARGETS``, ``ALL_TARGETS``, ``apply_to_model``, ``is_applied``, the
+``fused_linear`` context manager, ``warmup``, ``apply_moe_to_model`` and
+``is_moe_applied``.  The model code is third-party (loaded through
+``trust_remote_code``), so the switch patches modules in place rather than
+editing call sites: target linears are swapped for ``ThinLinear`` (which
+aliases the original parameters), and LLaDA2's MoE block gets a class-level
+``moe_infer`` that calls ``moe_dispatch`` on stacked expert weights.
+
+Default is off.  Call it before graph capture: a captured graph keeps
+whichever forward was installed when it was recorded.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from .thin_linear_fused import ThinLinear, reset_workspace
+
+# Leaf names of the projections to swap; lm_head is opt-in (ALL_TARGETS).
+DEFAULT_TARGETS = (
+    "q_proj", "k_proj", "v_proj", "o_proj",
+    "gate_proj", "up_proj", "down_proj",
+)
+ALL_TARGETS = DEFAULT_TARGETS + ("lm_head",)
+
+# id(model) -> {qualified name: original module}
+_ORIGINALS: dict[int, dict[str, nn.Module]] = {}
+
+
+def _targets_in(model: nn.Module, targets):
+    for qualified, mod in model.named_modules():
+        if isinstance(mod, nn.Linear) and qualified.rsplit(".", 1)[-1] in targets:
+            yield qualified, mod
+
+
+def _replace(model: nn.Module, qualified: str, new: nn.Module) -> None:
+    owner_path, _, leaf = qualified.rpartition(".")
+    owner = model.get_submodule(owner_path) if owner_path else model
+    setattr(owner, leaf, new)
+
+
+def apply_to_model(model: nn.Module, enable: bool = True,
+                   targets=DEFAULT_TARGETS,
+                   config: tuple[int, int, int, int] | None = None) -> int:
+    """Swap the target ``nn.Linear`` modules for ``ThinLinear`` (or restore them).
+
+    Idempotent both ways; returns how many modules were swapped or restored.
+    """
+    key = id(model)
+    if not enable:
+        saved = _ORIGINALS.pop(key, None)
+        if not saved:
+            return 0
+        for qualified, orig in saved.items():
+            _replace(model, qualified, orig)
+        reset_workspace()
+        return len(saved)
+    if key in _ORIGINALS:
+        return 0
+    saved = {}
+    for qualified, mod in list(_targets_in(model, targets)):
+        saved[qualified] = mod
+        _replace(model, qualified, ThinLinear(mod, config=config))
+    if saved:
+        _ORIGINALS[key] = saved
+    return len(saved)
+
+
+def is_applied(model: nn.Module) -> bool:
+    return id(model) in _ORIGINALS
+
+
+class fused_linear:
+    """Context-manager form::
+
+        with fused_toggle.fused_linear(model):
+            ...
+    """
+
+    def __init__(self, model: nn.Module, enable: bool = True, **kw):
+        self.model, self.enable, self.kw = model, enable, kw
+        self.n = 0
+
+    def __enter__(self):
+        self.n = apply_to_model(self.model, self.enable, **self.kw)
+        return self
+
+    def __exit__(self, *exc):
+        if self.enable:
+            apply_to_model(self.model, False)
+        return False
+
+
+def warmup(model: nn.Module, block_length: int = 4, extra_M=()) -> None:
+    """Run every swapped module once at each M the pipeline uses.
+
+    The kernels are compiled ahead of time, so there is no JIT to trigger;
+    what this still does is allocate the per-device split-K workspace and load
+    the library before any graph capture, at M in {1, block_length,
+    2*block_length, 96, 97, *extra_M} (the reference's sweep,
+    kernels/fused_toggle.py:107-133).
+    """
+    Ms = {1, block_length, 2 * block_length, 96, 97, *extra_M}
+    mods = [m for _, m in model.named_modules() if isinstance(m, ThinLinear)]
+    with torch.inference_mode():
+        for mod in mods:
+            for M in sorted(Ms):
+                mod(torch.zeros(M, mod.in_features, device=mod.weight.device,
+                                dtype=mod.weight.dtype))
+    if mods and mods[0].weight.is_cuda:
+        torch.cuda.synchronize()
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# LLaDA2 MoE expert dispatch (moe_dispatch_fused.py)
+# ─────────────────────────────────────────────────────────────────────────────
+_MOE_ATTR = "_simsd_fused_moe"
+_MOE_CLASS = "LLaDA2MoeSparseMoeBlock"
+
+
+def apply_moe_to_model(model: nn.Module, enable: bool = True) -> int:
+    """Switch LLaDA2 MoE blocks to the grouped dispatch.  Idempotent.
+
+    Returns the number of blocks switched.  Stacking releases the per-expert
+    weights, so ``enable=False`` cannot restore them and raises.
+    """
+    from .moe_dispatch_fused import moe_dispatch, stack_expert_weights
+
+    n = 0
+    for mod in model.modules():
+        if mod.__class__.__name__ != _MOE_CLASS:
+            continue
+        if enable:
+            if getattr(mod, _MOE_ATTR, None) is not None:
+                continue
+            setattr(mod, _MOE_ATTR, stack_expert_weights(mod.experts))
+            n += 1
+        elif getattr(mod, _MOE_ATTR, None) is not None:
+            raise NotImplementedError(
+                "apply_moe_to_model(enable=False) is not supported: stacking "
+                "releases the per-expert weights so the layer's footprint stays "
+                "flat. Reload the checkpoint to get the stock path back.")
+    if n == 0:
+        return 0
+
+    cls = next(m.__class__ for m in model.modules() if m.__class__.__name__ == _MOE_CLASS)
+    if not getattr(cls, "_simsd_moe_patched", False):
+        stock = cls.moe_infer
+
+        def moe_infer(self, x, topk_ids, topk_weight):
+            packed = getattr(self, _MOE_ATTR, None)
+            if packed is None:
+                return stock(self, x, topk_ids, topk_weight)
+            return moe_dispatch(x, topk_ids, topk_weight, *packed)
+
+        cls.moe_infer = moe_infer
+        cls._simsd_moe_stock = stock
+        cls._simsd_moe_patched = True
+    return n
+
+
+def is_moe_applied(model: nn.Module) -> bool:
+    return any(getattr(m, _MOE_ATTR, None) is not None for m in model.modules())

@@ -1,0 +1,278 @@
+"""Skinny-M ``F.linear`` for MI355X -- drop-in for kernels/thin_linear_fused.py.
+
+Same public surface as the reference module (kernels/thin_linear_fused.py:57-419):
+``thin_linear``, ``ThinLinear``, ``should_fuse``, ``pick_config``, ``TUNED``,
+``_tuned_for``, ``_heuristic_config``, ``reset_workspace``, ``make_bench_fn`` and
+the ``TARGET_CTAS`` / ``MAX_SPLIT_K`` / ``MIN_K_PER_SPLIT`` knobs, with the same
+argument meaning and the same exceptions.  The arithmetic runs in a
+hand-written gfx950 HIP kernel (``libsimsd_kernels.so``, C ABI in
+``include/simsd_kernels.h``) instead of Triton.
+
+How the MI355X kernel works (``csrc/thin_gemm.hip``)
+----------------------------------------------------
+At M <= 32 the op is a stream over the weight: arithmetic intensity is at most
+~32 flop/byte against a ~312 flop/byte ridge, so HBM bandwidth is the bound.
+Each wave streams 16 weight rows with 128-bit loads straight into the A
+operand of ``v_mfma_f32_16x16x32_bf16`` while the M activation rows are the B
+operand (masked lanes below 16 rows, a second column block up to 32 rows).
+MFMA does the fp32-accumulate arithmetic for free relative to the byte rate,
+which leaves the VALU idle and keeps the loads in flight.  A workgroup splits K
+over its waves and sums their fp32 partials in LDS in fixed order; a narrow N
+additionally splits K over workgroups, whose partials are summed in index order
+by the last workgroup to finish (one launch, no atomics on data).
+
+Config tuples keep the reference's shape ``(BLOCK_M, BLOCK_N, BLOCK_K,
+SPLIT_K[, num_warps, num_stages])`` but describe the MI355X kernel:
+BLOCK_M is the activation-row envelope (16, or 32 with two column blocks),
+BLOCK_N the weight rows per workgroup (16 or 32), BLOCK_K the K elements one
+wave streams per pipeline stage, SPLIT_K the workgroups along K, num_warps the
+waves per workgroup (2, 4 or 8) and num_stages the register double-buffer
+depth (always 2).
+
+Contract (reference CONTRACT, kernels/workspace/thin_linear/CONTRACT.md:26-91):
+forward only; fp32 accumulation for bf16/fp16/fp32 inputs; deterministic
+(fixed-order reductions, bit-identical across calls and graph replays); no
+host sync, no value-dependent host branching and no allocation outside torch's
+caching allocator, so it captures into a HIP graph.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+# Tuning knobs (kernels/thin_linear_fused.py:59-61).  MI355X has 256 CUs.
+TARGET_CTAS = 2 * 256          # aim for two workgroups on every CU
+MAX_SPLIT_K = 16
+MIN_K_PER_SPLIT = 512          # bf16 elements; a split is at least 4 k-steps per wave
+
+_STEP_BYTES = 64               # bytes of a weight row one MFMA k-step consumes
+_DEFAULT_WAVES = 4
+_STAGES = 2
+
+
+def _next_pow2(n: int) -> int:
+    n = max(int(n), 1)
+    return 1 << (n - 1).bit_length()
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# Workspace (kernels/thin_linear_fused.py:173-190)
+# ─────────────────────────────────────────────────────────────────────────────
+# device -> byte buffer holding the split-K tile counters and fp32 partials.
+# Zero-filled when (re)allocated; every kernel call leaves its counters at zero
+# again, so the buffer is reused without clearing.  Calls that share a device
+# are ordered on one stream (a captured graph replays them serially); two
+# streams running split-K calls on one device at once would race on it.
+_PARTIALS: dict[torch.device, torch.Tensor] = {}
+
+
+def _partials(dev: torch.device, nbytes: int) -> torch.Tensor:
+    buf = _PARTIALS.get(dev)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 4096), device=dev, dtype=torch.uint8)
+        _PARTIALS[dev] = buf
+    return buf
+
+
+def reset_workspace() -> None:
+    """Drop the staging buffers (call before re-capturing graphs in a new pool)."""
+    _PARTIALS.clear()
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# Configs (kernels/thin_linear_fused.py:193-262)
+# ─────────────────────────────────────────────────────────────────────────────
+# (K, N) -> (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages).
+# BLOCK_M is the largest M the entry covers.  Values are the automatic plan's
+# choice until an MI355X sweep (M=4 draft, M=16/32 target, bf16, HIP graph over
+# a weight pool larger than the 256 MB MALL) replaces them.
+TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
+    # SDAR-1.7B draft projections (hidden 2048, 16 q / 8 kv heads, inter 6144)
+    (2048, 2048): (16, 16, 256, 4, 4, 2),     # q_proj, o_proj
+    (2048, 1024): (16, 16, 256, 4, 4, 2),     # k_proj, v_proj
+    (2048, 6144): (16, 16, 256, 2, 4, 2),     # gate_proj, up_proj
+    (6144, 2048): (16, 16, 256, 4, 4, 2),     # down_proj
+    (2048, 151936): (16, 16, 256, 1, 4, 2),   # lm_head
+    (2048, 4096): (16, 16, 256, 2, 4, 2),     # merged qkv
+    (2048, 12288): (16, 16, 256, 1, 4, 2),    # merged gate+up
+    # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
+    (4096, 12288): (32, 16, 128, 1, 4, 2),    # gate_proj / up_proj
+    (4096, 4096): (32, 16, 128, 2, 4, 2),     # q_proj, o_proj
+    (4096, 1024): (32, 16, 128, 8, 4, 2),     # k_proj, v_proj
+    (4096, 6144): (32, 16, 128, 2, 4, 2),     # merged qkv
+    (4096, 24576): (32, 16, 128, 1, 4, 2),    # merged gate+up
+    (12288, 4096): (32, 16, 128, 2, 4, 2),    # down_proj
+    (4096, 151936): (32, 16, 128, 1, 4, 2),   # lm_head
+}
+
+
+def pick_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, int, int, int]:
+    """(BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K) -- tuned where known, else heuristic."""
+    full = _tuned_for(M, N, K)
+    if full is not None:
+        return full[0], full[1], full[2], full[3]
+    return _heuristic_config(M, N, K, itemsize)
+
+
+def _tuned_for(M: int, N: int, K: int):
+    """The tuned 6-tuple, or None when this (M, K, N) is outside its envelope.
+
+    An entry covers every M whose rounded-up block ``max(16, next_pow2(M))``
+    fits its BLOCK_M: draft entries (BLOCK_M=16) stop at M=16, exactly the
+    reference's rule (kernels/thin_linear_fused.py:232-242); target entries
+    (BLOCK_M=32) extend to the 32-row multi-block verify.
+    """
+    c = TUNED.get((K, N))
+    if c is None:
+        return None
+    return c if max(16, _next_pow2(max(M, 1))) <= c[0] else None
+
+
+def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, int, int, int]:
+    """Same rule as the library's automatic plan (``simsd_thin_linear_plan``)."""
+    BLOCK_M = 16 if M <= 16 else 32
+    BLOCK_N = 16
+    BLOCK_K = (256 if BLOCK_M == 16 else 128) * 2 // itemsize
+    tiles = _cdiv(N, BLOCK_N) * _cdiv(M, BLOCK_M)
+    steps = _cdiv(K * itemsize, _STEP_BYTES)
+    split = _cdiv(TARGET_CTAS, tiles)
+    split = max(1, min(split, MAX_SPLIT_K, steps // (MIN_K_PER_SPLIT * 2 // _STEP_BYTES)))
+    return BLOCK_M, BLOCK_N, BLOCK_K, split
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# The op (kernels/thin_linear_fused.py:265-345)
+# ─────────────────────────────────────────────────────────────────────────────
+def thin_linear(x: torch.Tensor, w: torch.Tensor,
+                bias: torch.Tensor | None = None,
+                config: tuple[int, ...] | None = None,
+                num_warps: int | None = None,
+                num_stages: int | None = None) -> torch.Tensor:
+    """`F.linear(x, w, bias)` for tiny M on the MI355X kernel.
+
+    x: [..., K]  (leading dims are flattened, as `nn.Linear` does)
+    w: [N, K]    (`nn.Linear.weight` layout)
+    -> [..., N]
+    """
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad):
+        raise RuntimeError(
+            "thin_linear is a forward-only inference kernel (contract mode="
+            "inference); it has no backward. Call it under torch.no_grad() / "
+            "torch.inference_mode(), or use F.linear for training.")
+    if x.dtype != w.dtype:
+        raise TypeError(f"dtype mismatch: x={x.dtype} w={w.dtype}")
+    if w.ndim != 2:
+        raise ValueError(f"w must be 2-D [N, K], got {tuple(w.shape)}")
+    code = _native.DTYPE_CODES.get(x.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {x.dtype} (bf16, fp16 or fp32)")
+
+    out_shape = (*x.shape[:-1], w.shape[0])
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"K mismatch: x[..., {K}] vs w[{N}, {w.shape[1]}]")
+    dev = _native.require_device(x2, w)
+
+    if M == 0 or N == 0 or K == 0:
+        y = torch.zeros((M, N), device=dev, dtype=x.dtype)
+        if bias is not None:
+            y += bias
+        return y.view(out_shape)
+
+    y = torch.empty((M, N), device=dev, dtype=x.dtype)
+
+    if config is not None:
+        block_n, split_k = int(config[1]), int(config[3])
+        waves = num_warps or _DEFAULT_WAVES
+    else:
+        tuned = _tuned_for(M, N, K)
+        if tuned is not None:
+            _, block_n, _, split_k, waves, _ = tuned
+        else:
+            _, block_n, _, split_k = _heuristic_config(M, N, K, x.element_size())
+            waves = _DEFAULT_WAVES
+        waves = num_warps or waves
+    if split_k < 1:
+        raise ValueError(f"SPLIT_K must be >= 1, got {split_k}")
+
+    fuse_bias = (bias is not None and bias.dtype == x.dtype and bias.ndim == 1
+                 and bias.shape[0] == N and bias.device == dev)
+    lib = _native.lib()
+    ws, ws_bytes = None, 0
+    if split_k > 1:
+        need = lib.simsd_thin_linear_workspace_bytes(M, N, K, code, block_n, split_k, waves)
+        if need < 0:
+            _native.check(-1, "thin_linear")
+        ws = _partials(dev, need)
+        ws_bytes = ws.numel()
+    with _native.device_guard(dev):
+        status = lib.simsd_thin_linear(
+            x2.data_ptr(), x2.stride(0), x2.stride(1),
+            w.data_ptr(), w.stride(0), w.stride(1),
+            bias.data_ptr() if fuse_bias else None, bias.stride(0) if fuse_bias else 0,
+            y.data_ptr(), y.stride(0), y.stride(1),
+            M, N, K, code, block_n, split_k, waves,
+            ws.data_ptr() if ws is not None else None, ws_bytes,
+            _native.stream_of(dev))
+    _native.check(status, "thin_linear")
+
+    if bias is not None and not fuse_bias:
+        y += bias
+    return y.view(out_shape)
+
+
+def should_fuse(M: int, N: int, K: int) -> bool:
+    """Is the fused kernel the production choice for this shape?
+
+    Only inside a tuned entry's envelope (M <= 16 for draft shapes, M <= 32
+    for target shapes), as in kernels/thin_linear_fused.py:348-377.  Outside it
+    ``ThinLinear`` hands the call to ``F.linear`` (hipBLASLt), which is
+    bit-exactly the stock path -- prefill must reproduce the stock KV cache.
+    """
+    return _tuned_for(M, N, K) is not None
+
+
+class ThinLinear(torch.nn.Module):
+    """`nn.Linear` drop-in that routes the forward through `thin_linear`.
+
+    Holds a *reference* to the original module's parameters (no copy), so
+    swapping it in costs no memory and `state_dict()` round-trips unchanged.
+    Falls back to `F.linear` outside the tuned envelope (see `should_fuse`).
+    """
+
+    def __init__(self, linear: torch.nn.Linear,
+                 config: tuple[int, int, int, int] | None = None,
+                 always_fuse: bool = False):
+        super().__init__()
+        self.in_features = linear.in_features
+        self.out_features = linear.out_features
+        self.weight = linear.weight
+        self.bias = linear.bias
+        self.config = config
+        self.always_fuse = always_fuse
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        M = x.numel() // x.shape[-1]
+        if (self.config is not None or self.always_fuse
+                or should_fuse(M, self.out_features, self.in_features)):
+            return thin_linear(x, self.weight, self.bias, config=self.config)
+        return torch.nn.functional.linear(x, self.weight, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, fused=mi355x-skinny-mfma "
+                f"(tuned envelope only unless always_fuse)")
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# Bench hook (kernels/thin_linear_fused.py:418-419)
+# ─────────────────────────────────────────────────────────────────────────────
+def make_bench_fn(x, pool, sh):
+    return lambda i: thin_linear(x, pool[i])

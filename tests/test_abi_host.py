@@ -1,0 +1,286 @@
+"""C-ABI and host-side logic (CPU only: no kernel is launched here).
+
+* libsimsd_kernels.so loads and exports every function include/simsd_kernels.h
+  declares, with the ABI version the header states;
+* the host-only entry points (sizes, plans) agree with the Python mirror of
+  the reference's config rules;
+* the dispatch envelope and error behaviour of the reference's module
+  (kernels/thin_linear_fused_test.py:112-127, 154-195) hold for the drop-in;
+* the toggle swaps/restores modules (kernels/thin_linear_fused_test.py:253-298).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+import torch.nn as nn
+
+from conftest import REPO
+
+HEADER = os.path.join(REPO, "include", "simsd_kernels.h")
+
+
+def header_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(simsd_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from kernels import _native
+    lib = _native.lib()
+    names = header_functions()
+    assert len(names) >= 10, names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+        assert name in _native.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_native.SIGNATURES) == set(names)
+
+
+def test_abi_version_matches_header():
+    from kernels import _native
+    m = re.search(r"#define SIMSD_ABI_VERSION (\d+)", open(HEADER).read())
+    assert int(m.group(1)) == _native.lib().simsd_abi_version() == _native.ABI_VERSION
+
+
+def test_header_constants_match_binding():
+    from kernels import _native
+    text = open(HEADER).read()
+    consts = dict(re.findall(r"#define (SIMSD_\w+) (\d+)", text))
+    assert int(consts["SIMSD_DTYPE_BF16"]) == _native.DTYPE_CODES[torch.bfloat16]
+    assert int(consts["SIMSD_DTYPE_F16"]) == _native.DTYPE_CODES[torch.float16]
+    assert int(consts["SIMSD_DTYPE_F32"]) == _native.DTYPE_CODES[torch.float32]
+    assert int(consts["SIMSD_SCORE_SOFTMAX"]) == _native.SCORE_SOFTMAX
+    assert int(consts["SIMSD_SCORE_SIGMOID"]) == _native.SCORE_SIGMOID
+    assert int(consts["SIMSD_MOE_MAX_EXPERTS"]) == _native.MOE_MAX_EXPERTS
+    assert int(consts["SIMSD_MOE_MAX_SLOTS"]) == _native.MOE_MAX_SLOTS
+
+
+def test_header_links_from_plain_c(tmp_path):
+    """A C program includes the header, links the library and calls the
+    host-only entry points (no GPU needed)."""
+    from kernels import _native
+    src = tmp_path / "t.c"
+    src.write_text(
+        '#include <stdio.h>\n#include "simsd_kernels.h"\n'
+        'int main(void){\n'
+        '  int out[4];\n'
+        '  if (simsd_abi_version() != SIMSD_ABI_VERSION) return 1;\n'
+        '  if (simsd_moe_num_tiles(512, 256) != 288) return 2;\n'
+        '  if (simsd_thin_linear_plan(4, 12288, 2048, SIMSD_DTYPE_BF16, 0, 0, 0, out) != 0) return 3;\n'
+        '  printf("%d %d %d %d\\n", out[0], out[1], out[2], out[3]);\n'
+        '  return 0;\n}\n')
+    libdir = os.path.dirname(_native.LIB_PATH)
+    exe = tmp_path / "t"
+    rc = os.system(f"gcc -std=c99 -Wall -Werror -I{REPO}/include {src} -o {exe} "
+                   f"-L{libdir} -lsimsd_kernels -Wl,-rpath,{libdir}")
+    assert rc == 0
+    assert os.system(f"{exe} > {tmp_path}/out.txt") == 0
+    assert open(f"{tmp_path}/out.txt").read().split() == ["16", "16", "4", "1"]
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 2048, 2048), (4, 1024, 2048), (4, 12288, 2048),
+                                   (4, 2048, 6144), (16, 4096, 4096), (32, 24576, 4096),
+                                   (32, 4096, 12288), (4, 151936, 2048), (96, 2048, 2048),
+                                   (1, 1, 1), (7, 33, 1000)])
+def test_c_plan_equals_python_heuristic(M, N, K):
+    from kernels import _native
+    from kernels.thin_linear_fused import _heuristic_config
+    out = (ctypes.c_int * 4)()
+    assert _native.lib().simsd_thin_linear_plan(M, N, K, 0, 0, 0, 0, out) == 0
+    rows, cols, waves, split = list(out)
+    BM, BN, BK, SK = _heuristic_config(M, N, K, 2)
+    assert (rows, cols, split) == (BN, BM, SK)
+    assert waves == 4
+
+
+def test_workspace_sizes():
+    from kernels import _native
+    lib = _native.lib()
+    assert lib.simsd_thin_linear_workspace_bytes(4, 2048, 2048, 0, 16, 1, 4) == 0
+    n = lib.simsd_thin_linear_workspace_bytes(4, 2048, 6144, 0, 16, 8, 4)
+    # counters for 128 tiles (rounded to 256 B) + 8 fp32 partial tiles of 4 x 2048
+    assert n == 512 + 8 * 4 * 2048 * 4
+    assert lib.simsd_moe_num_tiles(512, 256) == 256 + 32
+    assert lib.simsd_moe_num_tiles(32, 256) == 32 + 2
+    w = lib.simsd_moe_workspace_bytes(64, 8, 2048, 512, 512, 0)
+    assert w >= 2 * (512 * 512 + 64 * 512 + 512 * 2048 + 64 * 2048)
+
+
+def test_error_string_round_trip():
+    from kernels import _native
+    lib = _native.lib()
+    st = lib.simsd_thin_linear(None, 0, 0, None, 0, 0, None, 0, None, 0, 0, 4, 4, 4, 9,
+                               0, 0, 0, None, 0, None)
+    assert st != 0
+    assert b"dtype" in lib.simsd_last_error_string()
+    with pytest.raises(RuntimeError, match="dtype"):
+        _native.check(st, "thin_linear")
+
+
+# ─────────────────────────────── reference envelope / errors (host only) ───
+def test_tuned_table_envelope():
+    from kernels.thin_linear_fused import TUNED, _tuned_for, should_fuse, pick_config
+    assert (2048, 2048) in TUNED
+    assert _tuned_for(4, 2048, 2048) is not None
+    assert _tuned_for(16, 2048, 2048) is not None
+    assert _tuned_for(96, 2048, 2048) is None
+    assert _tuned_for(4, 999, 2048) is None
+    assert should_fuse(4, 2048, 2048) and should_fuse(16, 2048, 2048)
+    assert not should_fuse(32, 2048, 2048) and not should_fuse(96, 2048, 2048)
+    # target shapes extend to the 32-row verify, not to prefill
+    for K, N in [(4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096), (4096, 151936)]:
+        assert should_fuse(4, N, K) and should_fuse(16, N, K) and should_fuse(32, N, K)
+        assert not should_fuse(33, N, K) and not should_fuse(96, N, K)
+    assert len(pick_config(4, 2048, 2048)) == 4
+    assert pick_config(96, 2048, 2048)[0] == 32
+
+
+def test_rejects_grad_mode_and_dtype_mismatch_on_host():
+    from kernels.thin_linear_fused import thin_linear
+    x = torch.randn(4, 64, dtype=torch.bfloat16).requires_grad_(True)
+    w = torch.randn(32, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="forward-only"):
+        thin_linear(x, w)
+    with pytest.raises(TypeError):
+        with torch.inference_mode():
+            thin_linear(torch.randn(4, 64, dtype=torch.bfloat16), torch.randn(32, 64))
+    with pytest.raises(ValueError):
+        with torch.inference_mode():
+            thin_linear(torch.randn(4, 64, dtype=torch.bfloat16),
+                        torch.randn(2, 32, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        with torch.inference_mode():
+            thin_linear(torch.randn(4, 64, dtype=torch.bfloat16),
+                        torch.randn(32, 63, dtype=torch.bfloat16))
+
+
+def test_cpu_tensors_fail_loudly():
+    """No silent CPU fallback: host tensors are refused."""
+    from kernels.thin_linear_fused import thin_linear
+    from kernels.moe_dispatch_fused import moe_dispatch, moe_route
+    with pytest.raises(RuntimeError, match="device"):
+        with torch.inference_mode():
+            thin_linear(torch.randn(4, 64, dtype=torch.bfloat16),
+                        torch.randn(32, 64, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="device"):
+        moe_route(torch.randn(4, 16), 2)
+    with pytest.raises(RuntimeError, match="device"):
+        moe_dispatch(torch.randn(4, 8), torch.zeros(4, 2, dtype=torch.long),
+                     torch.ones(4, 2), torch.randn(3, 4, 8), torch.randn(3, 4, 8),
+                     torch.randn(3, 8, 4))
+
+
+def test_moe_num_tiles_and_block_m():
+    from kernels import moe_dispatch_fused as m
+    from kernels import _native
+    assert m.BLOCK_M == 16
+    for M, E in [(1, 256), (32, 256), (512, 256), (256, 8), (7, 13)]:
+        assert m._num_tiles(M, E) == _native.lib().simsd_moe_num_tiles(M, E)
+
+
+# ────────────────────────────────────────────── toggle (host modules) ───
+class _Tiny(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.q_proj = nn.Linear(512, 512, bias=False)
+        self.gate_proj = nn.Linear(512, 1024, bias=False)
+        self.other = nn.Linear(512, 8, bias=False)
+
+    def forward(self, x):
+        return self.gate_proj(self.q_proj(x)), self.other(x)
+
+
+def test_toggle_swaps_and_restores_host():
+    from kernels import fused_toggle
+    from kernels.thin_linear_fused import ThinLinear
+    m = _Tiny().eval()
+    x = torch.randn(4, 512)
+    with torch.inference_mode():
+        ref = m(x)
+    assert fused_toggle.apply_to_model(m, True) == 2
+    assert isinstance(m.q_proj, ThinLinear) and isinstance(m.other, nn.Linear)
+    assert fused_toggle.apply_to_model(m, True) == 0
+    with torch.inference_mode():
+        got = m(x)             # (512, 512) is not a tuned shape -> F.linear
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    assert fused_toggle.apply_to_model(m, False) == 2
+    assert isinstance(m.q_proj, nn.Linear) and not fused_toggle.is_applied(m)
+
+
+def test_toggle_state_dict_aliasing_and_noop_host():
+    from kernels import fused_toggle
+    m = _Tiny().eval()
+    before = {k: v.clone() for k, v in m.state_dict().items()}
+    ptr = m.q_proj.weight.data_ptr()
+    with fused_toggle.fused_linear(m):
+        after = m.state_dict()
+        assert set(after) == set(before)
+        assert all(torch.equal(after[k], before[k]) for k in before)
+        assert m.q_proj.weight.data_ptr() == ptr
+    m2 = _Tiny()
+    assert fused_toggle.apply_to_model(m2, False) == 0
+    assert isinstance(m2.q_proj, nn.Linear)
+
+
+def test_toggle_lm_head_opt_in():
+    from kernels import fused_toggle
+    from kernels.thin_linear_fused import ThinLinear
+
+    class M(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.o_proj = nn.Linear(8, 8)
+            self.lm_head = nn.Linear(8, 16)
+    m = M()
+    assert fused_toggle.apply_to_model(m, True) == 1
+    assert isinstance(m.lm_head, nn.Linear)
+    fused_toggle.apply_to_model(m, False)
+    assert fused_toggle.apply_to_model(m, True, targets=fused_toggle.ALL_TARGETS) == 2
+    assert isinstance(m.lm_head, ThinLinear)
+    fused_toggle.apply_to_model(m, False)
+
+
+class _Expert(nn.Module):
+    def __init__(self, H, I):
+        super().__init__()
+        self.gate_proj = nn.Linear(H, I, bias=False)
+        self.up_proj = nn.Linear(H, I, bias=False)
+        self.down_proj = nn.Linear(I, H, bias=False)
+
+
+class LLaDA2MoeSparseMoeBlock(nn.Module):
+    """Stand-in with the remote class's name and the moe_infer signature."""
+
+    def __init__(self, E=4, H=16, I=8):
+        super().__init__()
+        self.experts = nn.ModuleList(_Expert(H, I) for _ in range(E))
+
+    def moe_infer(self, x, topk_ids, topk_weight):
+        return "stock"
+
+
+def test_apply_moe_to_model_host():
+    from kernels import fused_toggle
+    from kernels.moe_dispatch_fused import stack_expert_weights
+    root = nn.Module()
+    root.blk = LLaDA2MoeSparseMoeBlock()
+    g0 = root.blk.experts[1].gate_proj.weight.detach().clone()
+    assert fused_toggle.apply_moe_to_model(root, True) == 1
+    assert fused_toggle.is_moe_applied(root)
+    wg, wu, wd = root.blk._simsd_fused_moe
+    assert wg.shape == (4, 8, 16) and wd.shape == (4, 16, 8)
+    assert torch.equal(wg[1], g0)
+    assert root.blk.experts[1].gate_proj.weight.numel() == 0        # destructive
+    assert fused_toggle.apply_moe_to_model(root, True) == 0          # idempotent
+    with pytest.raises(NotImplementedError):
+        fused_toggle.apply_moe_to_model(root, False)
+    # unpatched instances keep the stock method
+    other = LLaDA2MoeSparseMoeBlock()
+    assert other.moe_infer(None, None, None) == "stock"
+    ex = nn.ModuleList(_Expert(16, 8) for _ in range(3))
+    a, b, c = stack_expert_weights(ex, free_originals=False)
+    assert a.is_contiguous() and ex[0].gate_proj.weight.numel() == 128
