@@ -47,13 +47,15 @@ const char* simsd_last_error_string(void);
  * the kernels themselves (67-171).
  *   strides are in elements; any stride works (non-unit K strides and
  *   unaligned rows take a slower element-wise path);
- *   block_n: weight rows per workgroup (16 or 32; 0 = 16);
- *   split_k: workgroups along K (0 = automatic); the split partials are summed
- *            in index order (deterministic);
+ *   block_n: weight rows per workgroup (4, 8, 16 or 32; 0 = automatic);
+ *   split_k: workgroups along K (0 = automatic); with split_k > 1 fp32
+ *            partial tiles go to the workspace and a second launch sums them
+ *            in split order (deterministic);
  *   num_waves: waves per workgroup splitting K (2, 4 or 8; 0 = 4);
  *   workspace: needed only when split_k > 1 (size from
- *            simsd_thin_linear_workspace_bytes); must be zero-filled once
- *            before first use -- every call leaves its counters at zero.
+ *            simsd_thin_linear_workspace_bytes, 16-byte aligned, no
+ *            initialisation needed).
+ * Results are bit-identical across calls for the same shape and config.
  * K must be >= 1 (the caller handles K == 0). */
 int simsd_thin_linear(const void* x, int64_t stride_xm, int64_t stride_xk,
                       const void* w, int64_t stride_wn, int64_t stride_wk,

@@ -3,20 +3,24 @@
 // Replaces the Triton _thin_gemv_kernel / _thin_gemv_reduce pair of
 // kernels/thin_linear_fused.py:67-171 (reference).  Design for MI355X:
 //   * the weight streams straight from HBM into MFMA A operands with 128-bit
-//     non-temporal loads (16 rows x 64 B per wave per k-step), double-buffered;
+//     non-temporal loads, 64 B of every row per wave per k-step,
+//     double-buffered in registers;
 //   * the few activation rows are the MFMA B operand (16 columns per block,
-//     masked lanes for M < 16), read through L1/L2 where they stay resident;
-//   * a workgroup owns RB*16 weight rows and splits K across KS waves, whose
-//     fp32 partials meet in LDS in fixed wave order;
-//   * optional split-K across workgroups (SPLIT) for narrow N: every workgroup
-//     writes an fp32 partial tile, and the last one to arrive (device-scope
-//     counter) sums the SPLIT partials in index order -- deterministic, one
-//     launch, no atomics on data, and it leaves its counter at zero again.
-#include <stdarg.h>
-#include <stdio.h>
-
+//     masked lanes below 16 rows), read through L1/L2 where they stay resident;
+//   * a workgroup owns ROWS weight rows (4, 8, 16 or 32) and splits K across
+//     KS waves whose fp32 partials meet in LDS in fixed wave order.  Below 16
+//     rows the 16 MFMA A rows repeat the tile's rows (duplicates are loaded
+//     from the same cache lines and their outputs dropped), which buys
+//     workgroups for narrow N without any cross-workgroup reduction;
+//   * an explicit split along K (SPLIT > 1) writes fp32 partial tiles and a
+//     second launch sums them in split order: deterministic, no atomics, no
+//     cross-workgroup synchronisation inside a launch.
 #include "simsd_common.hpp"
 #include "simsd_kernels.h"
+
+#ifndef SIMSD_THIN_U
+#define SIMSD_THIN_U 8   // k-steps per pipeline stage at one A and one B block
+#endif
 
 namespace simsd {
 
@@ -29,22 +33,22 @@ struct ThinArgs {
   int64_t sb;
   char* y;
   int64_t sym, syn;
-  float* part;               // [split][M][N] fp32, used when split > 1
-  uint32_t* counters;        // [gridDim.z][gridDim.x], zero between launches
+  float* part;               // [split][M][N] fp32 partials when split > 1
   int64_t M, N, K;
   int steps;                 // ceil(K * esize / 64)
-  int split;                 // workgroups along K
   int steps_per_split;
 };
 
-template <int DT, int RB, int CB, int KS, int U, bool FAST>
+template <int DT, int RT, int RB, int CB, int KS, int U, bool FAST, bool PARTIAL>
 __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
+  static_assert(RT == 4 || RT == 8 || RT == 16, "rows per block");
+  static_assert(RT == 16 || RB == 1, "sub-16-row tiles use one block");
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int NF = RB * CB;
   const int lane = threadIdx.x & 63;
   const int wk = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int64_t n_tile = (int64_t)blockIdx.x * (RB * 16);
+  const int64_t n_tile = (int64_t)blockIdx.x * (RT * RB);
   const int64_t m_tile = (int64_t)blockIdx.z * (CB * 16);
   const int split_id = blockIdx.y;
 
@@ -66,7 +70,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
   const char* brow[CB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int64_t n = min(n_tile + rb * 16 + r, a.N - 1);
+    const int64_t n = min(n_tile + rb * RT + (r % RT), a.N - 1);
     arow[rb] = a.w + n * a.swn * ES;
   }
 #pragma unroll
@@ -82,157 +86,167 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
 
   __shared__ float red[KS > 1 ? (KS - 1) * NF * 4 * 64 : 1];
   reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, red);
+  if (wk != 0 || 4 * g >= RT) return;   // lanes of duplicated rows hold no new output
 
-  const bool single = a.split == 1;
-  if (wk == 0) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int64_t m = m_tile + cb * 16 + r;
-        const int64_t nb = n_tile + rb * 16 + 4 * g;
-        if (m < a.M) {
+    for (int cb = 0; cb < CB; ++cb) {
+      const int64_t m = m_tile + cb * 16 + r;
+      const int64_t nb = n_tile + rb * RT + 4 * g;
+      if (m < a.M) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int64_t n = nb + j;
-            if (n < a.N) {
-              float v = acc[rb][cb][j];
-              if (single) {
-                if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
-                store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
-              } else {
-                a.part[((int64_t)split_id * a.M + m) * a.N + n] = v;
-              }
+        for (int j = 0; j < 4; ++j) {
+          const int64_t n = nb + j;
+          if (n < a.N) {
+            float v = acc[rb][cb][j];
+            if (PARTIAL) {
+              a.part[((int64_t)split_id * a.M + m) * a.N + n] = v;
+            } else {
+              if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+              store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
             }
           }
         }
       }
-  }
-  if (single) return;
-
-  // ---- split-K: the last workgroup of this tile sums the partials in order
-  __shared__ uint32_t s_last;
-  __threadfence();
-  __syncthreads();
-  const int64_t cidx = (int64_t)blockIdx.z * gridDim.x + blockIdx.x;
-  if (threadIdx.x == 0) {
-    const uint32_t old = atomicAdd(&a.counters[cidx], 1u);
-    s_last = (old == (uint32_t)(a.split - 1)) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (s_last == 0u) return;
-  __threadfence();
-  constexpr int TR = RB * 16, TC = CB * 16;
-  for (int e = threadIdx.x; e < TR * TC; e += blockDim.x) {
-    const int64_t n = n_tile + (e % TR);
-    const int64_t m = m_tile + (e / TR);
-    if (n < a.N && m < a.M) {
-      float v = 0.f;
-      for (int s = 0; s < a.split; ++s) v += a.part[((int64_t)s * a.M + m) * a.N + n];
-      if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
-      store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
     }
-  }
-  if (threadIdx.x == 0) a.counters[cidx] = 0u;
+}
+
+// Sum the split partials in split order (fixed: bit-reproducible), add bias,
+// round to the output dtype.  One thread per output element.
+template <int DT>
+__global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restrict__ part, int split,
+                                                          int64_t M, int64_t N,
+                                                          const char* bias, int64_t sb, char* y,
+                                                          int64_t sym, int64_t syn) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= M * N) return;
+  const int64_t m = e / N, n = e % N;
+  float v = 0.f;
+  for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + e];
+  if (bias != nullptr) v += load_elem<DT>(bias, n * sb);
+  store_elem<DT>(y, m * sym + n * syn, v);
 }
 
 // ------------------------------------------------------------------ host side
 namespace {
 
 struct ThinPlan {
-  int rb, cb, ks, split;
+  int rows, rt, rb, cb, ks, split;
   bool fast;
   int64_t tiles_n, tiles_m;
   int steps, steps_per_split;
-  int64_t counter_bytes, part_bytes;
+  int64_t part_bytes;
 };
 
 inline int esize_of(int dtype) { return dtype == kF32 ? 4 : 2; }
-
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-constexpr int kTargetWorkgroups = 512;   // 2 per CU on 256 CUs
+constexpr int kMinWorkgroups = 256;   // one per CU on MI355X
 constexpr int kMaxSplit = 16;
 
-// Geometry only (no pointers): rows per workgroup, column blocks, waves per
-// workgroup, split along K, and the workspace that split needs.
-int plan_geometry(ThinPlan& pl, int64_t M, int64_t N, int64_t K, int dtype, int rb, int ks,
-                  int split_k) {
+// Geometry only (no pointers).  block_n = weight rows per workgroup (0 = the
+// fewest of 16, 8, 4 that still gives every CU a workgroup); split along K
+// only when even 4-row tiles leave CUs idle (0 = automatic).
+int plan_geometry(ThinPlan& pl, int64_t M, int64_t N, int64_t K, int dtype, int block_n,
+                  int num_waves, int split_k) {
   const int es = esize_of(dtype);
   pl.cb = M <= 16 ? 1 : 2;
-  pl.rb = rb;
-  pl.ks = ks;
-  pl.tiles_n = (N + 16 * pl.rb - 1) / (16 * pl.rb);
-  pl.tiles_m = (M + 16 * pl.cb - 1) / (16 * pl.cb);
-  pl.steps = (int)((K * es + kStepBytes - 1) / kStepBytes);
+  pl.tiles_m = cdiv(M, 16 * pl.cb);
+  pl.ks = num_waves <= 0 ? 4 : num_waves;
+  if (pl.ks != 2 && pl.ks != 4 && pl.ks != 8)
+    return set_error("thin_linear: num_waves must be 2, 4 or 8 (got %d)", num_waves);
+  int rows = block_n;
+  if (rows == 0) {
+    rows = 4;
+    for (int cand : {16, 8}) {
+      if (cdiv(N, cand) * pl.tiles_m >= kMinWorkgroups) { rows = cand; break; }
+    }
+  }
+  if (rows != 4 && rows != 8 && rows != 16 && rows != 32)
+    return set_error("thin_linear: block_n must be 4, 8, 16 or 32 (got %d)", block_n);
+  pl.rows = rows;
+  pl.rt = rows >= 16 ? 16 : rows;
+  pl.rb = rows >= 16 ? rows / 16 : 1;
+  pl.tiles_n = cdiv(N, rows);
+  pl.steps = (int)cdiv(K * es, kStepBytes);
   int split = split_k;
   if (split <= 0) {
-    // Enough workgroups to put two on every CU, but never fewer than four
-    // k-steps per wave.
     const int64_t wgs = pl.tiles_n * pl.tiles_m;
-    split = (int)((kTargetWorkgroups + wgs - 1) / wgs);
-    const int max_by_k = pl.steps / (pl.ks * 4);
-    split = max(1, min(split, min(kMaxSplit, max_by_k)));
+    split = 1;
+    if (wgs < kMinWorkgroups / 2) {
+      split = (int)cdiv(kMinWorkgroups, wgs);
+      split = max(1, min(split, min(kMaxSplit, pl.steps / (pl.ks * 4))));
+    }
   }
   if (split > 1024) return set_error("thin_linear: split_k=%d exceeds 1024", split);
   pl.split = split;
-  pl.steps_per_split = (pl.steps + split - 1) / split;
-  pl.counter_bytes = split > 1 ? ((pl.tiles_n * pl.tiles_m * 4 + 255) / 256) * 256 : 0;
+  pl.steps_per_split = (int)cdiv(pl.steps, split);
   pl.part_bytes = split > 1 ? (int64_t)split * M * N * 4 : 0;
   return 0;
-}
-
-inline int rb_of(int block_n) { return block_n >= 32 ? 2 : 1; }
-inline int ks_of(int num_waves) {
-  return num_waves <= 0 ? 4 : (num_waves <= 2 ? 2 : (num_waves <= 4 ? 4 : 8));
 }
 
 int make_plan(ThinPlan& pl, const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn,
               int64_t swk, int64_t M, int64_t N, int64_t K, int dtype, int block_n, int split_k,
               int num_waves) {
   const int es = esize_of(dtype);
-  const bool w_vec = swk == 1 && aligned16(w) && ((swn * es) % 16 == 0 || N == 1) && (K * es) % 16 == 0;
+  const bool w_vec = swk == 1 && aligned16(w) && ((swn * es) % 16 == 0 || N == 1) &&
+                     (K * es) % 16 == 0;
   const bool x_vec = sxk == 1 && aligned16(x) && ((sxm * es) % 16 == 0 || M == 1);
-  const bool fast = w_vec && x_vec;
-  // The strided path has a single shape: 16 rows per workgroup, 4 waves.
-  if (plan_geometry(pl, M, N, K, dtype, fast ? rb_of(block_n) : 1, fast ? ks_of(num_waves) : 4,
+  pl.fast = w_vec && x_vec;
+  // The strided path has one shape: 16 rows per workgroup, 4 waves.
+  if (plan_geometry(pl, M, N, K, dtype, pl.fast ? block_n : 16, pl.fast ? num_waves : 4,
                     split_k) != 0)
     return -1;
-  pl.fast = fast;
   return 0;
 }
 
-template <int DT, int RB, int CB, int KS, bool FAST>
-void launch_thin(const ThinPlan& pl, const ThinArgs& args, void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  constexpr int U = (RB * CB == 1) ? 8 : 4;
+template <int DT, int RT, int RB, int CB, int KS, bool FAST>
+void launch_main(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  constexpr int U = (RB * CB == 1) ? SIMSD_THIN_U : SIMSD_THIN_U / 2;
   dim3 grid((unsigned)pl.tiles_n, (unsigned)pl.split, (unsigned)pl.tiles_m);
-  hipLaunchKernelGGL((thin_gemm_kernel<DT, RB, CB, KS, U, FAST>), grid, dim3(64 * KS), 0, stream,
-                     args);
+  if (pl.split > 1)
+    hipLaunchKernelGGL((thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, true>), grid, dim3(64 * KS),
+                       0, stream, args);
+  else
+    hipLaunchKernelGGL((thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, false>), grid, dim3(64 * KS),
+                       0, stream, args);
 }
 
-template <int DT, int RB, int CB>
-void dispatch_ks(const ThinPlan& pl, const ThinArgs& args, void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
+template <int DT, int RT, int RB, int CB>
+void dispatch_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.ks) {
-    case 2: launch_thin<DT, RB, CB, 2, true>(pl, args, stream); break;
-    case 8: launch_thin<DT, RB, CB, 8, true>(pl, args, stream); break;
-    default: launch_thin<DT, RB, CB, 4, true>(pl, args, stream); break;
+    case 2: launch_main<DT, RT, RB, CB, 2, true>(pl, args, stream); break;
+    case 8: launch_main<DT, RT, RB, CB, 8, true>(pl, args, stream); break;
+    default: launch_main<DT, RT, RB, CB, 4, true>(pl, args, stream); break;
+  }
+}
+
+template <int DT, int CB>
+void dispatch_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  if (!pl.fast) {   // strided path: one shape, 16 rows, 4 waves
+    launch_main<DT, 16, 1, CB, 4, false>(pl, args, stream);
+    return;
+  }
+  switch (pl.rows) {
+    case 4: dispatch_ks<DT, 4, 1, CB>(pl, args, stream); break;
+    case 8: dispatch_ks<DT, 8, 1, CB>(pl, args, stream); break;
+    case 32: dispatch_ks<DT, 16, 2, CB>(pl, args, stream); break;
+    default: dispatch_ks<DT, 16, 1, CB>(pl, args, stream); break;
   }
 }
 
 template <int DT>
-void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, void* stream_) {
-  hipStream_t stream = static_cast<hipStream_t>(stream_);
-  if (!pl.fast) {
-    if (pl.cb == 1) launch_thin<DT, 1, 1, 4, false>(pl, args, stream);
-    else launch_thin<DT, 1, 2, 4, false>(pl, args, stream);
-    return;
+void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  if (pl.cb == 1) dispatch_rows<DT, 1>(pl, args, stream);
+  else dispatch_rows<DT, 2>(pl, args, stream);
+  if (pl.split > 1) {
+    const int64_t total = args.M * args.N;
+    hipLaunchKernelGGL((thin_reduce_kernel<DT>), dim3((unsigned)cdiv(total, 256)), dim3(256), 0,
+                       stream, args.part, pl.split, args.M, args.N, args.bias, args.sb, args.y,
+                       args.sym, args.syn);
   }
-  if (pl.rb == 1 && pl.cb == 1) dispatch_ks<DT, 1, 1>(pl, args, stream);
-  else if (pl.rb == 1) dispatch_ks<DT, 1, 2>(pl, args, stream);
-  else if (pl.cb == 1) dispatch_ks<DT, 2, 1>(pl, args, stream);
-  else dispatch_ks<DT, 2, 2>(pl, args, stream);
 }
 
 }  // namespace
@@ -243,12 +257,11 @@ using namespace simsd;
 extern "C" int64_t simsd_thin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype,
                                                      int block_n, int split_k, int num_waves) {
   // Enough for either path: the requested geometry (vector-capable operands)
-  // and the strided fallback (16 rows, 4 waves).
+  // and the strided one (16 rows, 4 waves).
   ThinPlan a{}, b{};
-  if (plan_geometry(a, M, N, K, dtype, rb_of(block_n), ks_of(num_waves), split_k) != 0) return -1;
-  if (plan_geometry(b, M, N, K, dtype, 1, 4, split_k) != 0) return -1;
-  const int64_t na = a.counter_bytes + a.part_bytes, nb = b.counter_bytes + b.part_bytes;
-  return na > nb ? na : nb;
+  if (plan_geometry(a, M, N, K, dtype, block_n, num_waves, split_k) != 0) return -1;
+  if (plan_geometry(b, M, N, K, dtype, 16, 4, split_k) != 0) return -1;
+  return a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes;
 }
 
 extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const void* w,
@@ -268,7 +281,7 @@ extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const 
   ThinPlan pl{};
   if (make_plan(pl, x, sxm, sxk, w, swn, swk, M, N, K, dtype, block_n, split_k, num_waves) != 0)
     return -1;
-  if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535)
+  if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535 || cdiv(M * N, 256) > 0x7fffffff)
     return set_error("thin_linear: grid too large (N=%lld, M=%lld)", (long long)N, (long long)M);
   ThinArgs args{};
   args.x = static_cast<const char*>(x);
@@ -281,16 +294,13 @@ extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const 
   args.sym = sym; args.syn = syn;
   args.M = M; args.N = N; args.K = K;
   args.steps = pl.steps;
-  args.split = pl.split;
   args.steps_per_split = pl.steps_per_split;
   if (pl.split > 1) {
-    const int64_t need = pl.counter_bytes + pl.part_bytes;
-    if (workspace == nullptr || workspace_bytes < need)
+    if (workspace == nullptr || workspace_bytes < pl.part_bytes)
       return set_error("thin_linear: split_k=%d needs a %lld-byte workspace (got %lld)", pl.split,
-                       (long long)need, (long long)workspace_bytes);
+                       (long long)pl.part_bytes, (long long)workspace_bytes);
     if (!aligned16(workspace)) return set_error("thin_linear: workspace must be 16-byte aligned");
-    args.counters = static_cast<uint32_t*>(workspace);
-    args.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.counter_bytes);
+    args.part = static_cast<float*>(workspace);
   }
   switch (dtype) {
     case kBF16: dispatch_dt<kBF16>(pl, args, stream); break;
@@ -305,8 +315,8 @@ extern "C" int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype
   // (rows per workgroup, columns per block, waves per workgroup, split) of the
   // vector-path geometry; lets the Python side report the config it runs.
   ThinPlan pl{};
-  if (plan_geometry(pl, M, N, K, dtype, rb_of(block_n), ks_of(num_waves), split_k) != 0) return -1;
-  out4[0] = 16 * pl.rb;
+  if (plan_geometry(pl, M, N, K, dtype, block_n, num_waves, split_k) != 0) return -1;
+  out4[0] = pl.rows;
   out4[1] = 16 * pl.cb;
   out4[2] = pl.ks;
   out4[3] = pl.split;

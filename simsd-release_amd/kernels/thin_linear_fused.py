@@ -16,18 +16,20 @@ Each wave streams 16 weight rows with 128-bit loads straight into the A
 operand of ``v_mfma_f32_16x16x32_bf16`` while the M activation rows are the B
 operand (masked lanes below 16 rows, a second column block up to 32 rows).
 MFMA does the fp32-accumulate arithmetic for free relative to the byte rate,
-which leaves the VALU idle and keeps the loads in flight.  A workgroup splits K
-over its waves and sums their fp32 partials in LDS in fixed order; a narrow N
-additionally splits K over workgroups, whose partials are summed in index order
-by the last workgroup to finish (one launch, no atomics on data).
+which leaves the VALU idle and keeps the loads in flight.  A workgroup owns 4,
+8, 16 or 32 weight rows and splits K over its waves, which sum their fp32
+partials in LDS in fixed order; narrow N uses fewer rows per workgroup (the
+MFMA rows repeat) so every CU still gets work without a cross-workgroup
+reduction.  An explicit SPLIT_K > 1 splits K over workgroups too: fp32 partial
+tiles, then a second launch sums them in split order.
 
 Config tuples keep the reference's shape ``(BLOCK_M, BLOCK_N, BLOCK_K,
 SPLIT_K[, num_warps, num_stages])`` but describe the MI355X kernel:
 BLOCK_M is the activation-row envelope (16, or 32 with two column blocks),
-BLOCK_N the weight rows per workgroup (16 or 32), BLOCK_K the K elements one
-wave streams per pipeline stage, SPLIT_K the workgroups along K, num_warps the
-waves per workgroup (2, 4 or 8) and num_stages the register double-buffer
-depth (always 2).
+BLOCK_N the weight rows per workgroup (4, 8, 16 or 32; other values round down
+to one of these), BLOCK_K the K elements one wave streams per pipeline stage,
+SPLIT_K the workgroups along K, num_warps the waves per workgroup (2, 4 or 8)
+and num_stages the register double-buffer depth (always 2).
 
 Contract (reference CONTRACT, kernels/workspace/thin_linear/CONTRACT.md:26-91):
 forward only; fp32 accumulation for bf16/fp16/fp32 inputs; deterministic
@@ -42,9 +44,10 @@ import torch
 from . import _native
 
 # Tuning knobs (kernels/thin_linear_fused.py:59-61).  MI355X has 256 CUs.
-TARGET_CTAS = 2 * 256          # aim for two workgroups on every CU
+TARGET_CTAS = 256              # at least one workgroup on every CU
 MAX_SPLIT_K = 16
 MIN_K_PER_SPLIT = 512          # bf16 elements; a split is at least 4 k-steps per wave
+_ROWS = (4, 8, 16, 32)         # weight rows per workgroup the kernel is built for
 
 _STEP_BYTES = 64               # bytes of a weight row one MFMA k-step consumes
 _DEFAULT_WAVES = 4
@@ -63,18 +66,18 @@ def _cdiv(a: int, b: int) -> int:
 # ─────────────────────────────────────────────────────────────────────────────
 # Workspace (kernels/thin_linear_fused.py:173-190)
 # ─────────────────────────────────────────────────────────────────────────────
-# device -> byte buffer holding the split-K tile counters and fp32 partials.
-# Zero-filled when (re)allocated; every kernel call leaves its counters at zero
-# again, so the buffer is reused without clearing.  Calls that share a device
-# are ordered on one stream (a captured graph replays them serially); two
-# streams running split-K calls on one device at once would race on it.
+# device -> byte buffer for the fp32 split-K partial tiles, reused without
+# reallocation (the hot path allocates nothing once it has grown).  Calls that
+# share a device are ordered on one stream (a captured graph replays them
+# serially); two streams running split-K calls on one device at once would
+# race on it.
 _PARTIALS: dict[torch.device, torch.Tensor] = {}
 
 
 def _partials(dev: torch.device, nbytes: int) -> torch.Tensor:
     buf = _PARTIALS.get(dev)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 4096), device=dev, dtype=torch.uint8)
+        buf = torch.empty(max(nbytes, 4096), device=dev, dtype=torch.uint8)
         _PARTIALS[dev] = buf
     return buf
 
@@ -88,26 +91,28 @@ def reset_workspace() -> None:
 # Configs (kernels/thin_linear_fused.py:193-262)
 # ─────────────────────────────────────────────────────────────────────────────
 # (K, N) -> (BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K, num_warps, num_stages).
-# BLOCK_M is the largest M the entry covers.  Values are the automatic plan's
-# choice until an MI355X sweep (M=4 draft, M=16/32 target, bf16, HIP graph over
-# a weight pool larger than the 256 MB MALL) replaces them.
+# BLOCK_M is the largest M the entry covers.  Chosen by sweeping rows per
+# workgroup x waves x split on one MI355X (M=4 for draft shapes, M=16 and 32
+# for target shapes; bf16; HIP graph over a >= 1 GiB weight pool so the
+# 256 MB MALL cannot serve repeats).  Entries not swept directly (separate
+# gate/up, k/v and lm_head of the target) follow the nearest swept shape.
 TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     # SDAR-1.7B draft projections (hidden 2048, 16 q / 8 kv heads, inter 6144)
-    (2048, 2048): (16, 16, 256, 4, 4, 2),     # q_proj, o_proj
-    (2048, 1024): (16, 16, 256, 4, 4, 2),     # k_proj, v_proj
-    (2048, 6144): (16, 16, 256, 2, 4, 2),     # gate_proj, up_proj
-    (6144, 2048): (16, 16, 256, 4, 4, 2),     # down_proj
-    (2048, 151936): (16, 16, 256, 1, 4, 2),   # lm_head
-    (2048, 4096): (16, 16, 256, 2, 4, 2),     # merged qkv
-    (2048, 12288): (16, 16, 256, 1, 4, 2),    # merged gate+up
+    (2048, 2048): (16, 8, 256, 1, 4, 2),      # q_proj, o_proj      5.3 us
+    (2048, 1024): (16, 8, 256, 1, 8, 2),      # k_proj, v_proj      5.2 us
+    (2048, 6144): (16, 16, 256, 1, 2, 2),     # gate_proj, up_proj
+    (6144, 2048): (16, 8, 256, 1, 8, 2),      # down_proj          11.0 us
+    (2048, 151936): (16, 16, 256, 1, 2, 2),   # lm_head
+    (2048, 4096): (16, 16, 256, 1, 4, 2),     # merged qkv          5.9 us
+    (2048, 12288): (16, 16, 256, 1, 2, 2),    # merged gate+up     12.3 us
     # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
-    (4096, 12288): (32, 16, 128, 1, 4, 2),    # gate_proj / up_proj
-    (4096, 4096): (32, 16, 128, 2, 4, 2),     # q_proj, o_proj
-    (4096, 1024): (32, 16, 128, 8, 4, 2),     # k_proj, v_proj
-    (4096, 6144): (32, 16, 128, 2, 4, 2),     # merged qkv
-    (4096, 24576): (32, 16, 128, 1, 4, 2),    # merged gate+up
-    (12288, 4096): (32, 16, 128, 2, 4, 2),    # down_proj
-    (4096, 151936): (32, 16, 128, 1, 4, 2),   # lm_head
+    (4096, 12288): (32, 32, 128, 1, 2, 2),    # gate_proj / up_proj
+    (4096, 4096): (32, 16, 128, 1, 4, 2),     # q_proj, o_proj     12.0 / 16.0 us (M=16 / 32)
+    (4096, 1024): (32, 8, 128, 1, 4, 2),      # k_proj, v_proj
+    (4096, 6144): (32, 32, 128, 1, 4, 2),     # merged qkv         17.7 / 23.3 us
+    (4096, 24576): (32, 32, 128, 1, 2, 2),    # merged gate+up     51.6 / 63.7 us
+    (12288, 4096): (32, 16, 128, 1, 4, 2),    # down_proj          32.7 / 43.4 us
+    (4096, 151936): (32, 32, 128, 1, 2, 2),   # lm_head
 }
 
 
@@ -134,15 +139,33 @@ def _tuned_for(M: int, N: int, K: int):
 
 
 def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, int, int, int]:
-    """Same rule as the library's automatic plan (``simsd_thin_linear_plan``)."""
+    """Same rule as the library's automatic plan (``simsd_thin_linear_plan``).
+
+    The fewest weight rows per workgroup (16, then 8, else 4) that still give
+    every CU a workgroup; a split along K only when even 4-row tiles leave
+    more than half the CUs idle.
+    """
     BLOCK_M = 16 if M <= 16 else 32
-    BLOCK_N = 16
     BLOCK_K = (256 if BLOCK_M == 16 else 128) * 2 // itemsize
-    tiles = _cdiv(N, BLOCK_N) * _cdiv(M, BLOCK_M)
-    steps = _cdiv(K * itemsize, _STEP_BYTES)
-    split = _cdiv(TARGET_CTAS, tiles)
-    split = max(1, min(split, MAX_SPLIT_K, steps // (MIN_K_PER_SPLIT * 2 // _STEP_BYTES)))
+    m_tiles = _cdiv(M, BLOCK_M)
+    BLOCK_N = 4
+    for cand in (16, 8):
+        if _cdiv(N, cand) * m_tiles >= TARGET_CTAS:
+            BLOCK_N = cand
+            break
+    tiles = _cdiv(N, BLOCK_N) * m_tiles
+    split = 1
+    if tiles < TARGET_CTAS // 2:
+        steps = _cdiv(K * itemsize, _STEP_BYTES)
+        split = _cdiv(TARGET_CTAS, tiles)
+        split = max(1, min(split, MAX_SPLIT_K, steps // (MIN_K_PER_SPLIT * 2 // _STEP_BYTES)))
     return BLOCK_M, BLOCK_N, BLOCK_K, split
+
+
+def _rows_for(block_n: int) -> int:
+    """The kernel's rows-per-workgroup for a requested BLOCK_N (round down)."""
+    fit = [r for r in _ROWS if r <= max(int(block_n), _ROWS[0])]
+    return fit[-1]
 
 
 # ─────────────────────────────────────────────────────────────────────────────
@@ -201,6 +224,8 @@ def thin_linear(x: torch.Tensor, w: torch.Tensor,
         waves = num_warps or waves
     if split_k < 1:
         raise ValueError(f"SPLIT_K must be >= 1, got {split_k}")
+    block_n = _rows_for(block_n)
+    waves = 2 if waves <= 2 else (4 if waves <= 4 else 8)
 
     fuse_bias = (bias is not None and bias.dtype == x.dtype and bias.ndim == 1
                  and bias.shape[0] == N and bias.device == dev)

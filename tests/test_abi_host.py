@@ -101,8 +101,8 @@ def test_workspace_sizes():
     lib = _native.lib()
     assert lib.simsd_thin_linear_workspace_bytes(4, 2048, 2048, 0, 16, 1, 4) == 0
     n = lib.simsd_thin_linear_workspace_bytes(4, 2048, 6144, 0, 16, 8, 4)
-    # counters for 128 tiles (rounded to 256 B) + 8 fp32 partial tiles of 4 x 2048
-    assert n == 512 + 8 * 4 * 2048 * 4
+    assert n == 8 * 4 * 2048 * 4          # 8 fp32 partial tiles of 4 x 2048
+    assert lib.simsd_thin_linear_workspace_bytes(4, 2048, 6144, 0, 12, 1, 4) == -1   # bad block_n
     assert lib.simsd_moe_num_tiles(512, 256) == 256 + 32
     assert lib.simsd_moe_num_tiles(32, 256) == 32 + 2
     w = lib.simsd_moe_workspace_bytes(64, 8, 2048, 512, 512, 0)
