@@ -294,28 +294,46 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   const bool shared = tr.e < 0;
   const int64_t II = shared ? a.Is : a.I;
   if (i0 >= II) return;
-  const int64_t i_row = min(i0 + r, II - 1);
-  const char* arow[2];
-  int64_t a_sk[2];
+  const char* wbase[2];
+  int64_t a_sn[2], a_sk[2];
   if (shared) {
-    arow[0] = a.shg + i_row * a.shg_i * ES;
-    arow[1] = a.shu + i_row * a.shu_i * ES;
+    wbase[0] = a.shg;
+    wbase[1] = a.shu;
+    a_sn[0] = a.shg_i; a_sn[1] = a.shu_i;
     a_sk[0] = a.shg_h * ES;
     a_sk[1] = a.shu_h * ES;
   } else {
-    arow[0] = a.wg + ((int64_t)tr.e * a.sge + i_row * a.sgi) * ES;
-    arow[1] = a.wu + ((int64_t)tr.e * a.sue + i_row * a.sui) * ES;
+    wbase[0] = a.wg + (int64_t)tr.e * a.sge * ES;
+    wbase[1] = a.wu + (int64_t)tr.e * a.sue * ES;
+    a_sn[0] = a.sgi; a_sn[1] = a.sui;
     a_sk[0] = a.sgh * ES;
     a_sk[1] = a.suh * ES;
   }
-  const char* brow[1] = {tr.token >= 0 ? a.x + tr.token * a.sxt * ES : nullptr};
   const int steps = (int)((a.H * ES + kStepBytes - 1) / kStepBytes);
   const int per_w = (steps + KS - 1) / KS;
   const int w0 = wk * per_w, w1 = min(steps, w0 + per_w);
   f32x4_t acc[2][1] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}}, {f32x4_t{0.f, 0.f, 0.f, 0.f}}};
   if (FAST) {
-    accum_fast<DT, 2, 1, U>(arow, brow, w0, w1, g * kLaneBytes, a.H * ES, acc);
+    // descriptors: the expert's gate and up matrices, and all of x; rows past
+    // II and empty slots read as zero
+    const uint32_t Kb = (uint32_t)(a.H * ES);
+    rsrc_t ra[2];
+    uint32_t aoff[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t sn_b = (uint32_t)(a_sn[b] * ES);
+      ra[b] = make_rsrc(wbase[b], (uint32_t)(II - 1) * sn_b + Kb);
+      aoff[b] = (uint32_t)(i0 + r) * sn_b;
+    }
+    const uint32_t sxt_b = (uint32_t)(a.sxt * ES);
+    const rsrc_t rB = make_rsrc(a.x, (uint32_t)(a.T - 1) * sxt_b + Kb);
+    const uint32_t boff[1] = {tr.token >= 0 ? (uint32_t)tr.token * sxt_b : 0u};
+    const bool bok[1] = {tr.token >= 0};
+    accum_fast<DT, 2, 1, U>(ra, aoff, rB, boff, bok, w0, w1, (uint32_t)(g * kLaneBytes), Kb, acc);
   } else {
+    const int64_t i_row = min(i0 + r, II - 1);
+    const char* arow[2] = {wbase[0] + i_row * a_sn[0] * ES, wbase[1] + i_row * a_sn[1] * ES};
+    const char* brow[1] = {tr.token >= 0 ? a.x + tr.token * a.sxt * ES : nullptr};
     // both A blocks share one k-stride in the generic gather; use per-block calls
     const char* a0[1] = {arow[0]};
     const char* a1[1] = {arow[1]};
@@ -356,22 +374,27 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
   const bool shared = tr.e < 0;
   if (n0 >= a.H) return;
   const int64_t II = shared ? a.Is : a.I;
-  const int64_t n_row = min(n0 + r, a.H - 1);
-  const char* arow[1];
-  int64_t a_sk;
-  if (shared) {
-    arow[0] = a.shd + n_row * a.shd_h * ES;
-    a_sk = a.shd_i * ES;
-  } else {
-    arow[0] = a.wd + ((int64_t)tr.e * a.sde + n_row * a.sdh) * ES;
-    a_sk = a.sdi * ES;
-  }
-  const char* brow[1] = {nullptr};
-  if (tr.slot >= 0) brow[0] = shared ? a.hs + tr.slot * a.Is * ES : a.h + tr.slot * a.I * ES;
+  const char* wbase = shared ? a.shd : a.wd + (int64_t)tr.e * a.sde * ES;
+  const int64_t a_sn = shared ? a.shd_h : a.sdh;
+  const int64_t a_sk = (shared ? a.shd_i : a.sdi) * ES;
+  const char* hbase = shared ? a.hs : a.h;   // slot-major (or token-major) h, row length II
   const int steps = (int)((II * ES + kStepBytes - 1) / kStepBytes);
   f32x4_t acc[1][1] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}}};
-  if (FAST) accum_fast<DT, 1, 1, U>(arow, brow, 0, steps, g * kLaneBytes, II * ES, acc);
-  else accum_generic<DT, 1, 1>(arow, a_sk, brow, ES, 0, steps, g, II, acc);
+  if (FAST) {
+    const uint32_t Kb = (uint32_t)(II * ES);
+    const uint32_t sn_b = (uint32_t)(a_sn * ES);
+    const int64_t h_rows = shared ? a.T : a.T * a.k;
+    const rsrc_t ra[1] = {make_rsrc(wbase, (uint32_t)(a.H - 1) * sn_b + Kb)};
+    const uint32_t aoff[1] = {(uint32_t)(n0 + r) * sn_b};
+    const rsrc_t rB = make_rsrc(hbase, (uint32_t)h_rows * Kb);
+    const uint32_t boff[1] = {tr.slot >= 0 ? (uint32_t)tr.slot * Kb : 0u};
+    const bool bok[1] = {tr.slot >= 0};
+    accum_fast<DT, 1, 1, U>(ra, aoff, rB, boff, bok, 0, steps, (uint32_t)(g * kLaneBytes), Kb, acc);
+  } else {
+    const char* arow[1] = {wbase + min(n0 + r, a.H - 1) * a_sn * ES};
+    const char* brow[1] = {tr.slot >= 0 ? hbase + tr.slot * II * ES : nullptr};
+    accum_generic<DT, 1, 1>(arow, a_sk, brow, ES, 0, steps, g, II, acc);
+  }
   if (tr.slot < 0) return;
   char* orow = shared ? a.ys + tr.slot * a.H * ES : a.y + tr.slot * a.H * ES;
 #pragma unroll
@@ -541,13 +564,21 @@ extern "C" int simsd_moe_grouped_ffn(
   a.out = static_cast<char*>(out); a.sot = sot; a.soh = soh;
   a.T = T; a.H = H; a.I = I; a.Is = Is;
   a.k = k; a.E = (int)E; a.num_tiles = num_tiles; a.shared_tiles = (int)shared_tiles;
-  // 16-byte paths: every operand row K-contiguous, 16-byte aligned, K*es % 16 == 0.
+  // 16-byte paths: every operand row K-contiguous, 16-byte aligned, K*es % 16 == 0,
+  // and every buffer-descriptor extent addressable with 32-bit offsets.
+  const int64_t lim = (int64_t)kOob;
+  const int64_t Imax = I > Is ? I : Is;
   bool fast_gu = row_ok(x, sxt, sxh, H, es) && row_ok(w_gate, sgi, sgh, H, es) &&
-                 row_ok(w_up, sui, suh, H, es) && (sge * es) % 16 == 0 && (sue * es) % 16 == 0;
-  bool fast_dn = row_ok(w_down, sdh, sdi, I, es) && (sde * es) % 16 == 0;
+                 row_ok(w_up, sui, suh, H, es) && (sge * es) % 16 == 0 && (sue * es) % 16 == 0 &&
+                 sxt > 0 && sgi > 0 && sui > 0 && T * sxt * es < lim &&
+                 (I + 16) * sgi * es < lim && (I + 16) * sui * es < lim;
+  bool fast_dn = row_ok(w_down, sdh, sdi, I, es) && (sde * es) % 16 == 0 && sdh > 0 &&
+                 (H + 16) * sdh * es < lim && T * k * Imax * es < lim;
   if (has_shared) {
-    fast_gu = fast_gu && row_ok(sh_gate, shg_i, shg_h, H, es) && row_ok(sh_up, shu_i, shu_h, H, es);
-    fast_dn = fast_dn && row_ok(sh_down, shd_h, shd_i, Is, es);
+    fast_gu = fast_gu && row_ok(sh_gate, shg_i, shg_h, H, es) && row_ok(sh_up, shu_i, shu_h, H, es) &&
+              shg_i > 0 && shu_i > 0 && (Is + 16) * shg_i * es < lim && (Is + 16) * shu_i * es < lim;
+    fast_dn = fast_dn && row_ok(sh_down, shd_h, shd_i, Is, es) && shd_h > 0 &&
+              (H + 16) * shd_h * es < lim;
   }
   switch (dtype) {
     case kBF16: launch_ffn<kBF16>(a, fast_gu, fast_dn, stream); break;

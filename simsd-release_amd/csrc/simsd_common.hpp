@@ -109,36 +109,84 @@ template <> struct Mfma<kF32> {
   }
 };
 
+// ------------------------------------------------- MFMA 4x4x4, 16 blocks
+// v_mfma_f32_4x4x4_16b_{bf16,f16}: 16 independent 4x4x4 products.
+//   A: lane l holds block b = l/4, row i = l%4, its 4 k values
+//   B: lane l holds block b = l/4, col j = l%4, its 4 k values
+//   D: lane l holds block b = l/4, col j = l%4, rows i = 0..3 in 4 registers
+// Used for M <= 8 GEMV: A rows are 4 weight rows, B cols are up to 4 tokens,
+// and the 16 blocks are 16 consecutive 4-element k chunks, so one 16-byte
+// load per lane covers 4 rows x 256 contiguous bytes (two MFMAs' worth).
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+template <int DT> struct Mfma4;
+template <> struct Mfma4<kBF16> {
+  static SIMSD_DEV f32x4_t step(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                  __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma4<kF16> {
+  static SIMSD_DEV f32x4_t step(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4_t, a),
+                                              __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+  }
+};
+
+SIMSD_DEV u32x2_t lo2(u32x4_t v) { return u32x2_t{v.x, v.y}; }
+SIMSD_DEV u32x2_t hi2(u32x4_t v) { return u32x2_t{v.z, v.w}; }
+
 SIMSD_DEV u32x4_t zero4() { return u32x4_t{0u, 0u, 0u, 0u}; }
 
-SIMSD_DEV u32x4_t load16(const char* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+// ------------------------------------------ fast accumulate (buffer loads)
+// Operands are read through buffer resources (one uniform descriptor per A
+// block and one for B) with per-lane 32-bit byte offsets.  An offset at or past
+// the descriptor's extent reads as zero in hardware, which covers the K tail,
+// weight rows past N, activation rows past M and empty slots -- so the loads
+// are unconditional, carry no branches, and the compiler can keep the next
+// batch in flight while the current one feeds the MFMAs.
+// Requirements: 16-byte aligned bases, row strides and row length Kb (bytes)
+// multiples of 16, every extent below kOob.
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef i32x4_t rsrc_t;                       // V# buffer descriptor, 4 dwords
+constexpr uint32_t kOob = 0xFFFFFFF0u;        // never inside a valid extent
+constexpr int kRsrcWord3 = 0x00020000;        // raw 32-bit buffer, gfx9 family
+constexpr int kAuxStream = 2;                 // nt: streamed once, do not keep
+constexpr int kAuxKeep = 0;
 
-// ------------------------------------------------- fast accumulate (16 B loads)
-// Rows are byte pointers to the START of a row; every row must be 16-byte
-// aligned and its length Kb (bytes) a multiple of 16.  A rows are always valid
-// (callers clamp out-of-range rows onto a real row and discard the result);
-// a null B row contributes zeros.  Steps [s0, s1) of 64 bytes are summed.
+// The LLVM intrinsic, bound by name: (descriptor, voffset, soffset, cache bits).
+__device__ i32x4_t simsd_raw_buffer_load_v4i32(i32x4_t rsrc, int32_t voffset, int32_t soffset,
+                                               int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
+SIMSD_DEV rsrc_t make_rsrc(const void* base, uint32_t extent_bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  // word1 high half = stride 0; word3 = raw dword format
+  return rsrc_t{(int32_t)(uint32_t)p, (int32_t)(uint32_t)((p >> 32) & 0xFFFFu),
+                (int32_t)extent_bytes, kRsrcWord3};
+}
+
+template <int AUX>
+SIMSD_DEV u32x4_t buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, simsd_raw_buffer_load_v4i32(r, (int32_t)off, 0, AUX));
+}
+
 template <int RB, int CB, int U>
-SIMSD_DEV void load_batch(u32x4_t (&A)[U][RB], u32x4_t (&B)[U][CB],
-                          const char* const (&arow)[RB], const char* const (&brow)[CB],
-                          int s, int s1, int lane_off, int64_t Kb) {
+SIMSD_DEV void load_batch(u32x4_t (&A)[U][RB], u32x4_t (&B)[U][CB], const rsrc_t (&ra)[RB],
+                          const uint32_t (&aoff)[RB], rsrc_t rb_, const uint32_t (&boff)[CB],
+                          const bool (&bok)[CB], int s, int s1, uint32_t lane_off, uint32_t Kb) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t off = (int64_t)(s + u) * kStepBytes + lane_off;
-    const bool ok = (s + u < s1) && (off < Kb);
-    const int64_t offc = ok ? off : 0;   // row start is always readable
+    const uint32_t k = (uint32_t)(s + u) * kStepBytes + lane_off;
+    const bool ok = (s + u < s1) && (k < Kb);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const u32x4_t v = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4_t*>(arow[rb] + offc));
-      A[u][rb] = ok ? v : zero4();
-    }
+    for (int rb = 0; rb < RB; ++rb)
+      A[u][rb] = buf_load16<kAuxStream>(ra[rb], ok ? aoff[rb] + k : kOob);
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      u32x4_t v = zero4();
-      if (brow[cb] != nullptr && ok) v = load16(brow[cb] + off);
-      B[u][cb] = v;
-    }
+    for (int cb = 0; cb < CB; ++cb)
+      B[u][cb] = buf_load16<kAuxKeep>(rb_, (ok && bok[cb]) ? boff[cb] + k : kOob);
   }
 }
 
@@ -154,24 +202,21 @@ SIMSD_DEV void mfma_batch(const u32x4_t (&A)[U][RB], const u32x4_t (&B)[U][CB],
         acc[rb][cb] = Mfma<DT>::step(A[u][rb], B[u][cb], acc[rb][cb]);
 }
 
-// Double-buffered: the loads of batch i+1 are in flight while batch i feeds
-// the MFMAs.
+// Sums k-steps [s0, s1) (64 bytes of every row each) into acc, U steps per
+// batch: the batch's loads all issue back to back, and each MFMA waits only
+// for its own operands (graduated vmcnt), so the batch streams through.
 template <int DT, int RB, int CB, int U>
-SIMSD_DEV void accum_fast(const char* const (&arow)[RB], const char* const (&brow)[CB],
-                          int s0, int s1, int lane_off, int64_t Kb, f32x4_t (&acc)[RB][CB]) {
-  if (s0 >= s1) return;
-  u32x4_t A0[U][RB], B0[U][CB], A1[U][RB], B1[U][CB];
-  int s = s0;
-  load_batch<RB, CB, U>(A0, B0, arow, brow, s, s1, lane_off, Kb);
-  while (true) {
-    if (s + U >= s1) { mfma_batch<DT, RB, CB, U>(A0, B0, acc); break; }
-    load_batch<RB, CB, U>(A1, B1, arow, brow, s + U, s1, lane_off, Kb);
-    mfma_batch<DT, RB, CB, U>(A0, B0, acc);
-    s += U;
-    if (s + U >= s1) { mfma_batch<DT, RB, CB, U>(A1, B1, acc); break; }
-    load_batch<RB, CB, U>(A0, B0, arow, brow, s + U, s1, lane_off, Kb);
-    mfma_batch<DT, RB, CB, U>(A1, B1, acc);
-    s += U;
+SIMSD_DEV void accum_fast(const rsrc_t (&ra)[RB], const uint32_t (&aoff)[RB], rsrc_t rb_,
+                          const uint32_t (&boff)[CB], const bool (&bok)[CB], int s0, int s1,
+                          uint32_t lane_off, uint32_t Kb, f32x4_t (&acc)[RB][CB]) {
+  for (int s = s0; s < s1; s += U) {
+    u32x4_t A[U][RB], B[U][CB];
+    load_batch<RB, CB, U>(A, B, ra, aoff, rb_, boff, bok, s, s1, lane_off, Kb);
+    // keep every load of the batch ahead of its first MFMA (the scheduler
+    // would otherwise interleave them to save registers and cut the loads
+    // in flight)
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_batch<DT, RB, CB, U>(A, B, acc);
   }
 }
 

@@ -66,21 +66,42 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const char* arow[RB];
-  const char* brow[CB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int64_t n = min(n_tile + rb * RT + (r % RT), a.N - 1);
-    arow[rb] = a.w + n * a.swn * ES;
-  }
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const int64_t m = m_tile + cb * 16 + r;
-    brow[cb] = m < a.M ? a.x + m * a.sxm * ES : nullptr;
-  }
   if (FAST) {
-    accum_fast<DT, RB, CB, U>(arow, brow, w0, w1, g * kLaneBytes, a.K * ES, acc);
+    // One descriptor over this tile's weight rows and one over its activation
+    // rows; rows past N or M fall outside the extents and read as zero.
+    const uint32_t Kb = (uint32_t)(a.K * ES);
+    const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
+    const int64_t rows_valid = min((int64_t)(RT * RB), a.N - n_tile);
+    const int64_t cols_valid = min((int64_t)(CB * 16), a.M - m_tile);
+    const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
+    const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+    rsrc_t ra[RB];
+    uint32_t aoff[RB], boff[CB];
+    bool bok[CB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      ra[rb] = rA;
+      aoff[rb] = (uint32_t)(rb * RT + (r % RT)) * swn_b;
+    }
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      boff[cb] = (uint32_t)(cb * 16 + r) * sxm_b;
+      bok[cb] = cb * 16 + r < cols_valid;
+    }
+    accum_fast<DT, RB, CB, U>(ra, aoff, rB, boff, bok, w0, w1, (uint32_t)(g * kLaneBytes), Kb, acc);
   } else {
+    const char* arow[RB];
+    const char* brow[CB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int64_t n = min(n_tile + rb * RT + (r % RT), a.N - 1);
+      arow[rb] = a.w + n * a.swn * ES;
+    }
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int64_t m = m_tile + cb * 16 + r;
+      brow[cb] = m < a.M ? a.x + m * a.sxm * ES : nullptr;
+    }
     accum_generic<DT, RB, CB>(arow, a.swk * ES, brow, a.sxk * ES, w0, w1, g, a.K, acc);
   }
 
@@ -112,6 +133,133 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// M <= 8 GEMV on v_mfma_f32_4x4x4_16b: the weight is read as 4 rows x 256
+// contiguous bytes per wave instruction (two full cache lines per row), the
+// activation chunk for the wave's K range sits in registers and is reused by
+// every 4-row group, so the inner loop issues weight loads only.
+//   RW  weight rows per workgroup (4..32), G = RW / 4 row groups
+//   MS  column sets of 4 tokens (1: M <= 4, 2: M <= 8)
+//   KS  waves per workgroup splitting K
+//   CH  load steps (128 k elements each) whose activations are held at once
+//   GB  row groups whose loads are issued together
+constexpr int kStep4Bytes = 256;   // bytes of one row per 4x4x4 load step
+
+template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL>
+__global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int G = RW / 4;
+  static_assert(RW % 4 == 0 && G % GB == 0, "row groups");
+  const int lane = threadIdx.x & 63;
+  const int wk = threadIdx.x >> 6;
+  const int i4 = lane & 3;          // A row / B column within a block
+  const int b4 = lane >> 2;         // 4x4x4 block = 8-element k chunk of a load step
+  const int64_t n_tile = (int64_t)blockIdx.x * RW;
+  const int64_t m_tile = (int64_t)blockIdx.z * (4 * MS);
+  const int split_id = blockIdx.y;
+
+  const int s_lo = split_id * a.steps_per_split;
+  const int s_hi = min(a.steps, s_lo + a.steps_per_split);
+  const int span = max(0, s_hi - s_lo);
+  const int per_w = (span + KS - 1) / KS;
+  const int w0 = s_lo + wk * per_w;
+  const int w1 = min(s_hi, w0 + per_w);
+
+  const uint32_t Kb = (uint32_t)(a.K * ES);
+  const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
+  const int64_t rows_valid = min((int64_t)RW, a.N - n_tile);
+  const int64_t cols_valid = min((int64_t)(4 * MS), a.M - m_tile);
+  const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
+  const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+  const uint32_t lane_k = (uint32_t)(b4 * kLaneBytes);
+
+  f32x4_t acc[G][MS];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int c = 0; c < MS; ++c) acc[g][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = w0; c0 < w1; c0 += CH) {
+    // activations of this chunk: lane (j, b) holds token 4c+j, k chunk b
+    u32x4_t B[CH][MS];
+#pragma unroll
+    for (int s = 0; s < CH; ++s) {
+      const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
+      const bool ok = (c0 + s < w1) && (k < Kb);
+#pragma unroll
+      for (int c = 0; c < MS; ++c) {
+        const bool col_ok = 4 * c + i4 < cols_valid;
+        B[s][c] = buf_load16<kAuxKeep>(rB, (ok && col_ok) ? (uint32_t)(4 * c + i4) * sxm_b + k : kOob);
+      }
+    }
+#pragma unroll
+    for (int g0 = 0; g0 < G; g0 += GB) {
+      u32x4_t A[GB][CH];
+#pragma unroll
+      for (int gg = 0; gg < GB; ++gg) {
+        const uint32_t roff = (uint32_t)(4 * (g0 + gg) + i4) * swn_b;
+#pragma unroll
+        for (int s = 0; s < CH; ++s) {
+          const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
+          const bool ok = (c0 + s < w1) && (k < Kb);
+          A[gg][s] = buf_load16<kAuxStream>(rA, ok ? roff + k : kOob);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int gg = 0; gg < GB; ++gg)
+#pragma unroll
+        for (int s = 0; s < CH; ++s)
+#pragma unroll
+          for (int c = 0; c < MS; ++c) {
+            acc[g0 + gg][c] = Mfma4<DT>::step(lo2(A[gg][s]), lo2(B[s][c]), acc[g0 + gg][c]);
+            acc[g0 + gg][c] = Mfma4<DT>::step(hi2(A[gg][s]), hi2(B[s][c]), acc[g0 + gg][c]);
+          }
+    }
+  }
+
+  // sum the 16 k-chunk blocks (lanes with equal j), fixed butterfly order
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int c = 0; c < MS; ++c)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float t = acc[g][c][v];
+        t += __shfl_xor(t, 4);
+        t += __shfl_xor(t, 8);
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        acc[g][c][v] = t;
+      }
+  // then the KS waves, in wave order, through LDS: red[wave][g][c][row i][col j]
+  __shared__ float red[KS * G * MS * 16];
+  if (lane < 4) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int c = 0; c < MS; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wk * G + g) * MS + c) * 16 + v * 4 + lane] = acc[g][c][v];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * MS * 16; e += 64 * KS) {
+    const int j = e & 3, v = (e >> 2) & 3, c = (e >> 4) % MS, g = (e >> 4) / MS;
+    const int64_t n = n_tile + 4 * g + v;
+    const int64_t m = m_tile + 4 * c + j;
+    if (n < a.N && m < a.M) {
+      float t = 0.f;
+      for (int w = 0; w < KS; ++w) t += red[((w * G + g) * MS + c) * 16 + v * 4 + j];
+      if (PARTIAL) {
+        a.part[((int64_t)split_id * a.M + m) * a.N + n] = t;
+      } else {
+        if (a.bias != nullptr) t += load_elem<DT>(a.bias, n * a.sb);
+        store_elem<DT>(a.y, m * a.sym + n * a.syn, t);
+      }
+    }
+  }
+}
+
 // Sum the split partials in split order (fixed: bit-reproducible), add bias,
 // round to the output dtype.  One thread per output element.
 template <int DT>
@@ -131,8 +279,11 @@ __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restric
 // ------------------------------------------------------------------ host side
 namespace {
 
+// kind 0: thin_gemm_kernel (16x16x32 MFMA; any M, fp32, strided views)
+// kind 1: thin_gemv4_kernel (4x4x4 MFMA; M <= 8, bf16/fp16, vector-capable)
 struct ThinPlan {
-  int rows, rt, rb, cb, ks, split;
+  int kind;
+  int rows, rt, rb, cb, ms, ks, split;
   bool fast;
   int64_t tiles_n, tiles_m;
   int steps, steps_per_split;
@@ -146,14 +297,19 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kMinWorkgroups = 256;   // one per CU on MI355X
 constexpr int kMaxSplit = 16;
 
+inline int gemv4_kind(int64_t M, int dtype) { return (M <= 8 && dtype != kF32) ? 1 : 0; }
+
 // Geometry only (no pointers).  block_n = weight rows per workgroup (0 = the
-// fewest of 16, 8, 4 that still gives every CU a workgroup); split along K
-// only when even 4-row tiles leave CUs idle (0 = automatic).
-int plan_geometry(ThinPlan& pl, int64_t M, int64_t N, int64_t K, int dtype, int block_n,
+// most of 16, 8, 4 that still gives every CU a workgroup); split along K only
+// when even 4-row tiles leave more than half the CUs idle (0 = automatic),
+// keeping at least 256 bytes of every row per wave and split.
+int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int dtype, int block_n,
                   int num_waves, int split_k) {
   const int es = esize_of(dtype);
+  pl.kind = kind;
   pl.cb = M <= 16 ? 1 : 2;
-  pl.tiles_m = cdiv(M, 16 * pl.cb);
+  pl.ms = M <= 4 ? 1 : 2;
+  pl.tiles_m = kind == 1 ? cdiv(M, 4 * pl.ms) : cdiv(M, 16 * pl.cb);
   pl.ks = num_waves <= 0 ? 4 : num_waves;
   if (pl.ks != 2 && pl.ks != 4 && pl.ks != 8)
     return set_error("thin_linear: num_waves must be 2, 4 or 8 (got %d)", num_waves);
@@ -170,14 +326,15 @@ int plan_geometry(ThinPlan& pl, int64_t M, int64_t N, int64_t K, int dtype, int 
   pl.rt = rows >= 16 ? 16 : rows;
   pl.rb = rows >= 16 ? rows / 16 : 1;
   pl.tiles_n = cdiv(N, rows);
-  pl.steps = (int)cdiv(K * es, kStepBytes);
+  pl.steps = (int)cdiv(K * es, kind == 1 ? kStep4Bytes : kStepBytes);
   int split = split_k;
   if (split <= 0) {
     const int64_t wgs = pl.tiles_n * pl.tiles_m;
     split = 1;
     if (wgs < kMinWorkgroups / 2) {
       split = (int)cdiv(kMinWorkgroups, wgs);
-      split = max(1, min(split, min(kMaxSplit, pl.steps / (pl.ks * 4))));
+      const int64_t max_by_k = (K * es) / (kStep4Bytes * (int64_t)pl.ks);
+      split = (int)max((int64_t)1, min((int64_t)min(split, kMaxSplit), max_by_k));
     }
   }
   if (split > 1024) return set_error("thin_linear: split_k=%d exceeds 1024", split);
@@ -194,53 +351,96 @@ int make_plan(ThinPlan& pl, const void* x, int64_t sxm, int64_t sxk, const void*
   const bool w_vec = swk == 1 && aligned16(w) && ((swn * es) % 16 == 0 || N == 1) &&
                      (K * es) % 16 == 0;
   const bool x_vec = sxk == 1 && aligned16(x) && ((sxm * es) % 16 == 0 || M == 1);
-  pl.fast = w_vec && x_vec;
+  // buffer descriptors address a tile with 32-bit offsets (a single row's
+  // stride is never used)
+  const int64_t w_extent = (N > 1 ? 31 * swn * es : 0) + K * es;
+  const int64_t x_extent = (M > 1 ? 31 * sxm * es : 0) + K * es;
+  const bool fast = w_vec && x_vec && (N == 1 || swn > 0) && (M == 1 || sxm > 0) &&
+                    w_extent < (int64_t)kOob && x_extent < (int64_t)kOob;
   // The strided path has one shape: 16 rows per workgroup, 4 waves.
-  if (plan_geometry(pl, M, N, K, dtype, pl.fast ? block_n : 16, pl.fast ? num_waves : 4,
-                    split_k) != 0)
+  if (plan_geometry(pl, fast ? gemv4_kind(M, dtype) : 0, M, N, K, dtype, fast ? block_n : 16,
+                    fast ? num_waves : 4, split_k) != 0)
     return -1;
+  pl.fast = fast;
   return 0;
 }
 
-template <int DT, int RT, int RB, int CB, int KS, bool FAST>
-void launch_main(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  constexpr int U = (RB * CB == 1) ? SIMSD_THIN_U : SIMSD_THIN_U / 2;
+template <bool PARTIAL, typename Kern>
+void launch(Kern k, const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   dim3 grid((unsigned)pl.tiles_n, (unsigned)pl.split, (unsigned)pl.tiles_m);
-  if (pl.split > 1)
-    hipLaunchKernelGGL((thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, true>), grid, dim3(64 * KS),
-                       0, stream, args);
-  else
-    hipLaunchKernelGGL((thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, false>), grid, dim3(64 * KS),
-                       0, stream, args);
+  hipLaunchKernelGGL(k, grid, dim3(64 * pl.ks), 0, stream, args);
+}
+
+template <int DT, int RT, int RB, int CB, int KS, bool FAST>
+void launch_gemm(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  constexpr int U = (RB * CB == 1) ? SIMSD_THIN_U : SIMSD_THIN_U / 2;
+  if (pl.split > 1) launch<true>(thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, true>, pl, args, stream);
+  else launch<false>(thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, false>, pl, args, stream);
 }
 
 template <int DT, int RT, int RB, int CB>
-void dispatch_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+void gemm_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.ks) {
-    case 2: launch_main<DT, RT, RB, CB, 2, true>(pl, args, stream); break;
-    case 8: launch_main<DT, RT, RB, CB, 8, true>(pl, args, stream); break;
-    default: launch_main<DT, RT, RB, CB, 4, true>(pl, args, stream); break;
+    case 2: launch_gemm<DT, RT, RB, CB, 2, true>(pl, args, stream); break;
+    case 8: launch_gemm<DT, RT, RB, CB, 8, true>(pl, args, stream); break;
+    default: launch_gemm<DT, RT, RB, CB, 4, true>(pl, args, stream); break;
   }
 }
 
 template <int DT, int CB>
-void dispatch_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+void gemm_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   if (!pl.fast) {   // strided path: one shape, 16 rows, 4 waves
-    launch_main<DT, 16, 1, CB, 4, false>(pl, args, stream);
+    launch_gemm<DT, 16, 1, CB, 4, false>(pl, args, stream);
     return;
   }
   switch (pl.rows) {
-    case 4: dispatch_ks<DT, 4, 1, CB>(pl, args, stream); break;
-    case 8: dispatch_ks<DT, 8, 1, CB>(pl, args, stream); break;
-    case 32: dispatch_ks<DT, 16, 2, CB>(pl, args, stream); break;
-    default: dispatch_ks<DT, 16, 1, CB>(pl, args, stream); break;
+    case 4: gemm_ks<DT, 4, 1, CB>(pl, args, stream); break;
+    case 8: gemm_ks<DT, 8, 1, CB>(pl, args, stream); break;
+    case 32: gemm_ks<DT, 16, 2, CB>(pl, args, stream); break;
+    default: gemm_ks<DT, 16, 1, CB>(pl, args, stream); break;
+  }
+}
+
+constexpr int kChunk4 = 8;   // load steps of activations held per chunk (1024 k)
+
+template <int DT, int RW, int MS, int KS>
+void launch_gemv4(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  constexpr int GB = RW >= 8 ? 2 : 1;
+  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, kChunk4, GB, true>, pl, args, stream);
+  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, kChunk4, GB, false>, pl, args, stream);
+}
+
+template <int DT, int RW, int MS>
+void gemv4_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  switch (pl.ks) {
+    case 2: launch_gemv4<DT, RW, MS, 2>(pl, args, stream); break;
+    case 8: launch_gemv4<DT, RW, MS, 8>(pl, args, stream); break;
+    default: launch_gemv4<DT, RW, MS, 4>(pl, args, stream); break;
+  }
+}
+
+template <int DT, int MS>
+void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  switch (pl.rows) {
+    case 4: gemv4_ks<DT, 4, MS>(pl, args, stream); break;
+    case 8: gemv4_ks<DT, 8, MS>(pl, args, stream); break;
+    case 32: gemv4_ks<DT, 32, MS>(pl, args, stream); break;
+    default: gemv4_ks<DT, 16, MS>(pl, args, stream); break;
   }
 }
 
 template <int DT>
 void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  if (pl.cb == 1) dispatch_rows<DT, 1>(pl, args, stream);
-  else dispatch_rows<DT, 2>(pl, args, stream);
+  if constexpr (DT != kF32) {
+    if (pl.kind == 1) {
+      if (pl.ms == 1) gemv4_rows<DT, 1>(pl, args, stream);
+      else gemv4_rows<DT, 2>(pl, args, stream);
+    }
+  }
+  if (pl.kind == 0) {
+    if (pl.cb == 1) gemm_rows<DT, 1>(pl, args, stream);
+    else gemm_rows<DT, 2>(pl, args, stream);
+  }
   if (pl.split > 1) {
     const int64_t total = args.M * args.N;
     hipLaunchKernelGGL((thin_reduce_kernel<DT>), dim3((unsigned)cdiv(total, 256)), dim3(256), 0,
@@ -256,12 +456,15 @@ using namespace simsd;
 
 extern "C" int64_t simsd_thin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype,
                                                      int block_n, int split_k, int num_waves) {
-  // Enough for either path: the requested geometry (vector-capable operands)
-  // and the strided one (16 rows, 4 waves).
-  ThinPlan a{}, b{};
-  if (plan_geometry(a, M, N, K, dtype, block_n, num_waves, split_k) != 0) return -1;
-  if (plan_geometry(b, M, N, K, dtype, 16, 4, split_k) != 0) return -1;
-  return a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes;
+  // Enough for any path the call may take: either kernel with the requested
+  // geometry, or the strided one (16 rows, 4 waves).
+  ThinPlan a{}, b{}, c{};
+  if (plan_geometry(a, 0, M, N, K, dtype, block_n, num_waves, split_k) != 0) return -1;
+  if (plan_geometry(b, 0, M, N, K, dtype, 16, 4, split_k) != 0) return -1;
+  if (plan_geometry(c, gemv4_kind(M, dtype), M, N, K, dtype, block_n, num_waves, split_k) != 0)
+    return -1;
+  int64_t need = a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes;
+  return need > c.part_bytes ? need : c.part_bytes;
 }
 
 extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const void* w,
@@ -313,11 +516,12 @@ extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const 
 extern "C" int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype, int block_n,
                                       int split_k, int num_waves, int* out4) {
   // (rows per workgroup, columns per block, waves per workgroup, split) of the
-  // vector-path geometry; lets the Python side report the config it runs.
+  // geometry a vector-capable call takes; lets the Python side report it.
   ThinPlan pl{};
-  if (plan_geometry(pl, M, N, K, dtype, block_n, num_waves, split_k) != 0) return -1;
+  if (plan_geometry(pl, gemv4_kind(M, dtype), M, N, K, dtype, block_n, num_waves, split_k) != 0)
+    return -1;
   out4[0] = pl.rows;
-  out4[1] = 16 * pl.cb;
+  out4[1] = pl.kind == 1 ? 4 * pl.ms : 16 * pl.cb;
   out4[2] = pl.ks;
   out4[3] = pl.split;
   return 0;

@@ -8,28 +8,39 @@ argument meaning and the same exceptions.  The arithmetic runs in a
 hand-written gfx950 HIP kernel (``libsimsd_kernels.so``, C ABI in
 ``include/simsd_kernels.h``) instead of Triton.
 
-How the MI355X kernel works (``csrc/thin_gemm.hip``)
-----------------------------------------------------
+How the MI355X kernels work (``csrc/thin_gemm.hip``)
+-----------------------------------------------------
 At M <= 32 the op is a stream over the weight: arithmetic intensity is at most
-~32 flop/byte against a ~312 flop/byte ridge, so HBM bandwidth is the bound.
-Each wave streams 16 weight rows with 128-bit loads straight into the A
-operand of ``v_mfma_f32_16x16x32_bf16`` while the M activation rows are the B
-operand (masked lanes below 16 rows, a second column block up to 32 rows).
-MFMA does the fp32-accumulate arithmetic for free relative to the byte rate,
-which leaves the VALU idle and keeps the loads in flight.  A workgroup owns 4,
-8, 16 or 32 weight rows and splits K over its waves, which sum their fp32
-partials in LDS in fixed order; narrow N uses fewer rows per workgroup (the
-MFMA rows repeat) so every CU still gets work without a cross-workgroup
-reduction.  An explicit SPLIT_K > 1 splits K over workgroups too: fp32 partial
-tiles, then a second launch sums them in split order.
+~32 flop/byte against a ~312 flop/byte ridge, so HBM bandwidth is the bound,
+and what matters is reading the weight once, in full cache lines, with enough
+loads in flight.  All weight and activation reads go through buffer
+descriptors whose hardware range check returns zeros past the tile, so the
+load stream carries no branches.
+
+* M <= 8 (bf16/fp16): ``v_mfma_f32_4x4x4_16b`` runs 16 independent 4x4x4
+  products per instruction.  Lanes map to (weight row l%4, k chunk l/4), so
+  one 16-byte load per lane covers 4 weight rows x 256 contiguous bytes, and
+  the 4 output columns are the (up to 4) tokens -- nothing is padded.  The
+  activations of a wave's K range sit in registers and serve every 4-row
+  group, so the inner loop issues weight loads only.
+* otherwise (M up to 32 per block, fp32, strided views):
+  ``v_mfma_f32_16x16x32_bf16`` with 16 weight rows as the A operand and up to
+  16 tokens as the B operand per block.
+
+A workgroup owns 4, 8, 16 or 32 weight rows and splits K over its waves,
+which sum their fp32 partials in fixed order; narrow N uses fewer rows per
+workgroup so every CU still gets work without a cross-workgroup reduction.  An
+explicit SPLIT_K > 1 splits K over workgroups too: fp32 partial tiles, then a
+second launch sums them in split order.
 
 Config tuples keep the reference's shape ``(BLOCK_M, BLOCK_N, BLOCK_K,
-SPLIT_K[, num_warps, num_stages])`` but describe the MI355X kernel:
-BLOCK_M is the activation-row envelope (16, or 32 with two column blocks),
+SPLIT_K[, num_warps, num_stages])`` and describe the MI355X kernels:
+BLOCK_M is the token envelope (``TUNED``: dispatch for M up to 16 or 32) or
+column-block width (heuristic: 4 or 8 for the GEMV, 16 or 32 otherwise),
 BLOCK_N the weight rows per workgroup (4, 8, 16 or 32; other values round down
-to one of these), BLOCK_K the K elements one wave streams per pipeline stage,
-SPLIT_K the workgroups along K, num_warps the waves per workgroup (2, 4 or 8)
-and num_stages the register double-buffer depth (always 2).
+to one of these), BLOCK_K the K elements of activations a wave holds at once,
+SPLIT_K the workgroups along K, num_warps the waves per workgroup (2, 4 or 8);
+num_stages is accepted and ignored.
 
 Contract (reference CONTRACT, kernels/workspace/thin_linear/CONTRACT.md:26-91):
 forward only; fp32 accumulation for bf16/fp16/fp32 inputs; deterministic
@@ -46,12 +57,10 @@ from . import _native
 # Tuning knobs (kernels/thin_linear_fused.py:59-61).  MI355X has 256 CUs.
 TARGET_CTAS = 256              # at least one workgroup on every CU
 MAX_SPLIT_K = 16
-MIN_K_PER_SPLIT = 512          # bf16 elements; a split is at least 4 k-steps per wave
+MIN_K_PER_SPLIT = 512          # bf16 elements of every row per split (256 B per wave)
 _ROWS = (4, 8, 16, 32)         # weight rows per workgroup the kernel is built for
 
-_STEP_BYTES = 64               # bytes of a weight row one MFMA k-step consumes
 _DEFAULT_WAVES = 4
-_STAGES = 2
 
 
 def _next_pow2(n: int) -> int:
@@ -98,13 +107,13 @@ def reset_workspace() -> None:
 # gate/up, k/v and lm_head of the target) follow the nearest swept shape.
 TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     # SDAR-1.7B draft projections (hidden 2048, 16 q / 8 kv heads, inter 6144)
-    (2048, 2048): (16, 8, 256, 1, 4, 2),      # q_proj, o_proj      5.3 us
-    (2048, 1024): (16, 8, 256, 1, 8, 2),      # k_proj, v_proj      5.2 us
-    (2048, 6144): (16, 16, 256, 1, 2, 2),     # gate_proj, up_proj
-    (6144, 2048): (16, 8, 256, 1, 8, 2),      # down_proj          11.0 us
-    (2048, 151936): (16, 16, 256, 1, 2, 2),   # lm_head
-    (2048, 4096): (16, 16, 256, 1, 4, 2),     # merged qkv          5.9 us
-    (2048, 12288): (16, 16, 256, 1, 2, 2),    # merged gate+up     12.3 us
+    (2048, 2048): (16, 8, 1024, 1, 2, 2),     # q_proj, o_proj      4.3 us
+    (2048, 1024): (16, 4, 1024, 1, 2, 2),     # k_proj, v_proj      3.5 us
+    (2048, 6144): (16, 8, 1024, 1, 2, 2),     # gate_proj, up_proj
+    (6144, 2048): (16, 8, 1024, 1, 8, 2),     # down_proj           7.5 us
+    (2048, 151936): (16, 8, 1024, 1, 2, 2),   # lm_head
+    (2048, 4096): (16, 8, 1024, 1, 2, 2),     # merged qkv          5.7 us
+    (2048, 12288): (16, 8, 1024, 1, 2, 2),    # merged gate+up     11.7 us
     # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
     (4096, 12288): (32, 32, 128, 1, 2, 2),    # gate_proj / up_proj
     (4096, 4096): (32, 16, 128, 1, 4, 2),     # q_proj, o_proj     12.0 / 16.0 us (M=16 / 32)
@@ -145,8 +154,11 @@ def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, i
     every CU a workgroup; a split along K only when even 4-row tiles leave
     more than half the CUs idle.
     """
-    BLOCK_M = 16 if M <= 16 else 32
-    BLOCK_K = (256 if BLOCK_M == 16 else 128) * 2 // itemsize
+    if itemsize == 2 and M <= 8:        # 4x4x4 GEMV: 4 tokens per column set
+        BLOCK_M, BLOCK_K = (4 if M <= 4 else 8), 1024
+    else:                               # 16x16 MFMA tiles
+        BLOCK_M = 16 if M <= 16 else 32
+        BLOCK_K = (256 if BLOCK_M == 16 else 128) * 2 // itemsize
     m_tiles = _cdiv(M, BLOCK_M)
     BLOCK_N = 4
     for cand in (16, 8):
@@ -156,9 +168,8 @@ def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, i
     tiles = _cdiv(N, BLOCK_N) * m_tiles
     split = 1
     if tiles < TARGET_CTAS // 2:
-        steps = _cdiv(K * itemsize, _STEP_BYTES)
         split = _cdiv(TARGET_CTAS, tiles)
-        split = max(1, min(split, MAX_SPLIT_K, steps // (MIN_K_PER_SPLIT * 2 // _STEP_BYTES)))
+        split = max(1, min(split, MAX_SPLIT_K, (K * itemsize) // (MIN_K_PER_SPLIT * 2)))
     return BLOCK_M, BLOCK_N, BLOCK_K, split
 
 

@@ -78,7 +78,8 @@ def test_header_links_from_plain_c(tmp_path):
                    f"-L{libdir} -lsimsd_kernels -Wl,-rpath,{libdir}")
     assert rc == 0
     assert os.system(f"{exe} > {tmp_path}/out.txt") == 0
-    assert open(f"{tmp_path}/out.txt").read().split() == ["16", "16", "4", "1"]
+    # 16 weight rows per workgroup, the 4-token GEMV column block, 4 waves, no split
+    assert open(f"{tmp_path}/out.txt").read().split() == ["16", "4", "4", "1"]
 
 
 @pytest.mark.parametrize("M,N,K", [(4, 2048, 2048), (4, 1024, 2048), (4, 12288, 2048),

@@ -342,8 +342,11 @@ def test_properties_at_full_size():
             w = rnd(N, K, scale=0.02, seed=300 + M)
             y = thin_linear(x, w)
             assert torch.equal(thin_linear(x, w), y)                         # deterministic
-            rows = torch.cat([thin_linear(x[i:i + 1], w) for i in range(M)])
-            assert torch.equal(rows, y)                                       # row independence
+            perm = torch.randperm(M, generator=torch.Generator().manual_seed(M))
+            assert torch.equal(thin_linear(x[perm], w), y[perm])              # rows independent
+            if M <= 4:   # one token or four: the same GEMV kernel and column set
+                rows = torch.cat([thin_linear(x[i:i + 1], w) for i in range(M)])
+                assert torch.equal(rows, y)
             assert torch.equal(thin_linear(x * 4, w), y * 4)                  # exact 2^k scaling
             wt = torch.empty(N, K + 64, device=DEV, dtype=w.dtype)
             wt[:, 32:32 + K] = w
