@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 1
+#define SIMSD_ABI_VERSION 2
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -48,6 +48,8 @@ const char* simsd_last_error_string(void);
  *   strides are in elements; any stride works (non-unit K strides and
  *   unaligned rows take a slower element-wise path);
  *   block_n: weight rows per workgroup (4, 8, 16 or 32; 0 = automatic);
+ *   block_k: k elements of activations a wave holds at once in the M <= 8
+ *            bf16/fp16 kernel (256 or 1024; 0 = 256; other kernels ignore it);
  *   split_k: workgroups along K (0 = automatic); with split_k > 1 fp32
  *            partial tiles go to the workspace and a second launch sums them
  *            in split order (deterministic);
@@ -62,7 +64,7 @@ int simsd_thin_linear(const void* x, int64_t stride_xm, int64_t stride_xk,
                       const void* bias, int64_t stride_b,
                       void* y, int64_t stride_ym, int64_t stride_yn,
                       int64_t M, int64_t N, int64_t K, int dtype,
-                      int block_n, int split_k, int num_waves,
+                      int block_n, int block_k, int split_k, int num_waves,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Workspace bytes simsd_thin_linear needs for this shape/config (0 if none).

@@ -1,26 +1,28 @@
 // Skinny GEMM y[M,N] = x[M,K] . w[N,K]^T (+ bias) for gfx950.
 //
 // Replaces the Triton _thin_gemv_kernel / _thin_gemv_reduce pair of
-// kernels/thin_linear_fused.py:67-171 (reference).  Design for MI355X:
-//   * the weight streams straight from HBM into MFMA A operands with 128-bit
-//     non-temporal loads, 64 B of every row per wave per k-step,
-//     double-buffered in registers;
-//   * the few activation rows are the MFMA B operand (16 columns per block,
-//     masked lanes below 16 rows), read through L1/L2 where they stay resident;
-//   * a workgroup owns ROWS weight rows (4, 8, 16 or 32) and splits K across
-//     KS waves whose fp32 partials meet in LDS in fixed wave order.  Below 16
-//     rows the 16 MFMA A rows repeat the tile's rows (duplicates are loaded
-//     from the same cache lines and their outputs dropped), which buys
-//     workgroups for narrow N without any cross-workgroup reduction;
-//   * an explicit split along K (SPLIT > 1) writes fp32 partial tiles and a
-//     second launch sums them in split order: deterministic, no atomics, no
-//     cross-workgroup synchronisation inside a launch.
+// kernels/thin_linear_fused.py:67-171 (reference).  The op streams the weight
+// once from HBM; three kernels cover the token counts:
+//   * thin_gemv4_kernel (M <= 8, bf16/fp16): v_mfma_f32_4x4x4_16b with the
+//     tokens as the 4 output columns, weight read as 4 rows x 256 contiguous
+//     bytes per instruction, activations held in registers;
+//   * thin_gemm_lds_kernel (M > 8, bf16/fp16): v_mfma_f32_16x16x32 with the
+//     same weight access, the tile re-laid out through LDS into the MFMA A
+//     operand;
+//   * thin_gemm_kernel (fp32, strided or unaligned views): 16x16 MFMA with
+//     the operands loaded directly in MFMA layout (below 16 rows per
+//     workgroup the A rows repeat and the duplicates' outputs are dropped).
+// A workgroup owns 4..32 weight rows and splits K across its waves, whose fp32
+// partials meet in LDS in fixed wave order.  An explicit split along K
+// (SPLIT > 1) writes fp32 partial tiles and a second launch sums them in split
+// order: deterministic, no atomics, no cross-workgroup synchronisation.
 #include "simsd_common.hpp"
 #include "simsd_kernels.h"
 
 #ifndef SIMSD_THIN_U
-#define SIMSD_THIN_U 8   // k-steps per pipeline stage at one A and one B block
+#define SIMSD_THIN_U 8   // k-steps per batch at one A and one B block
 #endif
+
 
 namespace simsd {
 
@@ -180,12 +182,13 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
     for (int c = 0; c < MS; ++c) acc[g][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int c0 = w0; c0 < w1; c0 += CH) {
+    const int c_lim = min(w1, c0 + CH);
     // activations of this chunk: lane (j, b) holds token 4c+j, k chunk b
     u32x4_t B[CH][MS];
 #pragma unroll
     for (int s = 0; s < CH; ++s) {
       const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
-      const bool ok = (c0 + s < w1) && (k < Kb);
+      const bool ok = (c0 + s < c_lim) && (k < Kb);
 #pragma unroll
       for (int c = 0; c < MS; ++c) {
         const bool col_ok = 4 * c + i4 < cols_valid;
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
 #pragma unroll
         for (int s = 0; s < CH; ++s) {
           const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
-          const bool ok = (c0 + s < w1) && (k < Kb);
+          const bool ok = (c0 + s < c_lim) && (k < Kb);
           A[gg][s] = buf_load16<kAuxStream>(rA, ok ? roff + k : kOob);
         }
       }
@@ -260,6 +263,126 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 9..32 tokens: v_mfma_f32_16x16x32 fed from contiguous weight loads.  Each
+// wave loads its 16*RB rows as 4 rows x 256 contiguous bytes per instruction
+// (the GEMV's access pattern), writes the 16*RB x 256 B tile to its own LDS
+// region (row stride 272 B: conflict-free both ways) and reads it back in the
+// MFMA A layout, 4 k-steps per tile.  Activations are the B operand as in
+// thin_gemm_kernel.
+constexpr int kLdsRow = kStep4Bytes + 16;   // padded LDS row of a 256 B weight chunk
+
+template <int DT, int RB, int CB, int KS, int U, bool PARTIAL>
+__global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int NF = RB * CB;
+  constexpr int ROWS = 16 * RB;
+  __shared__ __attribute__((aligned(16))) char tile[KS][ROWS * kLdsRow];
+  const int lane = threadIdx.x & 63;
+  const int wk = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int64_t n_tile = (int64_t)blockIdx.x * ROWS;
+  const int64_t m_tile = (int64_t)blockIdx.z * (CB * 16);
+  const int split_id = blockIdx.y;
+
+  // chunks of 256 B per row (4 MFMA k-steps) of this workgroup, then of this wave
+  const int s_lo = split_id * a.steps_per_split;
+  const int s_hi = min(a.steps, s_lo + a.steps_per_split);
+  const int span = max(0, s_hi - s_lo);
+  const int per_w = (span + KS - 1) / KS;
+  const int w0 = s_lo + wk * per_w;
+  const int w1 = min(s_hi, w0 + per_w);
+
+  const uint32_t Kb = (uint32_t)(a.K * ES);
+  const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
+  const int64_t rows_valid = min((int64_t)ROWS, a.N - n_tile);
+  const int64_t cols_valid = min((int64_t)(CB * 16), a.M - m_tile);
+  const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
+  const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+  char* my = tile[wk];
+  // loader lanes: row (l / 16) of a 4-row group, 16-byte chunk (l % 16)
+  const int lr = lane >> 4, lc = lane & 15;
+
+  f32x4_t acc[RB][CB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // U chunks per batch: all their loads are issued before the first LDS
+  // write, so a wave keeps U * (16*RB + 16*CB) * 256 B in flight.  Chunks past
+  // the wave's range read as zero (they belong to another wave).
+  for (int c = w0; c < w1; c += U) {
+    u32x4_t W[U][4 * RB], B[U][4][CB];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = c + u < w1;
+      const uint32_t kc = (uint32_t)(c + u) * kStep4Bytes;
+#pragma unroll
+      for (int q = 0; q < 4 * RB; ++q) {
+        const uint32_t k = kc + lc * kLaneBytes;
+        W[u][q] = buf_load16<kAuxStream>(rA, live && k < Kb ? (uint32_t)(4 * q + lr) * swn_b + k : kOob);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const uint32_t k = kc + j * kStepBytes + g * kLaneBytes;
+          const bool ok = live && k < Kb && cb * 16 + r < cols_valid;
+          B[u][j][cb] = buf_load16<kAuxKeep>(rB, ok ? (uint32_t)(cb * 16 + r) * sxm_b + k : kOob);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // a wave's LDS accesses complete in order: the reads below see these
+      // writes, and the next chunk's writes follow these reads
+#pragma unroll
+      for (int q = 0; q < 4 * RB; ++q)
+        *reinterpret_cast<u32x4_t*>(my + (4 * q + lr) * kLdsRow + lc * kLaneBytes) = W[u][q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x4_t A[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          A[rb] = *reinterpret_cast<const u32x4_t*>(my + (16 * rb + r) * kLdsRow + j * kStepBytes +
+                                                    g * kLaneBytes);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb)
+            acc[rb][cb] = Mfma<DT>::step(A[rb], B[u][j][cb], acc[rb][cb]);
+      }
+    }
+  }
+
+  __shared__ float red[KS > 1 ? (KS - 1) * NF * 4 * 64 : 1];
+  reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, red);
+  if (wk != 0) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int64_t m = m_tile + cb * 16 + r;
+      const int64_t nb = n_tile + rb * 16 + 4 * g;
+      if (m < a.M) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t n = nb + j;
+          if (n < a.N) {
+            float v = acc[rb][cb][j];
+            if (PARTIAL) {
+              a.part[((int64_t)split_id * a.M + m) * a.N + n] = v;
+            } else {
+              if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+              store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
+            }
+          }
+        }
+      }
+    }
+}
+
 // Sum the split partials in split order (fixed: bit-reproducible), add bias,
 // round to the output dtype.  One thread per output element.
 template <int DT>
@@ -279,11 +402,12 @@ __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restric
 // ------------------------------------------------------------------ host side
 namespace {
 
-// kind 0: thin_gemm_kernel (16x16x32 MFMA; any M, fp32, strided views)
+// kind 0: thin_gemm_kernel (16x16 MFMA; fp32 and strided views)
 // kind 1: thin_gemv4_kernel (4x4x4 MFMA; M <= 8, bf16/fp16, vector-capable)
+// kind 2: thin_gemm_lds_kernel (16x16x32 MFMA via LDS; M > 8, bf16/fp16, vector-capable)
 struct ThinPlan {
   int kind;
-  int rows, rt, rb, cb, ms, ks, split;
+  int rows, rt, rb, cb, ms, ks, ch, split;
   bool fast;
   int64_t tiles_n, tiles_m;
   int steps, steps_per_split;
@@ -297,16 +421,18 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kMinWorkgroups = 256;   // one per CU on MI355X
 constexpr int kMaxSplit = 16;
 
-inline int gemv4_kind(int64_t M, int dtype) { return (M <= 8 && dtype != kF32) ? 1 : 0; }
+inline int fast_kind(int64_t M, int dtype) { return dtype == kF32 ? 0 : (M <= 8 ? 1 : 2); }
 
 // Geometry only (no pointers).  block_n = weight rows per workgroup (0 = the
 // most of 16, 8, 4 that still gives every CU a workgroup); split along K only
 // when even 4-row tiles leave more than half the CUs idle (0 = automatic),
 // keeping at least 256 bytes of every row per wave and split.
 int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int dtype, int block_n,
-                  int num_waves, int split_k) {
+                  int block_k, int num_waves, int split_k) {
   const int es = esize_of(dtype);
   pl.kind = kind;
+  // GEMV activations held per chunk: 256 (2 load steps) or 1024 (8) k elements
+  pl.ch = block_k >= 512 ? 8 : 2;
   pl.cb = M <= 16 ? 1 : 2;
   pl.ms = M <= 4 ? 1 : 2;
   pl.tiles_m = kind == 1 ? cdiv(M, 4 * pl.ms) : cdiv(M, 16 * pl.cb);
@@ -322,11 +448,13 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
   }
   if (rows != 4 && rows != 8 && rows != 16 && rows != 32)
     return set_error("thin_linear: block_n must be 4, 8, 16 or 32 (got %d)", block_n);
+  if (kind == 2 && rows < 16) rows = 16;   // whole 16-row MFMA blocks
+  if (kind == 2 && pl.ks > 4) pl.ks = 4;   // per-wave LDS tiles
   pl.rows = rows;
   pl.rt = rows >= 16 ? 16 : rows;
   pl.rb = rows >= 16 ? rows / 16 : 1;
   pl.tiles_n = cdiv(N, rows);
-  pl.steps = (int)cdiv(K * es, kind == 1 ? kStep4Bytes : kStepBytes);
+  pl.steps = (int)cdiv(K * es, kind == 0 ? kStepBytes : kStep4Bytes);
   int split = split_k;
   if (split <= 0) {
     const int64_t wgs = pl.tiles_n * pl.tiles_m;
@@ -345,8 +473,8 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
 }
 
 int make_plan(ThinPlan& pl, const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn,
-              int64_t swk, int64_t M, int64_t N, int64_t K, int dtype, int block_n, int split_k,
-              int num_waves) {
+              int64_t swk, int64_t M, int64_t N, int64_t K, int dtype, int block_n, int block_k,
+              int split_k, int num_waves) {
   const int es = esize_of(dtype);
   const bool w_vec = swk == 1 && aligned16(w) && ((swn * es) % 16 == 0 || N == 1) &&
                      (K * es) % 16 == 0;
@@ -358,8 +486,8 @@ int make_plan(ThinPlan& pl, const void* x, int64_t sxm, int64_t sxk, const void*
   const bool fast = w_vec && x_vec && (N == 1 || swn > 0) && (M == 1 || sxm > 0) &&
                     w_extent < (int64_t)kOob && x_extent < (int64_t)kOob;
   // The strided path has one shape: 16 rows per workgroup, 4 waves.
-  if (plan_geometry(pl, fast ? gemv4_kind(M, dtype) : 0, M, N, K, dtype, fast ? block_n : 16,
-                    fast ? num_waves : 4, split_k) != 0)
+  if (plan_geometry(pl, fast ? fast_kind(M, dtype) : 0, M, N, K, dtype, fast ? block_n : 16,
+                    block_k, fast ? num_waves : 4, split_k) != 0)
     return -1;
   pl.fast = fast;
   return 0;
@@ -401,13 +529,17 @@ void gemm_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   }
 }
 
-constexpr int kChunk4 = 8;   // load steps of activations held per chunk (1024 k)
+template <int DT, int RW, int MS, int KS, int CH>
+void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  constexpr int GB = RW >= 8 ? 2 : 1;
+  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true>, pl, args, stream);
+  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false>, pl, args, stream);
+}
 
 template <int DT, int RW, int MS, int KS>
 void launch_gemv4(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  constexpr int GB = RW >= 8 ? 2 : 1;
-  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, kChunk4, GB, true>, pl, args, stream);
-  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, kChunk4, GB, false>, pl, args, stream);
+  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, 8>(pl, args, stream);
+  else launch_gemv4_ch<DT, RW, MS, KS, 2>(pl, args, stream);
 }
 
 template <int DT, int RW, int MS>
@@ -429,12 +561,33 @@ void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   }
 }
 
+#ifndef SIMSD_LDS_U
+#define SIMSD_LDS_U 4
+#endif
+
+template <int DT, int RB, int CB, int KS>
+void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  constexpr int U = (RB * CB == 1) ? SIMSD_LDS_U : (SIMSD_LDS_U + 1) / 2;
+  if (pl.split > 1) launch<true>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true>, pl, args, stream);
+  else launch<false>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false>, pl, args, stream);
+}
+
+template <int DT, int RB, int CB>
+void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  if (pl.ks == 2) launch_lds<DT, RB, CB, 2>(pl, args, stream);
+  else launch_lds<DT, RB, CB, 4>(pl, args, stream);
+}
+
 template <int DT>
 void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   if constexpr (DT != kF32) {
     if (pl.kind == 1) {
       if (pl.ms == 1) gemv4_rows<DT, 1>(pl, args, stream);
       else gemv4_rows<DT, 2>(pl, args, stream);
+    } else if (pl.kind == 2) {
+      const bool two_rows = pl.rows == 32;
+      if (pl.cb == 1) { if (two_rows) lds_ks<DT, 2, 1>(pl, args, stream); else lds_ks<DT, 1, 1>(pl, args, stream); }
+      else { if (two_rows) lds_ks<DT, 2, 2>(pl, args, stream); else lds_ks<DT, 1, 2>(pl, args, stream); }
     }
   }
   if (pl.kind == 0) {
@@ -456,12 +609,13 @@ using namespace simsd;
 
 extern "C" int64_t simsd_thin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int dtype,
                                                      int block_n, int split_k, int num_waves) {
+  const int block_k = 0;   // the chunk size does not change the workspace
   // Enough for any path the call may take: either kernel with the requested
   // geometry, or the strided one (16 rows, 4 waves).
   ThinPlan a{}, b{}, c{};
-  if (plan_geometry(a, 0, M, N, K, dtype, block_n, num_waves, split_k) != 0) return -1;
-  if (plan_geometry(b, 0, M, N, K, dtype, 16, 4, split_k) != 0) return -1;
-  if (plan_geometry(c, gemv4_kind(M, dtype), M, N, K, dtype, block_n, num_waves, split_k) != 0)
+  if (plan_geometry(a, 0, M, N, K, dtype, block_n, block_k, num_waves, split_k) != 0) return -1;
+  if (plan_geometry(b, 0, M, N, K, dtype, 16, block_k, 4, split_k) != 0) return -1;
+  if (plan_geometry(c, fast_kind(M, dtype), M, N, K, dtype, block_n, block_k, num_waves, split_k) != 0)
     return -1;
   int64_t need = a.part_bytes > b.part_bytes ? a.part_bytes : b.part_bytes;
   return need > c.part_bytes ? need : c.part_bytes;
@@ -470,7 +624,7 @@ extern "C" int64_t simsd_thin_linear_workspace_bytes(int64_t M, int64_t N, int64
 extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const void* w,
                                  int64_t swn, int64_t swk, const void* bias, int64_t sb, void* y,
                                  int64_t sym, int64_t syn, int64_t M, int64_t N, int64_t K,
-                                 int dtype, int block_n, int split_k, int num_waves,
+                                 int dtype, int block_n, int block_k, int split_k, int num_waves,
                                  void* workspace, int64_t workspace_bytes, void* stream_) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
@@ -482,7 +636,7 @@ extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const 
   if (K * (int64_t)esize_of(dtype) > ((int64_t)1 << 31) - 64)
     return set_error("thin_linear: K=%lld too large", (long long)K);
   ThinPlan pl{};
-  if (make_plan(pl, x, sxm, sxk, w, swn, swk, M, N, K, dtype, block_n, split_k, num_waves) != 0)
+  if (make_plan(pl, x, sxm, sxk, w, swn, swk, M, N, K, dtype, block_n, block_k, split_k, num_waves) != 0)
     return -1;
   if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535 || cdiv(M * N, 256) > 0x7fffffff)
     return set_error("thin_linear: grid too large (N=%lld, M=%lld)", (long long)N, (long long)M);
@@ -515,10 +669,11 @@ extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const 
 
 extern "C" int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype, int block_n,
                                       int split_k, int num_waves, int* out4) {
+  const int block_k = 0;
   // (rows per workgroup, columns per block, waves per workgroup, split) of the
   // geometry a vector-capable call takes; lets the Python side report it.
   ThinPlan pl{};
-  if (plan_geometry(pl, gemv4_kind(M, dtype), M, N, K, dtype, block_n, num_waves, split_k) != 0)
+  if (plan_geometry(pl, fast_kind(M, dtype), M, N, K, dtype, block_n, block_k, num_waves, split_k) != 0)
     return -1;
   out4[0] = pl.rows;
   out4[1] = pl.kind == 1 ? 4 * pl.ms : 16 * pl.cb;

@@ -23,9 +23,15 @@ load stream carries no branches.
   the 4 output columns are the (up to 4) tokens -- nothing is padded.  The
   activations of a wave's K range sit in registers and serve every 4-row
   group, so the inner loop issues weight loads only.
-* otherwise (M up to 32 per block, fp32, strided views):
-  ``v_mfma_f32_16x16x32_bf16`` with 16 weight rows as the A operand and up to
-  16 tokens as the B operand per block.
+* M > 8 (bf16/fp16): ``v_mfma_f32_16x16x32_bf16`` with 16 weight rows as the
+  A operand and up to 16 tokens per block as the B operand.  The weight is
+  still read as 4 rows x 256 contiguous bytes per instruction; each wave
+  writes its 16- or 32-row tile through a padded LDS region and reads it back
+  in the MFMA operand layout.  Several 256-byte k chunks are loaded per batch
+  so enough bytes are in flight.
+* fp32 and strided / unaligned views: the same 16x16 MFMA shape with the
+  operands loaded straight in their MFMA layout (64 B of a row per lane
+  group), element by element where the view is not vector-aligned.
 
 A workgroup owns 4, 8, 16 or 32 weight rows and splits K over its waves,
 which sum their fp32 partials in fixed order; narrow N uses fewer rows per
@@ -38,7 +44,8 @@ SPLIT_K[, num_warps, num_stages])`` and describe the MI355X kernels:
 BLOCK_M is the token envelope (``TUNED``: dispatch for M up to 16 or 32) or
 column-block width (heuristic: 4 or 8 for the GEMV, 16 or 32 otherwise),
 BLOCK_N the weight rows per workgroup (4, 8, 16 or 32; other values round down
-to one of these), BLOCK_K the K elements of activations a wave holds at once,
+to one of these; at least 16 above 8 tokens), BLOCK_K the K elements of
+activations a wave holds at once in the GEMV (256 or 1024),
 SPLIT_K the workgroups along K, num_warps the waves per workgroup (2, 4 or 8);
 num_stages is accepted and ignored.
 
@@ -109,19 +116,19 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     # SDAR-1.7B draft projections (hidden 2048, 16 q / 8 kv heads, inter 6144)
     (2048, 2048): (16, 8, 1024, 1, 2, 2),     # q_proj, o_proj      4.3 us
     (2048, 1024): (16, 4, 1024, 1, 2, 2),     # k_proj, v_proj      3.5 us
-    (2048, 6144): (16, 8, 1024, 1, 2, 2),     # gate_proj, up_proj
-    (6144, 2048): (16, 8, 1024, 1, 8, 2),     # down_proj           7.5 us
-    (2048, 151936): (16, 8, 1024, 1, 2, 2),   # lm_head
-    (2048, 4096): (16, 8, 1024, 1, 2, 2),     # merged qkv          5.7 us
-    (2048, 12288): (16, 8, 1024, 1, 2, 2),    # merged gate+up     11.7 us
+    (2048, 6144): (16, 16, 256, 1, 4, 2),     # gate_proj, up_proj
+    (6144, 2048): (16, 8, 256, 1, 8, 2),      # down_proj           6.9 us
+    (2048, 151936): (16, 16, 256, 1, 4, 2),   # lm_head
+    (2048, 4096): (16, 8, 256, 1, 4, 2),      # merged qkv          5.6 us
+    (2048, 12288): (16, 16, 256, 1, 4, 2),    # merged gate+up     10.8 us
     # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
-    (4096, 12288): (32, 32, 128, 1, 2, 2),    # gate_proj / up_proj
-    (4096, 4096): (32, 16, 128, 1, 4, 2),     # q_proj, o_proj     12.0 / 16.0 us (M=16 / 32)
-    (4096, 1024): (32, 8, 128, 1, 4, 2),      # k_proj, v_proj
-    (4096, 6144): (32, 32, 128, 1, 4, 2),     # merged qkv         17.7 / 23.3 us
-    (4096, 24576): (32, 32, 128, 1, 2, 2),    # merged gate+up     51.6 / 63.7 us
-    (12288, 4096): (32, 16, 128, 1, 4, 2),    # down_proj          32.7 / 43.4 us
-    (4096, 151936): (32, 32, 128, 1, 2, 2),   # lm_head
+    (4096, 12288): (32, 32, 256, 1, 4, 2),    # gate_proj / up_proj
+    (4096, 4096): (32, 16, 256, 1, 4, 2),     # q_proj, o_proj      9.0 / 12.8 us (M=16 / 32)
+    (4096, 1024): (32, 16, 256, 4, 4, 2),     # k_proj, v_proj
+    (4096, 6144): (32, 32, 256, 1, 4, 2),     # merged qkv         12.1 / 16.4 us
+    (4096, 24576): (32, 32, 256, 1, 4, 2),    # merged gate+up     34.1 / 45.2 us
+    (12288, 4096): (32, 32, 256, 2, 4, 2),    # down_proj          21.6 / 27.4 us
+    (4096, 151936): (32, 32, 256, 1, 4, 2),   # lm_head
 }
 
 
@@ -150,12 +157,13 @@ def _tuned_for(M: int, N: int, K: int):
 def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, int, int, int]:
     """Same rule as the library's automatic plan (``simsd_thin_linear_plan``).
 
-    The fewest weight rows per workgroup (16, then 8, else 4) that still give
-    every CU a workgroup; a split along K only when even 4-row tiles leave
-    more than half the CUs idle.
+    The most weight rows per workgroup (16, then 8, else 4) that still give
+    every CU a workgroup (never below 16 for the 16x16 MFMA kernel above 8
+    tokens); a split along K only when the tiles leave more than half the CUs
+    idle.
     """
     if itemsize == 2 and M <= 8:        # 4x4x4 GEMV: 4 tokens per column set
-        BLOCK_M, BLOCK_K = (4 if M <= 4 else 8), 1024
+        BLOCK_M, BLOCK_K = (4 if M <= 4 else 8), 256
     else:                               # 16x16 MFMA tiles
         BLOCK_M = 16 if M <= 16 else 32
         BLOCK_K = (256 if BLOCK_M == 16 else 128) * 2 // itemsize
@@ -165,6 +173,8 @@ def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, i
         if _cdiv(N, cand) * m_tiles >= TARGET_CTAS:
             BLOCK_N = cand
             break
+    if itemsize == 2 and M > 8:
+        BLOCK_N = 16
     tiles = _cdiv(N, BLOCK_N) * m_tiles
     split = 1
     if tiles < TARGET_CTAS // 2:
@@ -223,14 +233,14 @@ def thin_linear(x: torch.Tensor, w: torch.Tensor,
     y = torch.empty((M, N), device=dev, dtype=x.dtype)
 
     if config is not None:
-        block_n, split_k = int(config[1]), int(config[3])
+        block_n, block_k, split_k = int(config[1]), int(config[2]), int(config[3])
         waves = num_warps or _DEFAULT_WAVES
     else:
         tuned = _tuned_for(M, N, K)
         if tuned is not None:
-            _, block_n, _, split_k, waves, _ = tuned
+            _, block_n, block_k, split_k, waves, _ = tuned
         else:
-            _, block_n, _, split_k = _heuristic_config(M, N, K, x.element_size())
+            _, block_n, block_k, split_k = _heuristic_config(M, N, K, x.element_size())
             waves = _DEFAULT_WAVES
         waves = num_warps or waves
     if split_k < 1:
@@ -254,7 +264,7 @@ def thin_linear(x: torch.Tensor, w: torch.Tensor,
             w.data_ptr(), w.stride(0), w.stride(1),
             bias.data_ptr() if fuse_bias else None, bias.stride(0) if fuse_bias else 0,
             y.data_ptr(), y.stride(0), y.stride(1),
-            M, N, K, code, block_n, split_k, waves,
+            M, N, K, code, block_n, block_k, split_k, waves,
             ws.data_ptr() if ws is not None else None, ws_bytes,
             _native.stream_of(dev))
     _native.check(status, "thin_linear")

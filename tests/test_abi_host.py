@@ -85,7 +85,7 @@ def test_header_links_from_plain_c(tmp_path):
 @pytest.mark.parametrize("M,N,K", [(4, 2048, 2048), (4, 1024, 2048), (4, 12288, 2048),
                                    (4, 2048, 6144), (16, 4096, 4096), (32, 24576, 4096),
                                    (32, 4096, 12288), (4, 151936, 2048), (96, 2048, 2048),
-                                   (1, 1, 1), (7, 33, 1000)])
+                                   (1, 1, 1), (7, 33, 1000), (24, 1024, 4096), (9, 100, 64)])
 def test_c_plan_equals_python_heuristic(M, N, K):
     from kernels import _native
     from kernels.thin_linear_fused import _heuristic_config
@@ -114,7 +114,7 @@ def test_error_string_round_trip():
     from kernels import _native
     lib = _native.lib()
     st = lib.simsd_thin_linear(None, 0, 0, None, 0, 0, None, 0, None, 0, 0, 4, 4, 4, 9,
-                               0, 0, 0, None, 0, None)
+                               0, 0, 0, 0, None, 0, None)
     assert st != 0
     assert b"dtype" in lib.simsd_last_error_string()
     with pytest.raises(RuntimeError, match="dtype"):

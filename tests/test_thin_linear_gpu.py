@@ -153,6 +153,23 @@ def test_reduction_is_deterministic(split_k):
         assert float((first.float() - ref.float()).abs().max()) <= tol(ref)
 
 
+@pytest.mark.parametrize("M", [1, 4, 7, 9, 16, 24, 32, 40])
+def test_every_launch_shape(M):
+    """Every rows / waves / split / block_k combination the planner accepts,
+    on dims that leave partial tiles and a partial last k chunk."""
+    from kernels.thin_linear_fused import thin_linear
+    x, w = rnd(M, 1000, seed=31 + M), rnd(531, 1000, scale=0.02, seed=32)
+    with torch.inference_mode():
+        ref = F.linear(x, w)
+        for rows in (4, 8, 16, 32):
+            for waves in (2, 4, 8):
+                for split in (1, 3):
+                    for block_k in (256, 1024):
+                        got = thin_linear(x, w, config=(16, rows, block_k, split), num_warps=waves)
+                        err = float((got.float() - ref.float()).abs().max())
+                        assert err <= tol(ref), (rows, waves, split, block_k, err)
+
+
 def test_dispatch_falls_back_above_searched_M():
     from kernels.thin_linear_fused import ThinLinear, should_fuse
     lin = nn.Linear(2048, 2048, bias=False).to(DEV, torch.bfloat16).eval()
