@@ -13,6 +13,7 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
   c3m16 / c3m32
           8B-shape target verify set, 36 layers x {qkv 4096->6144, o 4096->4096,
           gate_up 4096->24576, down 12288->4096} + lm_head 4096->151936, M=16/32.
+  copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
           gate_up + SiLU.mul -> down -> combine, + one shared expert),
@@ -23,17 +24,20 @@ K replays bracketed by synchronisations and HIP events on the replay stream.
 value = algorithmic bytes per step / time per step (weights read once +
 activations in + outputs out).  The roofline object is for the dominant
 kernel; every launch in the c1/c2/c3 timed region is that kernel, so its
-average launch duration is the region time / launches.  Per-launch event
-timings of one eager pass are reported alongside (kernel time without the
-inter-launch gaps).  The CPU baseline is the reference's CPU path -- torch
+average launch duration is the region time / launches.  "traffic" is the
+HBM bytes per launch from the committed rocprofv3 PMC summary under
+profiles/ for the workload (null if none).  "breakdown" times each op's
+calls alone in a graph of their own.  The CPU baseline is the reference's CPU path -- torch
 F.linear in bf16 (its oracle ref_thin_linear) or the stock MoE loop --
 timed on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
 import argparse
+import glob
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -63,6 +67,20 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown"
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the dominant kernel for this workload, as
+    recorded in a committed rocprofv3 PMC summary under profiles/ (FETCH_SIZE
+    + WRITE_SIZE per dispatch, scaled by a plain copy kernel's reading); None
+    when no summary covers the workload."""
+    pat = re.compile(r"^traffic_bytes_per_launch:\s*(\w+)\s*=\s*(\d+)")
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", "*.md"))):
+        for line in open(path):
+            m = pat.match(line.strip())
+            if m and m.group(1) == workload:
+                return int(m.group(2))
+    return None
 
 
 # ───────────────────────────────────────────────────────────── workloads ───
@@ -96,6 +114,30 @@ def make_linear_calls(torch, dev, workload):
         calls.append((name, rand((M, K), 1.0, 7), rand((N, K), 0.02, 8)))
         return M, calls
     raise ValueError(workload)
+
+
+def graph_us_per_call(torch, fns, reps=20):
+    """Capture fns (no-arg launches) in one graph; replay; us per launch."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps / len(fns)
 
 
 def cpu_baseline_linear(torch, workload, M):
@@ -159,23 +201,14 @@ def run_linear(args, torch, dev):
         for _ in range(2):
             step()
         torch.cuda.synchronize()
-        # one eager pass with an event pair around every launch: kernel time
-        # per op without the gaps between launches
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in calls]
-        for (name, x, w), (e0, e1) in zip(calls, evs):
-            e0.record()
-            thin_linear(x, w)
-            e1.record()
-        torch.cuda.synchronize()
+        # per-op time: each op's calls alone in a graph of their own
         per_op = {}
-        for (name, x, w), (e0, e1) in zip(calls, evs):
-            us = e0.elapsed_time(e1) * 1e3
-            d = per_op.setdefault(name, {"K": x.shape[1], "N": w.shape[0], "us": [], "bytes": 0})
-            d["us"].append(us)
-            d["bytes"] = linear_bytes(M, x.shape[1], w.shape[0])
-        eager_bytes = sum(d["bytes"] * len(d["us"]) for d in per_op.values())
-        eager_us = sum(sum(d["us"]) for d in per_op.values())
+        for name in dict.fromkeys(n for n, _, _ in calls):
+            mine = [(x, w) for n, x, w in calls if n == name]
+            us = graph_us_per_call(torch, [lambda x=x, w=w: thin_linear(x, w) for x, w in mine])
+            K, N = mine[0][0].shape[1], mine[0][1].shape[0]
+            per_op[name] = {"K": K, "N": N, "calls": len(mine), "us": us,
+                            "bytes": linear_bytes(M, K, N)}
 
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -200,11 +233,13 @@ def run_linear(args, torch, dev):
 
     gbs = step_bytes / (ms * 1e-3) / 1e9
     avg_launch_us = ms * 1e3 / launches
+    kernel = ("thin_gemv4_kernel (4x4x4 MFMA GEMV, M <= 8)" if M <= 8 else
+              "thin_gemm_lds_kernel (16x16x32 MFMA via LDS; per call, the split-K reduce "
+              "launch of down_proj included)")
     breakdown = {
-        n: {"K": d["K"], "N": d["N"], "calls": len(d["us"]),
-            "us_per_call": round(statistics.mean(d["us"]), 3),
-            "GB/s": round(d["bytes"] / (statistics.mean(d["us"]) * 1e-6) / 1e9, 1),
-            "frac": round(d["bytes"] / (statistics.mean(d["us"]) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        n: {"K": d["K"], "N": d["N"], "calls": d["calls"], "us_per_call": round(d["us"], 3),
+            "GB/s": round(d["bytes"] / (d["us"] * 1e-6) / 1e9, 1),
+            "frac": round(d["bytes"] / (d["us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         for n, d in per_op.items()}
     result = {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
@@ -219,12 +254,10 @@ def run_linear(args, torch, dev):
         "roofline": {"bound": "hbm", "achieved": round(step_bytes / launches / (avg_launch_us * 1e-6) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(step_bytes / launches / (avg_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None,
-                     "kernel": "thin_gemm_kernel",
+                     "traffic": measured_traffic(args.workload),
+                     "kernel": kernel,
                      "bytes_per_launch": round(step_bytes / launches),
-                     "avg_launch_us": round(avg_launch_us, 3),
-                     "eager_event_kernel_us": round(eager_us / launches, 3),
-                     "eager_event_GBs": round(eager_bytes / (eager_us * 1e-6) / 1e9, 1)},
+                     "avg_launch_us": round(avg_launch_us, 3)},
         "breakdown": breakdown,
         "tflops": round(sum(2 * M * x.shape[1] * w.shape[0] for _, x, w in calls) / (ms * 1e-3) / 1e12, 2),
     }
@@ -282,11 +315,11 @@ def run_moe(args, torch, dev):
     gbs = total_bytes / L / (ms * 1e-3) / 1e9
     return {
         "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "steps": args.steps * L, "warmup": args.warmup * L, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": f"moe-step-T{T}-E{E}-k{k}-H{H}-I{I}+shared", "T": T,
-                   "layers_cycled": L, "algorithmic_bytes_per_step": total_bytes // L,
+                   "layers_cycled": L, "graph_replays": args.steps, "algorithmic_bytes_per_step": total_bytes // L,
                    "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
@@ -295,7 +328,8 @@ def run_moe(args, torch, dev):
 
 
 def cpu_baseline_moe(torch, T):
-    """The stock per-expert loop (oracle restatement, fp64 numpy) on one layer."""
+    """The stock per-expert loop (oracle restatement, numpy) on one layer of
+    the workload: only the experts the routing picks are materialised."""
     import numpy as np
     from oracle import moe as omoe
 
@@ -304,21 +338,58 @@ def cpu_baseline_moe(torch, T):
     x = rng.standard_normal((T, H))
     logits = rng.standard_normal((T, E))
     ids, w = omoe.route_topk(logits, k, scoring="softmax", renorm=False)
-    act = np.unique(ids)
-    wg = rng.standard_normal((E, I, H)) * 0.02
-    wu = rng.standard_normal((E, I, H)) * 0.02
-    wd = rng.standard_normal((E, H, I)) * 0.02
+    act, local = np.unique(ids, return_inverse=True)
+    local = local.reshape(ids.shape)
+    n = act.size
+    wg = rng.standard_normal((n, I, H)) * 0.02
+    wu = rng.standard_normal((n, I, H)) * 0.02
+    wd = rng.standard_normal((n, H, I)) * 0.02
     times = []
-    for _ in range(3):
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 3 or (len(times) < 10 and time.perf_counter() < t_end):
         t0 = time.perf_counter()
-        omoe.dispatch_grouped(x, ids, w, wg, wu, wd, dtype="bf16")
+        omoe.dispatch_grouped(x, local, w, wg, wu, wd, dtype="bf16")
         times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end:
+            break
     med = statistics.median(times)
-    byts = (act.size) * (2 * I * H + H * I) * BF16
-    return {"value": round(byts / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+    byts = n * (2 * I * H + H * I) * BF16
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()
+                     if i.get("user_api") == "blas"] or [1])
+    except Exception:   # threadpoolctl missing: numpy's BLAS pool size unknown
+        cores = os.cpu_count() or 1
+    return {"value": round(byts / med / 1e9, 3), "unit": "GB/s", "cores": cores,
             "kind": "port",
-            "sample": f"oracle stock per-expert loop (numpy fp64), one layer T={T}, "
-                      f"median of 3 ({med * 1e3:.1f} ms); cpu={cpu_model()}"}
+            "sample": f"oracle per-expert loop (numpy, fp64 sums, bf16 rounding points), one "
+                      f"layer T={T} ({n} active experts), median of {len(times)} "
+                      f"({med * 1e3:.1f} ms); cpu={cpu_model()}"}
+
+
+def run_copy(args, torch, dev):
+    """A plain 1 GiB device copy (torch's elementwise copy kernel): the known
+    byte count that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
+    n = 1 << 29   # bf16 elements = 1 GiB
+    src = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    byts = 2 * n * BF16
+    return {"metric": "device copy GB/s (read + write)", "value": round(byts / (ms * 1e-3) / 1e9, 2),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 2,
+            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "copy-1GiB", "bytes_read": n * BF16, "bytes_written": n * BF16,
+                       "parallelism": "single-gpu"}}
 
 
 def main():
@@ -327,7 +398,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64"])
+                    choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -342,6 +413,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "copy":
+        print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
     if args.workload.startswith("c4"):
         result, T = run_moe(args, torch, dev)
         if not args.no_cpu_baseline:

@@ -60,6 +60,26 @@ def test_linear_exact_golden_k1(golden):
     assert np.array_equal(othin.linear_exact(d["x"], d["w"], dtype="bf16"), d["y"])
 
 
+def test_planted_linear_mistakes_are_caught(golden):
+    """Plausible slips in a linear restatement each fail a golden vector."""
+    from oracle.numerics import round_bf16
+    d = golden("thin_int")
+    x, w = d["c0_x"].astype(np.float64), d["c0_w"].astype(np.float64)
+    expect = d["c0_y_bf16"]
+    assert x.shape[1] > 1
+    slips = {
+        "dropped last k term": round_bf16(x[:, :-1] @ w[:, :-1].T),
+        "reversed k pairing": round_bf16(x @ w[:, ::-1].T),
+        "off-by-one output row": np.roll(round_bf16(x @ w.T), 1, axis=1),
+        "sign flip": round_bf16(-(x @ w.T)),
+        "rounded product terms": round_bf16(round_bf16(x[:, None, :] * w[None, :, :] / 3).sum(-1) * 3),
+    }
+    for name, bad in slips.items():
+        assert not np.array_equal(bad, expect), name
+    bias_bad = othin.linear_exact(d["bias_x"], d["bias_w"], None, dtype="bf16")
+    assert not np.array_equal(bias_bad, d["bias_y"]), "bias dropped"
+
+
 def test_linear_exact_vs_torch_cpu_linear():
     """Second opinion: torch's CPU bf16 F.linear (the reference oracle) sits
     within the reference tolerance of the exact-sum oracle."""
