@@ -147,6 +147,37 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
 //   GB  row groups whose loads are issued together
 constexpr int kStep4Bytes = 256;   // bytes of one row per 4x4x4 load step
 
+// Sum NV per-lane values over the 16 lanes that share lane bits 0..1 (the
+// 4x4x4 blocks of a wave).  Bits 5 and 4 by reduce-scatter on the gfx950 lane
+// swaps: v_permlane32_swap(a, b) leaves [a.lo, b.lo] / [a.hi, b.hi], so one
+// swap and one add sum a pair of values over the two half-waves and keep one
+// of them per half (likewise rows 0/1 and 2/3 with v_permlane16_swap).  Bits
+// 3 and 2 by adding a row rotation by 8 and then by 4.  Afterwards lane l
+// holds, in val[p] for p < NV/4, the full sum of original value
+// p + bit5(l) * NV/2 + bit4(l) * NV/4 (lanes differing in bits 2..3 agree).
+// A fixed instruction sequence: bit-reproducible.
+template <int NV>
+__device__ __forceinline__ void reduce_kblocks(float (&val)[NV]) {
+  static_assert(NV >= 4 && (NV & (NV - 1)) == 0, "power of two >= 4");
+#pragma unroll
+  for (int p = 0; p < NV / 2; ++p) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(val[p]),
+                                                    __float_as_uint(val[p + NV / 2]), false, false);
+    val[p] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int p = 0; p < NV / 4; ++p) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(val[p]),
+                                                    __float_as_uint(val[p + NV / 4]), false, false);
+    val[p] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int p = 0; p < NV / 4; ++p) {
+    val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x128, 0xF, 0xF, false));
+    val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x124, 0xF, 0xF, false));
+  }
+}
+
 template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL>
 __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
@@ -221,29 +252,22 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
     }
   }
 
-  // sum the 16 k-chunk blocks (lanes with equal j), fixed butterfly order
+  // sum the 16 k-chunk blocks (lane bits 2..5), then the KS waves in wave
+  // order through LDS: red[wave][value][col j]
+  constexpr int NV = G * MS * 4;
+  float val[NV];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int c = 0; c < MS; ++c)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float t = acc[g][c][v];
-        t += __shfl_xor(t, 4);
-        t += __shfl_xor(t, 8);
-        t += __shfl_xor(t, 16);
-        t += __shfl_xor(t, 32);
-        acc[g][c][v] = t;
-      }
-  // then the KS waves, in wave order, through LDS: red[wave][g][c][row i][col j]
-  __shared__ float red[KS * G * MS * 16];
-  if (lane < 4) {
+      for (int v = 0; v < 4; ++v) val[(g * MS + c) * 4 + v] = acc[g][c][v];
+  reduce_kblocks<NV>(val);
+  __shared__ float red[KS * NV * 4];
+  if (((lane >> 2) & 3) == 0) {
+    const int q0 = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int c = 0; c < MS; ++c)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) red[((wk * G + g) * MS + c) * 16 + v * 4 + lane] = acc[g][c][v];
+    for (int p = 0; p < NV / 4; ++p) red[(wk * NV + q0 + p) * 4 + i4] = val[p];
   }
   __syncthreads();
   for (int e = threadIdx.x; e < G * MS * 16; e += 64 * KS) {
@@ -529,16 +553,23 @@ void gemm_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   }
 }
 
+#ifndef SIMSD_GEMV_GB_ALL
+#define SIMSD_GEMV_GB_ALL 0   // 1: every row group's loads of a chunk issued together
+#endif
+#ifndef SIMSD_GEMV_CH_BIG
+#define SIMSD_GEMV_CH_BIG 8   // load steps per chunk for block_k >= 512
+#endif
+
 template <int DT, int RW, int MS, int KS, int CH>
 void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  constexpr int GB = RW >= 8 ? 2 : 1;
+  constexpr int GB = SIMSD_GEMV_GB_ALL ? RW / 4 : (RW >= 8 ? 2 : 1);
   if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true>, pl, args, stream);
   else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false>, pl, args, stream);
 }
 
 template <int DT, int RW, int MS, int KS>
 void launch_gemv4(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, 8>(pl, args, stream);
+  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG>(pl, args, stream);
   else launch_gemv4_ch<DT, RW, MS, KS, 2>(pl, args, stream);
 }
 
