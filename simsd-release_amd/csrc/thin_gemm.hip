@@ -147,18 +147,19 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
 //   GB  row groups whose loads are issued together
 constexpr int kStep4Bytes = 256;   // bytes of one row per 4x4x4 load step
 
-// Sum NV per-lane values over the 16 lanes that share lane bits 0..1 (the
-// 4x4x4 blocks of a wave).  Bits 5 and 4 by reduce-scatter on the gfx950 lane
-// swaps: v_permlane32_swap(a, b) leaves [a.lo, b.lo] / [a.hi, b.hi], so one
-// swap and one add sum a pair of values over the two half-waves and keep one
-// of them per half (likewise rows 0/1 and 2/3 with v_permlane16_swap).  Bits
-// 3 and 2 by adding a row rotation by 8 and then by 4.  Afterwards lane l
-// holds, in val[p] for p < NV/4, the full sum of original value
-// p + bit5(l) * NV/2 + bit4(l) * NV/4 (lanes differing in bits 2..3 agree).
+// Sum NV per-lane values over lane bits 5, 4 and the row bits from log2(LO)
+// up to 3.  Bits 5 and 4 by reduce-scatter on the gfx950 lane swaps:
+// v_permlane32_swap(a, b) leaves [a.lo, b.lo] / [a.hi, b.hi], so one swap and
+// one add sum a pair of values over the two half-waves and keep one of them
+// per half (likewise rows 0/1 and 2/3 with v_permlane16_swap).  The row bits
+// by adding row rotations by 8, 4, ..., LO (after which every lane of the
+// rotation class holds the full sum).  Afterwards lane l holds, in val[p] for
+// p < NV/4, the sum of original value p + bit5(l) * NV/2 + bit4(l) * NV/4.
 // A fixed instruction sequence: bit-reproducible.
-template <int NV>
-__device__ __forceinline__ void reduce_kblocks(float (&val)[NV]) {
+template <int NV, int LO>
+__device__ __forceinline__ void reduce_lanes(float (&val)[NV]) {
   static_assert(NV >= 4 && (NV & (NV - 1)) == 0, "power of two >= 4");
+  static_assert(LO == 1 || LO == 2 || LO == 4 || LO == 8, "rotation");
 #pragma unroll
   for (int p = 0; p < NV / 2; ++p) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(val[p]),
@@ -174,7 +175,12 @@ __device__ __forceinline__ void reduce_kblocks(float (&val)[NV]) {
 #pragma unroll
   for (int p = 0; p < NV / 4; ++p) {
     val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x128, 0xF, 0xF, false));
-    val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x124, 0xF, 0xF, false));
+    if (LO <= 4)
+      val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x124, 0xF, 0xF, false));
+    if (LO <= 2)
+      val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x122, 0xF, 0xF, false));
+    if (LO <= 1)
+      val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x121, 0xF, 0xF, false));
   }
 }
 
@@ -262,7 +268,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
     for (int c = 0; c < MS; ++c)
 #pragma unroll
       for (int v = 0; v < 4; ++v) val[(g * MS + c) * 4 + v] = acc[g][c][v];
-  reduce_kblocks<NV>(val);
+  reduce_lanes<NV, 4>(val);   // the 16 k blocks: lane bits 2..5
   __shared__ float red[KS * NV * 4];
   if (((lane >> 2) & 3) == 0) {
     const int q0 = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);

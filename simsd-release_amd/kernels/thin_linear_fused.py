@@ -114,13 +114,13 @@ def reset_workspace() -> None:
 # gate/up, k/v and lm_head of the target) follow the nearest swept shape.
 TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     # SDAR-1.7B draft projections (hidden 2048, 16 q / 8 kv heads, inter 6144)
-    (2048, 2048): (16, 8, 1024, 1, 2, 2),     # q_proj, o_proj      4.3 us
-    (2048, 1024): (16, 4, 1024, 1, 2, 2),     # k_proj, v_proj      3.5 us
+    (2048, 2048): (16, 8, 1024, 1, 2, 2),     # q_proj, o_proj      4.0 us
+    (2048, 1024): (16, 4, 1024, 1, 2, 2),     # k_proj, v_proj      3.2 us
     (2048, 6144): (16, 16, 256, 1, 4, 2),     # gate_proj, up_proj
-    (6144, 2048): (16, 8, 256, 1, 8, 2),      # down_proj           6.9 us
+    (6144, 2048): (16, 8, 256, 1, 8, 2),      # down_proj           6.6 us
     (2048, 151936): (16, 16, 256, 1, 4, 2),   # lm_head
-    (2048, 4096): (16, 8, 256, 1, 4, 2),      # merged qkv          5.6 us
-    (2048, 12288): (16, 16, 256, 1, 4, 2),    # merged gate+up     10.8 us
+    (2048, 4096): (16, 8, 256, 1, 4, 2),      # merged qkv          5.2 us
+    (2048, 12288): (16, 16, 256, 1, 2, 2),    # merged gate+up     10.0 us
     # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
     (4096, 12288): (32, 32, 256, 1, 4, 2),    # gate_proj / up_proj
     (4096, 4096): (32, 16, 256, 1, 4, 2),     # q_proj, o_proj      9.0 / 12.8 us (M=16 / 32)
