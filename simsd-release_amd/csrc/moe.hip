@@ -22,13 +22,16 @@ constexpr int kTile = 16;   // slots per tile (the reference's BLOCK_M)
 
 // ============================================================ route top-k ===
 // One wave per token; the E logits are spread over the 64 lanes.  Selection
-// order is value descending, ties to the lower expert index.
+// order is value descending, ties to the lower expert index.  Every reduction
+// over the wave runs on lane permutes (wave_max / wave_sum / wave_argmax),
+// none through LDS.
 template <int PL>
 __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int64_t T,
                                                         int E, int64_t stride_t, int k, int scoring,
                                                         int renorm, float scale,
                                                         int64_t* __restrict__ ids,
                                                         float* __restrict__ wout) {
+  constexpr int kNone = 0x7fffffff;
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -43,19 +46,17 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
   }
   float mx = 0.f, denom = 1.f;
   if (scoring == SIMSD_SCORE_SOFTMAX) {
-    mx = -INFINITY;
+    float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PL; ++i)
-      if (!((used >> i) & 1u)) mx = fmaxf(mx, v[i]);
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    float s = 0.f;
+      if (!((used >> i) & 1u)) m = fmaxf(m, v[i]);
+    mx = wave_max(m);
+    float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < PL; ++i)
-      if (!((used >> i) & 1u)) s += expf(v[i] - mx);
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    denom = s;
+      if (!((used >> i) & 1u)) sum += expf(v[i] - mx);
+    denom = wave_sum(sum);
   }
-  constexpr int kNone = 0x7fffffff;
   float my_v = 0.f;
   int my_i = 0;
   for (int j = 0; j < k; ++j) {
@@ -68,27 +69,21 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
         bi = lane + 64 * i;
       }
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      const bool take = oi != kNone && (bi == kNone || ov > bv || (ov == bv && oi < bi));
-      if (take) { bv = ov; bi = oi; }
-    }
+    wave_argmax(bv, bi);
     if ((bi & 63) == lane) used |= 1u << (bi >> 6);
     if (lane == j) { my_v = bv; my_i = bi; }
   }
-  float s = 0.f;
+  float sc = 0.f;
   if (lane < k) {
-    s = scoring == SIMSD_SCORE_SOFTMAX ? expf(my_v - mx) / denom : 1.f / (1.f + expf(-my_v));
+    sc = scoring == SIMSD_SCORE_SOFTMAX ? expf(my_v - mx) / denom : 1.f / (1.f + expf(-my_v));
   }
   if (renorm && k > 1) {
-    float tot = lane < k ? s : 0.f;
-    for (int off = 32; off >= 1; off >>= 1) tot += __shfl_xor(tot, off);
-    s = s / (tot + 1e-20f);
+    const float tot = wave_sum(lane < k ? sc : 0.f);
+    sc = sc / (tot + 1e-20f);
   }
   if (lane < k) {
     ids[t * k + lane] = (int64_t)my_i;
-    wout[t * k + lane] = s * scale;
+    wout[t * k + lane] = sc * scale;
   }
 }
 
@@ -281,10 +276,18 @@ SIMSD_DEV float silu_f32(float v) { return v / (1.f + expf(-v)); }
 // and W_up are the two A blocks, the tile's 16 gathered x rows the B block;
 // 4 waves split H.  Epilogue h = silu(g) * u with the reference's rounding
 // points (g, u, silu(g) and h each rounded to the storage dtype).
+#ifndef SIMSD_MOE_GU_U
+#define SIMSD_MOE_GU_U 2   // 256-byte k chunks per load batch in gate_up
+#endif
+#ifndef SIMSD_MOE_DN_U
+#define SIMSD_MOE_DN_U 4   // 256-byte k chunks per load batch in down
+#endif
+
 template <int DT, bool FAST>
 __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
-  constexpr int KS = 4, U = 4;
+  constexpr int KS = 4;
+  __shared__ __attribute__((aligned(16))) char gu_tile[KS][FAST ? 32 * kLdsRow : 16];
   const int lane = threadIdx.x & 63, wk = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int t = blockIdx.x;
@@ -315,21 +318,25 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   f32x4_t acc[2][1] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}}, {f32x4_t{0.f, 0.f, 0.f, 0.f}}};
   if (FAST) {
     // descriptors: the expert's gate and up matrices, and all of x; rows past
-    // II and empty slots read as zero
+    // II and empty slots read as zero.  Weights stream as 4 rows x 256 B per
+    // load through the wave's LDS tile (accum_lds).
     const uint32_t Kb = (uint32_t)(a.H * ES);
     rsrc_t ra[2];
-    uint32_t aoff[2];
+    uint32_t a_row0[2], a_snb[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const uint32_t sn_b = (uint32_t)(a_sn[b] * ES);
-      ra[b] = make_rsrc(wbase[b], (uint32_t)(II - 1) * sn_b + Kb);
-      aoff[b] = (uint32_t)(i0 + r) * sn_b;
+      a_snb[b] = (uint32_t)(a_sn[b] * ES);
+      ra[b] = make_rsrc(wbase[b], (uint32_t)(II - 1) * a_snb[b] + Kb);
+      a_row0[b] = (uint32_t)i0 * a_snb[b];
     }
     const uint32_t sxt_b = (uint32_t)(a.sxt * ES);
     const rsrc_t rB = make_rsrc(a.x, (uint32_t)(a.T - 1) * sxt_b + Kb);
     const uint32_t boff[1] = {tr.token >= 0 ? (uint32_t)tr.token * sxt_b : 0u};
     const bool bok[1] = {tr.token >= 0};
-    accum_fast<DT, 2, 1, U>(ra, aoff, rB, boff, bok, w0, w1, (uint32_t)(g * kLaneBytes), Kb, acc);
+    const int chunks = (int)((Kb + kStep4Bytes - 1) / kStep4Bytes);
+    const int per = (chunks + KS - 1) / KS;
+    const int c0 = wk * per, c1 = min(chunks, c0 + per);
+    accum_lds<DT, 2, 1, SIMSD_MOE_GU_U>(ra, a_row0, a_snb, rB, boff, bok, c0, c1, Kb, gu_tile[wk], acc);
   } else {
     const int64_t i_row = min(i0 + r, II - 1);
     const char* arow[2] = {wbase[0] + i_row * a_sn[0] * ES, wbase[1] + i_row * a_sn[1] * ES};
@@ -364,7 +371,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
 template <int DT, bool FAST>
 __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
-  constexpr int U = 8;
+  __shared__ __attribute__((aligned(16))) char dn_tile[4][FAST ? 16 * kLdsRow : 16];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int t = blockIdx.x;
@@ -385,11 +392,13 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
     const uint32_t sn_b = (uint32_t)(a_sn * ES);
     const int64_t h_rows = shared ? a.T : a.T * a.k;
     const rsrc_t ra[1] = {make_rsrc(wbase, (uint32_t)(a.H - 1) * sn_b + Kb)};
-    const uint32_t aoff[1] = {(uint32_t)(n0 + r) * sn_b};
+    const uint32_t a_row0[1] = {(uint32_t)n0 * sn_b};
+    const uint32_t a_snb[1] = {sn_b};
     const rsrc_t rB = make_rsrc(hbase, (uint32_t)h_rows * Kb);
     const uint32_t boff[1] = {tr.slot >= 0 ? (uint32_t)tr.slot * Kb : 0u};
     const bool bok[1] = {tr.slot >= 0};
-    accum_fast<DT, 1, 1, U>(ra, aoff, rB, boff, bok, 0, steps, (uint32_t)(g * kLaneBytes), Kb, acc);
+    const int chunks = (int)((Kb + kStep4Bytes - 1) / kStep4Bytes);
+    accum_lds<DT, 1, 1, SIMSD_MOE_DN_U>(ra, a_row0, a_snb, rB, boff, bok, 0, chunks, Kb, dn_tile[wv], acc);
   } else {
     const char* arow[1] = {wbase + min(n0 + r, a.H - 1) * a_sn * ES};
     const char* brow[1] = {tr.slot >= 0 ? hbase + tr.slot * II * ES : nullptr};
@@ -405,19 +414,29 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
 }
 
 // combine: out[t] = dtype( sum_j fp32(y[t*k+j]) * w[t,j] ), summed in j order,
-// then (shared expert) out = dtype(out + ys[t]).
+// then (shared expert) out = dtype(out + ys[t]).  The ids, weights and expert
+// outputs of 8 picks are loaded before any is used (one round trip, not 8);
+// rows of invalid ids are read but not added.
 template <int DT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
-  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int J = 8;
   const int64_t t = blockIdx.y;
   const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (h >= a.H) return;
   float acc = 0.f;
-  for (int j = 0; j < a.k; ++j) {
-    const int64_t e = a.ids[t * a.sidt + j * a.sidk];
-    if (e < 0 || e >= a.E) continue;
-    const float yv = load_elem<DT>(a.y, (t * a.k + j) * a.H + h);
-    acc = __fadd_rn(acc, __fmul_rn(yv, a.topk_w[t * a.swt + j * a.swk]));
+  for (int j0 = 0; j0 < a.k; j0 += J) {
+    int64_t e[J];
+    float wv[J], yv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const bool in = j0 + j < a.k;
+      e[j] = in ? a.ids[t * a.sidt + (j0 + j) * a.sidk] : -1;
+      wv[j] = in ? a.topk_w[t * a.swt + (j0 + j) * a.swk] : 0.f;
+      yv[j] = in ? load_elem<DT>(a.y, (t * a.k + j0 + j) * a.H + h) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+      if (e[j] >= 0 && e[j] < a.E) acc = __fadd_rn(acc, __fmul_rn(yv[j], wv[j]));
   }
   float o = round_to<DT>(acc);
   if (a.shared_tiles > 0) o = o + load_elem<DT>(a.ys, t * a.H + h);

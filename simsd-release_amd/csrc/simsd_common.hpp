@@ -266,6 +266,75 @@ SIMSD_DEV void accum_generic(const char* const (&arow)[RB], int64_t a_sk_bytes,
   }
 }
 
+// ------------------------------------------- LDS-relayout MFMA accumulation
+// acc[rb][cb] += A_rb . B_cb^T over the 256-byte k chunks [c0, c1) with
+// v_mfma_f32_16x16x32.  Weight block rb (16 rows, descriptor ra[rb], row 0 at
+// byte a_row0[rb], row stride a_sn[rb]) is read as 4 rows x 256 contiguous
+// bytes per load instruction (lane l: row 4q + l/16, bytes 16*(l%16)), written
+// to the wave's own LDS tile (16*RB rows, row stride kLdsRow = 272 B: no bank
+// conflicts for the 16-byte writes or for the MFMA-layout reads) and read back
+// in the A layout.  B block cb is loaded in the B layout straight from memory:
+// lane (g, r) reads 16 bytes at boff[cb] + k + 16 g of its row r (invalid rows
+// and bytes past Kb read zero).  U chunks are loaded per batch, all before the
+// first LDS write.  A wave's LDS accesses complete in order, so the reads see
+// the writes and the next chunk's writes follow the reads: no barrier.
+constexpr int kStep4Bytes = 256;            // bytes of one row per 4-row load step
+constexpr int kLdsRow = kStep4Bytes + 16;   // padded LDS row of a 256 B chunk
+
+template <int DT, int RB, int CB, int U>
+SIMSD_DEV void accum_lds(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
+                         const uint32_t (&a_sn)[RB], rsrc_t rbx, const uint32_t (&boff)[CB],
+                         const bool (&bok)[CB], int c0, int c1, uint32_t Kb, char* tile,
+                         f32x4_t (&acc)[RB][CB]) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, r = lane & 15;     // MFMA operand layout
+  const int lr = lane >> 4, lc = lane & 15;   // loader layout: row l/16 of 4, chunk l%16
+  for (int c = c0; c < c1; c += U) {
+    u32x4_t W[U][RB][4], B[U][4][CB];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = c + u < c1;
+      const uint32_t kc = (uint32_t)(c + u) * kStep4Bytes;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t k = kc + lc * kLaneBytes;
+          W[u][rb][q] = buf_load16<kAuxStream>(
+              ra[rb], live && k < Kb ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob);
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const uint32_t k = kc + j * kStepBytes + g * kLaneBytes;
+          B[u][j][cb] = buf_load16<kAuxKeep>(rbx, live && bok[cb] && k < Kb ? boff[cb] + k : kOob);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<u32x4_t*>(tile + (16 * rb + 4 * q + lr) * kLdsRow + lc * kLaneBytes) = W[u][rb][q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x4_t A[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          A[rb] = *reinterpret_cast<const u32x4_t*>(tile + (16 * rb + r) * kLdsRow + j * kStepBytes +
+                                                    g * kLaneBytes);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = Mfma<DT>::step(A[rb], B[u][j][cb], acc[rb][cb]);
+      }
+    }
+  }
+}
+
 // Sum the per-wave accumulators of KS waves that split the reduction, in a
 // fixed wave order (bit-reproducible).  Wave 0 ends up with the total.
 template <int KS, int NFRAG>
@@ -285,6 +354,71 @@ SIMSD_DEV void reduce_waves(f32x4_t (&acc)[NFRAG], int wave_k, int lane, float* 
       for (int f = 0; f < NFRAG; ++f)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[f][j] += red[((w - 1) * NFRAG * 4 + f * 4 + j) * 64 + lane];
+  }
+}
+
+// ------------------------------------------------------- wave all-reduces
+// Lane exchanges without LDS: DPP quad permutes (lane xor 1, xor 2), DPP row
+// rotations by 4 and 8 (which, after the quad stages, cover a 16-lane row),
+// and the gfx950 swaps v_permlane16_swap / v_permlane32_swap, which applied
+// to (v, v) return the values of both rows of a row pair (both half-waves):
+// combining the two outputs in a fixed order gives every lane the same result.
+SIMSD_DEV int dpp_quad_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+SIMSD_DEV int dpp_quad_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+SIMSD_DEV int dpp_row_ror4(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false); }
+SIMSD_DEV int dpp_row_ror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); }
+
+// Combine(a, b) must be commutative for the in-row stages; the result of the
+// last two stages is combine(lower half, upper half) on every lane.
+template <typename Combine>
+SIMSD_DEV float wave_allreduce(float v, Combine combine) {
+  v = combine(v, __int_as_float(dpp_quad_xor1(__float_as_int(v))));
+  v = combine(v, __int_as_float(dpp_quad_xor2(__float_as_int(v))));
+  v = combine(v, __int_as_float(dpp_row_ror4(__float_as_int(v))));
+  v = combine(v, __int_as_float(dpp_row_ror8(__float_as_int(v))));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = combine(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = combine(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  // the in-row stages may associate differently per lane: take lane 0's value
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+SIMSD_DEV float wave_max(float v) {
+  return wave_allreduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+SIMSD_DEV float wave_sum(float v) {
+  return wave_allreduce(v, [](float a, float b) { return a + b; });
+}
+
+// Largest (v, i) over the wave: larger v first, then smaller i; i == INT_MAX
+// marks an empty lane.  Every lane gets the winner (a total order: no
+// per-lane rounding differences).
+SIMSD_DEV bool argmax_take(float ov, int oi, float bv, int bi) {
+  return oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+}
+SIMSD_DEV void wave_argmax(float& v, int& i) {
+  auto stage = [&](int pv_bits, int pi) {
+    const float pv = __int_as_float(pv_bits);
+    if (argmax_take(pv, pi, v, i)) { v = pv; i = pi; }
+  };
+  stage(dpp_quad_xor1(__float_as_int(v)), dpp_quad_xor1(i));
+  stage(dpp_quad_xor2(__float_as_int(v)), dpp_quad_xor2(i));
+  stage(dpp_row_ror4(__float_as_int(v)), dpp_row_ror4(i));
+  stage(dpp_row_ror8(__float_as_int(v)), dpp_row_ror8(i));
+  {
+    const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const auto ri = __builtin_amdgcn_permlane16_swap((uint32_t)i, (uint32_t)i, false, false);
+    v = __uint_as_float(rv[0]);
+    i = (int)ri[0];
+    stage(__float_as_int(__uint_as_float(rv[1])), (int)ri[1]);
+  }
+  {
+    const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const auto ri = __builtin_amdgcn_permlane32_swap((uint32_t)i, (uint32_t)i, false, false);
+    v = __uint_as_float(rv[0]);
+    i = (int)ri[0];
+    stage(__float_as_int(__uint_as_float(rv[1])), (int)ri[1]);
   }
 }
 

@@ -145,7 +145,6 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
 //   KS  waves per workgroup splitting K
 //   CH  load steps (128 k elements each) whose activations are held at once
 //   GB  row groups whose loads are issued together
-constexpr int kStep4Bytes = 256;   // bytes of one row per 4x4x4 load step
 
 // Sum NV per-lane values over lane bits 5, 4 and the row bits from log2(LO)
 // up to 3.  Bits 5 and 4 by reduce-scatter on the gfx950 lane swaps:
@@ -294,13 +293,9 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 9..32 tokens: v_mfma_f32_16x16x32 fed from contiguous weight loads.  Each
-// wave loads its 16*RB rows as 4 rows x 256 contiguous bytes per instruction
-// (the GEMV's access pattern), writes the 16*RB x 256 B tile to its own LDS
-// region (row stride 272 B: conflict-free both ways) and reads it back in the
-// MFMA A layout, 4 k-steps per tile.  Activations are the B operand as in
-// thin_gemm_kernel.
-constexpr int kLdsRow = kStep4Bytes + 16;   // padded LDS row of a 256 B weight chunk
+// 9..32 tokens: v_mfma_f32_16x16x32 fed from contiguous weight loads (4 rows x
+// 256 bytes per instruction, the GEMV's access pattern) through a per-wave LDS
+// tile (accum_lds).  Activations are the B operand as in thin_gemm_kernel.
 
 template <int DT, int RB, int CB, int KS, int U, bool PARTIAL>
 __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
@@ -329,62 +324,26 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
   const int64_t cols_valid = min((int64_t)(CB * 16), a.M - m_tile);
   const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
   const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
-  char* my = tile[wk];
-  // loader lanes: row (l / 16) of a 4-row group, 16-byte chunk (l % 16)
-  const int lr = lane >> 4, lc = lane & 15;
-
   f32x4_t acc[RB][CB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  // U chunks per batch: all their loads are issued before the first LDS
-  // write, so a wave keeps U * (16*RB + 16*CB) * 256 B in flight.  Chunks past
-  // the wave's range read as zero (they belong to another wave).
-  for (int c = w0; c < w1; c += U) {
-    u32x4_t W[U][4 * RB], B[U][4][CB];
+  rsrc_t ra[RB];
+  uint32_t a_row0[RB], a_sn[RB], boff[CB];
+  bool bok[CB];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool live = c + u < w1;
-      const uint32_t kc = (uint32_t)(c + u) * kStep4Bytes;
-#pragma unroll
-      for (int q = 0; q < 4 * RB; ++q) {
-        const uint32_t k = kc + lc * kLaneBytes;
-        W[u][q] = buf_load16<kAuxStream>(rA, live && k < Kb ? (uint32_t)(4 * q + lr) * swn_b + k : kOob);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          const uint32_t k = kc + j * kStepBytes + g * kLaneBytes;
-          const bool ok = live && k < Kb && cb * 16 + r < cols_valid;
-          B[u][j][cb] = buf_load16<kAuxKeep>(rB, ok ? (uint32_t)(cb * 16 + r) * sxm_b + k : kOob);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      // a wave's LDS accesses complete in order: the reads below see these
-      // writes, and the next chunk's writes follow these reads
-#pragma unroll
-      for (int q = 0; q < 4 * RB; ++q)
-        *reinterpret_cast<u32x4_t*>(my + (4 * q + lr) * kLdsRow + lc * kLaneBytes) = W[u][q];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x4_t A[RB];
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-          A[rb] = *reinterpret_cast<const u32x4_t*>(my + (16 * rb + r) * kLdsRow + j * kStepBytes +
-                                                    g * kLaneBytes);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int cb = 0; cb < CB; ++cb)
-            acc[rb][cb] = Mfma<DT>::step(A[rb], B[u][j][cb], acc[rb][cb]);
-      }
-    }
+  for (int rb = 0; rb < RB; ++rb) {
+    ra[rb] = rA;
+    a_row0[rb] = (uint32_t)(16 * rb) * swn_b;
+    a_sn[rb] = swn_b;
   }
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) {
+    boff[cb] = (uint32_t)(cb * 16 + r) * sxm_b;
+    bok[cb] = cb * 16 + r < cols_valid;
+  }
+  accum_lds<DT, RB, CB, U>(ra, a_row0, a_sn, rB, boff, bok, w0, w1, Kb, tile[wk], acc);
 
   __shared__ float red[KS > 1 ? (KS - 1) * NF * 4 * 64 : 1];
   reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, red);
