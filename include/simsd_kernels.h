@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 2
+#define SIMSD_ABI_VERSION 3
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -108,6 +108,19 @@ int simsd_moe_num_tiles(int64_t M, int64_t E);
 int simsd_moe_align(const int64_t* ids, int64_t M, int64_t E, int num_tiles,
                     int32_t* counts, int32_t* offsets, int32_t* pad_offsets, int32_t* perm,
                     int32_t* slots, int32_t* tile_expert, void* stream);
+
+/* Route and align in one launch (one workgroup): the outputs of
+ * simsd_moe_route_topk (ids_out, w_out) followed by those of simsd_moe_align
+ * on the same ids, identical to calling the two in sequence.  The picks stay
+ * in LDS between the steps, which saves a launch and a round trip through
+ * memory at small token counts.  Counterpart of the remote gate's top-k
+ * followed by _align, kernels/moe_dispatch_fused.py:93-132.  T*k <= 8192,
+ * E <= 1024, k <= 64; tokens are routed 16 at a time, so large T is better
+ * served by the two separate calls. */
+int simsd_moe_route_align(const float* logits, int64_t T, int64_t E, int64_t stride_t, int k,
+                          int scoring, int renorm, float scale, int64_t* ids_out, float* w_out,
+                          int num_tiles, int32_t* counts, int32_t* offsets, int32_t* pad_offsets,
+                          int32_t* perm, int32_t* slots, int32_t* tile_expert, void* stream);
 
 /* ---- MoE: grouped expert FFN + combine ----------------------------------
  * out[t] = dtype( sum_j fp32(down_e(silu(gate_e(x_t)) * up_e(x_t))) * w[t, j] )

@@ -24,54 +24,47 @@ constexpr int kTile = 16;   // slots per tile (the reference's BLOCK_M)
 // One wave per token; the E logits are spread over the 64 lanes.  Selection
 // order is value descending, ties to the lower expert index.  Every reduction
 // over the wave runs on lane permutes (wave_max / wave_sum / wave_argmax),
-// none through LDS.
+// none through LDS.  Lane j < k ends with pick j: its expert and weight.
 template <int PL>
-__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int64_t T,
-                                                        int E, int64_t stride_t, int k, int scoring,
-                                                        int renorm, float scale,
-                                                        int64_t* __restrict__ ids,
-                                                        float* __restrict__ wout) {
-  constexpr int kNone = 0x7fffffff;
+SIMSD_DEV void route_token(const float* row, int E, int k, int scoring, int renorm, float scale,
+                           int& pick, float& weight) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const float* row = logits + t * stride_t;
   float v[PL];
-  uint32_t used = 0u;   // bit i: entry i taken, or past E
+  uint64_t key[PL];   // (order bits of the logit) << 32 | ~expert; 0 once taken or past E
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const int e = lane + 64 * i;
     v[i] = e < E ? row[e] : -INFINITY;
-    if (e >= E) used |= 1u << i;
+    key[i] = e < E ? ((uint64_t)float_order_bits(v[i]) << 32) | (uint32_t)~e : 0ull;
   }
   float mx = 0.f, denom = 1.f;
   if (scoring == SIMSD_SCORE_SOFTMAX) {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PL; ++i)
-      if (!((used >> i) & 1u)) m = fmaxf(m, v[i]);
+      if (lane + 64 * i < E) m = fmaxf(m, v[i]);
     mx = wave_max(m);
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < PL; ++i)
-      if (!((used >> i) & 1u)) sum += expf(v[i] - mx);
+      if (lane + 64 * i < E) sum += expf(v[i] - mx);
     denom = wave_sum(sum);
   }
   float my_v = 0.f;
   int my_i = 0;
   for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-    int bi = kNone;
+    uint64_t best = key[0];
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-      if (!((used >> i) & 1u) && (bi == kNone || v[i] > bv)) {
-        bv = v[i];
-        bi = lane + 64 * i;
-      }
+    for (int i = 1; i < PL; ++i) best = key[i] > best ? key[i] : best;
+    best = wave_max_u64(best);
+    const int bi = (int)~(uint32_t)best;   // a real entry: k <= E
+#pragma unroll
+    for (int i = 0; i < PL; ++i)
+      if (bi == lane + 64 * i) key[i] = 0ull;
+    if (lane == j) {
+      my_i = bi;
+      my_v = float_from_order_bits((uint32_t)(best >> 32));
     }
-    wave_argmax(bv, bi);
-    if ((bi & 63) == lane) used |= 1u << (bi >> 6);
-    if (lane == j) { my_v = bv; my_i = bi; }
   }
   float sc = 0.f;
   if (lane < k) {
@@ -81,9 +74,25 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
     const float tot = wave_sum(lane < k ? sc : 0.f);
     sc = sc / (tot + 1e-20f);
   }
+  pick = my_i;
+  weight = sc * scale;
+}
+
+template <int PL>
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int64_t T,
+                                                        int E, int64_t stride_t, int k, int scoring,
+                                                        int renorm, float scale,
+                                                        int64_t* __restrict__ ids,
+                                                        float* __restrict__ wout) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  int pick;
+  float weight;
+  route_token<PL>(logits + t * stride_t, E, k, scoring, renorm, scale, pick, weight);
   if (lane < k) {
-    ids[t * k + lane] = (int64_t)my_i;
-    wout[t * k + lane] = sc * scale;
+    ids[t * k + lane] = (int64_t)pick;
+    wout[t * k + lane] = weight;
   }
 }
 
@@ -131,39 +140,43 @@ SIMSD_DEV int upper_bound_lds(const int* arr, int n, int val) {
   return lo;
 }
 
-__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
-    const int64_t* __restrict__ ids, int M, int E, int num_tiles, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets, int32_t* __restrict__ perm,
-    int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
-  __shared__ int s_pos[SIMSD_MOE_MAX_EXPERTS + 1];   // histogram, then running position
-  __shared__ int s_off[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of counts
-  __shared__ int s_pad[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of padded counts
-  __shared__ int s_perm[SIMSD_MOE_MAX_SLOTS];
-  __shared__ int s_wa[32], s_wb[32];
+// LDS of the align step (one workgroup).
+struct AlignLds {
+  int key[SIMSD_MOE_MAX_SLOTS];         // expert of each slot, E for an invalid id
+  int pos[SIMSD_MOE_MAX_EXPERTS + 1];   // histogram, then running position
+  int off[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of counts
+  int pad[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of padded counts
+  int perm[SIMSD_MOE_MAX_SLOTS];
+  int wa[32], wb[32];
+};
+
+// The align tables from sm.key[0..M): called by every thread of the
+// workgroup after the keys are in LDS and visible (__syncthreads).
+SIMSD_DEV void align_from_keys(AlignLds& sm, int M, int E, int num_tiles, int32_t* __restrict__ counts,
+                               int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets,
+                               int32_t* __restrict__ perm, int32_t* __restrict__ slots,
+                               int32_t* __restrict__ tile_expert) {
   const int tid = threadIdx.x;
-  for (int e = tid; e <= E; e += kAlignThreads) s_pos[e] = 0;
+  for (int e = tid; e <= E; e += kAlignThreads) sm.pos[e] = 0;
   __syncthreads();
-  // 1. histogram; ids outside [0, E) go to bucket E (kept out of every group)
-  for (int i = tid; i < M; i += kAlignThreads) {
-    const int64_t e = ids[i];
-    atomicAdd(&s_pos[(e >= 0 && e < E) ? (int)e : E], 1);
-  }
+  // 1. histogram; bucket E collects ids outside [0, E) (kept out of every group)
+  for (int i = tid; i < M; i += kAlignThreads) atomicAdd(&sm.pos[sm.key[i]], 1);
   __syncthreads();
   // 2. scans (E <= 1024: one expert per thread)
-  const int c = tid < E ? s_pos[tid] : 0;
+  const int c = tid < E ? sm.pos[tid] : 0;
   const int pc = (c + kTile - 1) / kTile * kTile;
   int ec, epc, tc, tpc;
-  block_exclusive_scan2(c, pc, ec, epc, tc, tpc, s_wa, s_wb);
+  block_exclusive_scan2(c, pc, ec, epc, tc, tpc, sm.wa, sm.wb);
   if (tid < E) {
-    s_off[tid] = ec;
-    s_pad[tid] = epc;
+    sm.off[tid] = ec;
+    sm.pad[tid] = epc;
     counts[tid] = c;
     offsets[tid] = ec;
     pad_offsets[tid] = epc;
   }
   if (tid == 0) {
-    s_off[E] = tc;
-    s_pad[E] = tpc;
+    sm.off[E] = tc;
+    sm.pad[E] = tpc;
     offsets[E] = tc;
     pad_offsets[E] = tpc;
   }
@@ -171,46 +184,79 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
   // 3. stable scatter, one wave, 64 slots at a time in slot order
   if (tid < 64) {
     const int lane = tid;
-    for (int e = lane; e <= E; e += 64) s_pos[e] = s_off[e];   // bucket E starts at tc
+    for (int e = lane; e <= E; e += 64) sm.pos[e] = sm.off[e];   // bucket E starts at tc
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     int key_bits = 1;
     while ((1 << key_bits) <= E + 1) ++key_bits;
     for (int base = 0; base < M; base += 64) {
       const int i = base + lane;
-      int key = 0;   // 0: no slot; else expert + 1 (E + 1 = out of range)
-      if (i < M) {
-        const int64_t e = ids[i];
-        key = ((e >= 0 && e < E) ? (int)e : E) + 1;
-      }
+      const int key = i < M ? sm.key[i] + 1 : 0;   // 0: no slot; else bucket + 1
       uint64_t same = ~0ull;
-      for (int b = 0; b < key_bits; ++b) {
-        const bool bit = (key >> b) & 1;
+      for (int bt = 0; bt < key_bits; ++bt) {
+        const bool bit = (key >> bt) & 1;
         const uint64_t bb = __ballot(bit);
         same &= bit ? bb : ~bb;
       }
       const int rank = __popcll(same & lt_mask);
       const int leader = __ffsll((unsigned long long)same) - 1;
       int p = 0;
-      if (key > 0) p = s_pos[key - 1] + rank;
-      if (key > 0 && lane == leader) s_pos[key - 1] = p + __popcll(same);
-      if (key > 0) s_perm[p] = i;
+      if (key > 0) p = sm.pos[key - 1] + rank;
+      if (key > 0 && lane == leader) sm.pos[key - 1] = p + __popcll(same);
+      if (key > 0) sm.perm[p] = i;
     }
   }
   __syncthreads();
   // 4. outputs
-  for (int p = tid; p < M; p += kAlignThreads) perm[p] = s_perm[p];
+  for (int p = tid; p < M; p += kAlignThreads) perm[p] = sm.perm[p];
   const int total_rows = num_tiles * kTile;
   for (int q = tid; q < total_rows; q += kAlignThreads) {
-    const int e = upper_bound_lds(s_pad + 1, E, q);
+    const int e = upper_bound_lds(sm.pad + 1, E, q);
     int slot = -1;
     if (e < E) {
-      const int r = q - s_pad[e];
-      if (r < s_off[e + 1] - s_off[e]) slot = s_perm[s_off[e] + r];
+      const int r = q - sm.pad[e];
+      if (r < sm.off[e + 1] - sm.off[e]) slot = sm.perm[sm.off[e] + r];
     }
     slots[q] = slot;
   }
   for (int t = tid; t < num_tiles; t += kAlignThreads)
-    tile_expert[t] = upper_bound_lds(s_pad + 1, E, t * kTile);
+    tile_expert[t] = upper_bound_lds(sm.pad + 1, E, t * kTile);
+}
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
+    const int64_t* __restrict__ ids, int M, int E, int num_tiles, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
+  __shared__ AlignLds sm;
+  for (int i = threadIdx.x; i < M; i += kAlignThreads) {
+    const int64_t e = ids[i];
+    sm.key[i] = (e >= 0 && e < E) ? (int)e : E;
+  }
+  __syncthreads();
+  align_from_keys(sm, M, E, num_tiles, counts, offsets, pad_offsets, perm, slots, tile_expert);
+}
+
+// Route every token (one wave per token, 16 waves) and align the picks in
+// the same workgroup: the keys never leave LDS and the step saves a launch.
+template <int PL>
+__global__ __launch_bounds__(kAlignThreads) void moe_route_align_kernel(
+    const float* __restrict__ logits, int T, int E, int64_t stride_t, int k, int scoring, int renorm,
+    float scale, int64_t* __restrict__ ids, float* __restrict__ wout, int num_tiles,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
+  __shared__ AlignLds sm;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int t = wv; t < T; t += kAlignThreads / 64) {
+    int pick;
+    float weight;
+    route_token<PL>(logits + (int64_t)t * stride_t, E, k, scoring, renorm, scale, pick, weight);
+    if (lane < k) {
+      ids[(int64_t)t * k + lane] = (int64_t)pick;
+      wout[(int64_t)t * k + lane] = weight;
+      sm.key[t * k + lane] = pick;
+    }
+  }
+  __syncthreads();
+  align_from_keys(sm, T * k, E, num_tiles, counts, offsets, pad_offsets, perm, slots, tile_expert);
 }
 
 // ======================================================== grouped FFN ======
@@ -530,6 +576,42 @@ extern "C" int simsd_moe_align(const int64_t* ids, int64_t M, int64_t E, int num
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, stream, ids, (int)M, (int)E,
                      num_tiles, counts, offsets, pad_offsets, perm, slots, tile_expert);
   return check_launch("moe_align");
+}
+
+extern "C" int simsd_moe_route_align(const float* logits, int64_t T, int64_t E, int64_t stride_t,
+                                     int k, int scoring, int renorm, float scale, int64_t* ids_out,
+                                     float* w_out, int num_tiles, int32_t* counts, int32_t* offsets,
+                                     int32_t* pad_offsets, int32_t* perm, int32_t* slots,
+                                     int32_t* tile_expert, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (E <= 0 || E > SIMSD_MOE_MAX_EXPERTS)
+    return set_error("moe_route_align: need 0 < E <= %d (E=%lld)", SIMSD_MOE_MAX_EXPERTS, (long long)E);
+  if (k <= 0 || k > 64 || k > E) return set_error("moe_route_align: need 0 < k <= min(64, E) (k=%d)", k);
+  if (scoring != SIMSD_SCORE_SOFTMAX && scoring != SIMSD_SCORE_SIGMOID)
+    return set_error("moe_route_align: unknown scoring %d", scoring);
+  if (T < 0 || T * k > SIMSD_MOE_MAX_SLOTS)
+    return set_error("moe_route_align: need 0 <= T*k <= %d (got %lld)", SIMSD_MOE_MAX_SLOTS,
+                     (long long)(T * k));
+  if (num_tiles < 0 || (int64_t)num_tiles * kTile > ((int64_t)1 << 30))
+    return set_error("moe_route_align: bad num_tiles %d", num_tiles);
+  if (counts == nullptr || offsets == nullptr || pad_offsets == nullptr || slots == nullptr ||
+      tile_expert == nullptr ||
+      (T > 0 && (logits == nullptr || ids_out == nullptr || w_out == nullptr || perm == nullptr)))
+    return set_error("moe_route_align: null pointer");
+  const dim3 grid(1), block(kAlignThreads);
+  if (E <= 64)
+    hipLaunchKernelGGL((moe_route_align_kernel<1>), grid, block, 0, stream, logits, (int)T, (int)E, stride_t, k,
+                       scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets, pad_offsets, perm,
+                       slots, tile_expert);
+  else if (E <= 256)
+    hipLaunchKernelGGL((moe_route_align_kernel<4>), grid, block, 0, stream, logits, (int)T, (int)E, stride_t, k,
+                       scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets, pad_offsets, perm,
+                       slots, tile_expert);
+  else
+    hipLaunchKernelGGL((moe_route_align_kernel<16>), grid, block, 0, stream, logits, (int)T, (int)E, stride_t, k,
+                       scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets, pad_offsets, perm,
+                       slots, tile_expert);
+  return check_launch("moe_route_align");
 }
 
 extern "C" int64_t simsd_moe_workspace_bytes(int64_t T, int k, int64_t H, int64_t I, int64_t Is,

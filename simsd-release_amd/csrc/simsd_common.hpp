@@ -391,35 +391,42 @@ SIMSD_DEV float wave_sum(float v) {
   return wave_allreduce(v, [](float a, float b) { return a + b; });
 }
 
-// Largest (v, i) over the wave: larger v first, then smaller i; i == INT_MAX
-// marks an empty lane.  Every lane gets the winner (a total order: no
-// per-lane rounding differences).
-SIMSD_DEV bool argmax_take(float ov, int oi, float bv, int bi) {
-  return oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+// Largest 64-bit key over the wave, on every lane.  Route keys are
+// (order-preserving bits of the logit) << 32 | ~index, so the maximum is the
+// largest logit and, among equal logits, the lowest index; 0 marks an entry
+// that is taken or absent.
+SIMSD_DEV uint32_t float_order_bits(float f) {
+  uint32_t b = __float_as_uint(f);
+  if (b == 0x80000000u) b = 0u;   // -0 == +0: equal keys, so ties go by index
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
-SIMSD_DEV void wave_argmax(float& v, int& i) {
-  auto stage = [&](int pv_bits, int pi) {
-    const float pv = __int_as_float(pv_bits);
-    if (argmax_take(pv, pi, v, i)) { v = pv; i = pi; }
+SIMSD_DEV float float_from_order_bits(uint32_t o) {
+  return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+SIMSD_DEV uint64_t wave_max_u64(uint64_t key) {
+  auto take = [&](uint32_t lo, uint32_t hi) {
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    key = o > key ? o : key;
   };
-  stage(dpp_quad_xor1(__float_as_int(v)), dpp_quad_xor1(i));
-  stage(dpp_quad_xor2(__float_as_int(v)), dpp_quad_xor2(i));
-  stage(dpp_row_ror4(__float_as_int(v)), dpp_row_ror4(i));
-  stage(dpp_row_ror8(__float_as_int(v)), dpp_row_ror8(i));
+  auto lo = [&]() { return (int)(uint32_t)key; };
+  auto hi = [&]() { return (int)(uint32_t)(key >> 32); };
+  take((uint32_t)dpp_quad_xor1(lo()), (uint32_t)dpp_quad_xor1(hi()));
+  take((uint32_t)dpp_quad_xor2(lo()), (uint32_t)dpp_quad_xor2(hi()));
+  take((uint32_t)dpp_row_ror4(lo()), (uint32_t)dpp_row_ror4(hi()));
+  take((uint32_t)dpp_row_ror8(lo()), (uint32_t)dpp_row_ror8(hi()));
   {
-    const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    const auto ri = __builtin_amdgcn_permlane16_swap((uint32_t)i, (uint32_t)i, false, false);
-    v = __uint_as_float(rv[0]);
-    i = (int)ri[0];
-    stage(__float_as_int(__uint_as_float(rv[1])), (int)ri[1]);
+    const auto l = __builtin_amdgcn_permlane16_swap((uint32_t)lo(), (uint32_t)lo(), false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap((uint32_t)hi(), (uint32_t)hi(), false, false);
+    key = ((uint64_t)h[0] << 32) | l[0];
+    take(l[1], h[1]);
   }
   {
-    const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    const auto ri = __builtin_amdgcn_permlane32_swap((uint32_t)i, (uint32_t)i, false, false);
-    v = __uint_as_float(rv[0]);
-    i = (int)ri[0];
-    stage(__float_as_int(__uint_as_float(rv[1])), (int)ri[1]);
+    const auto l = __builtin_amdgcn_permlane32_swap((uint32_t)lo(), (uint32_t)lo(), false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap((uint32_t)hi(), (uint32_t)hi(), false, false);
+    key = ((uint64_t)h[0] << 32) | l[0];
+    take(l[1], h[1]);
   }
+  return key;
 }
 
 }  // namespace simsd

@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -39,6 +39,8 @@ SIGNATURES = {
     "simsd_moe_route_topk": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
     "simsd_moe_num_tiles": (_i32, [_i64, _i64]),
     "simsd_moe_align": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "simsd_moe_route_align": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _vp, _vp,
+                                      _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "simsd_moe_workspace_bytes": (_i64, [_i64, _i32, _i64, _i64, _i64, _i32]),
     "simsd_moe_grouped_ffn": (_i32, [
         _vp, _i64, _i64,                 # x

@@ -4,8 +4,9 @@ Keeps the reference's public surface (kernels/moe_dispatch_fused.py:29-231):
 ``moe_dispatch(x, topk_ids, topk_weight, w_gate, w_up, w_down)``,
 ``stack_expert_weights``, ``FusedMoEDispatch``, ``BLOCK_M``, ``_align`` and
 ``_num_tiles``; adds the routing step the reference leaves to the remote
-LLaDA2 gate (``moe_route``), the align outputs as a record (``moe_align``) and
-the whole step with a shared expert (``moe_forward``).
+LLaDA2 gate (``moe_route``), the align outputs as a record (``moe_align``),
+both in one launch (``moe_route_align``) and the whole step with a shared
+expert (``moe_forward``).
 
 Kernels (``csrc/moe.hip``, C ABI in ``include/simsd_kernels.h``):
   route    one wave per token: top-k over the E logits (ties -> lower index),
@@ -205,6 +206,59 @@ def moe_dispatch(x, topk_ids, topk_weight, w_gate, w_up, w_down):
     return _grouped_ffn(x, topk_ids, topk_weight, w_gate, w_up, w_down, slots, tile_expert)
 
 
+# Up to this many tokens (one per wave of the single workgroup), routing and
+# align run as one launch; beyond it, as two launches (routing in parallel).
+FUSED_ROUTE_MAX_T = 16
+
+
+def moe_route_align(logits: torch.Tensor, k: int, E: int | None = None, scoring: str = "softmax",
+                    renorm: bool = True, scale: float = 1.0, num_tiles: int | None = None):
+    """``moe_route`` followed by ``moe_align`` of its ids, in one launch.
+
+    Returns (topk_ids, topk_weight, MoeAlignment), identical to the two calls
+    in sequence.
+    """
+    if logits.ndim != 2:
+        raise ValueError(f"logits must be (T, E), got {tuple(logits.shape)}")
+    if scoring not in _SCORING:
+        raise ValueError(f"scoring must be one of {sorted(_SCORING)}, got {scoring!r}")
+    dev = _native.require_device(logits)
+    T, El = logits.shape
+    E = El if E is None else E
+    if E != El:
+        raise ValueError(f"E={E} but logits have {El} columns")
+    if not 0 < E <= _native.MOE_MAX_EXPERTS:
+        raise ValueError(f"E={E} outside 1..{_native.MOE_MAX_EXPERTS}")
+    if not 0 < k <= min(64, E):
+        raise ValueError(f"need 0 < k <= min(64, E={E}), got k={k}")
+    M = T * k
+    if M > _native.MOE_MAX_SLOTS:
+        raise ValueError(f"T*k={M} exceeds {_native.MOE_MAX_SLOTS} slots")
+    if num_tiles is None:
+        num_tiles = _num_tiles(M, E)
+    lg = logits
+    if lg.dtype != torch.float32:
+        lg = lg.float()
+    if lg.stride(1) != 1:
+        lg = lg.contiguous()
+    ids = torch.empty((T, k), device=dev, dtype=torch.int64)
+    w = torch.empty((T, k), device=dev, dtype=torch.float32)
+    i32 = dict(device=dev, dtype=torch.int32)
+    al = MoeAlignment(
+        counts=torch.empty(E, **i32), offsets=torch.empty(E + 1, **i32),
+        pad_offsets=torch.empty(E + 1, **i32), perm=torch.empty(M, **i32),
+        slots=torch.empty(num_tiles * BLOCK_M, **i32), tile_expert=torch.empty(num_tiles, **i32))
+    lib = _native.lib()
+    with _native.device_guard(dev):
+        st = lib.simsd_moe_route_align(
+            lg.data_ptr(), T, E, lg.stride(0), k, _SCORING[scoring], int(bool(renorm)), float(scale),
+            ids.data_ptr(), w.data_ptr(), num_tiles, al.counts.data_ptr(), al.offsets.data_ptr(),
+            al.pad_offsets.data_ptr(), al.perm.data_ptr(), al.slots.data_ptr(),
+            al.tile_expert.data_ptr(), _native.stream_of(dev))
+    _native.check(st, "moe_route_align")
+    return ids, w, al
+
+
 def moe_forward(x, router_logits, k, w_gate, w_up, w_down, shared=None,
                 scoring: str = "softmax", renorm: bool = True, scale: float = 1.0):
     """Route + dispatch + shared expert in one graph-capturable sequence.
@@ -213,9 +267,14 @@ def moe_forward(x, router_logits, k, w_gate, w_up, w_down, shared=None,
     output is added to the routed output in x's dtype, as the LLaDA2 forward
     adds ``shared_experts(x)`` after ``moe_infer``.
     """
-    ids, w = moe_route(router_logits, k, scoring=scoring, renorm=renorm, scale=scale)
     E = w_gate.shape[0]
-    slots, tile_expert = _align(ids, E, _num_tiles(ids.numel(), E))
+    T = router_logits.shape[0]
+    if 0 < T <= FUSED_ROUTE_MAX_T and T * k <= _native.MOE_MAX_SLOTS:
+        ids, w, al = moe_route_align(router_logits, k, E, scoring=scoring, renorm=renorm, scale=scale)
+        slots, tile_expert = al.slots, al.tile_expert
+    else:
+        ids, w = moe_route(router_logits, k, scoring=scoring, renorm=renorm, scale=scale)
+        slots, tile_expert = _align(ids, E, _num_tiles(ids.numel(), E))
     return _grouped_ffn(x, ids, w, w_gate, w_up, w_down, slots, tile_expert, shared=shared)
 
 

@@ -117,6 +117,27 @@ def test_align_random_vs_oracle():
         _check_align(al, omoe.align(ids, E))
 
 
+@pytest.mark.parametrize("scoring,renorm,scale", [("softmax", False, 1.0), ("sigmoid", True, 2.5)])
+def test_route_align_fused_equals_two_calls(scoring, renorm, scale):
+    """One launch (route + align) gives exactly the two calls' outputs, and
+    the ids and tables match the oracle."""
+    from kernels.moe_dispatch_fused import moe_align, moe_route, moe_route_align
+    g = torch.Generator(device=DEV).manual_seed(21)
+    for T, E, k in [(1, 8, 1), (4, 256, 8), (16, 256, 8), (64, 256, 8), (5, 13, 3), (33, 1000, 6),
+                    (1024, 256, 8), (3, 64, 64)]:
+        logits = torch.randn(T, E, device=DEV, generator=g)
+        ids1, w1 = moe_route(logits, k, scoring=scoring, renorm=renorm, scale=scale)
+        al1 = moe_align(ids1, E)
+        ids2, w2, al2 = moe_route_align(logits, k, scoring=scoring, renorm=renorm, scale=scale)
+        assert torch.equal(ids1, ids2) and torch.equal(w1, w2), (T, E, k)
+        for name in al1._fields:
+            assert torch.equal(getattr(al1, name), getattr(al2, name)), (T, E, k, name)
+        ids_ref, _ = omoe.route_topk(logits.cpu().numpy().astype(np.float64), k, scoring=scoring,
+                                     renorm=renorm, scale=scale)
+        assert np.array_equal(ids2.cpu().numpy(), ids_ref), (T, E, k)
+        _check_align(al2, omoe.align(ids_ref, E))
+
+
 def test_align_max_slots():
     from kernels.moe_dispatch_fused import moe_align
     rng = np.random.default_rng(12)
