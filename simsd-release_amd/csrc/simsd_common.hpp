@@ -335,6 +335,75 @@ SIMSD_DEV void accum_lds(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
   }
 }
 
+// accum_lds with the B operand staged the same way: B block cb is 16
+// consecutive rows of one matrix (rows 16 cb .. 16 cb + 15, stride b_sn bytes,
+// rows >= b_rows read zero), loaded as 4 rows x 256 B per instruction into
+// LDS rows 16 RB + 16 cb + ... of the wave's tile and read back in the B
+// layout.  Whole cache lines per load instead of 64 bytes of 16 rows, for
+// activations that every workgroup re-reads from L2.  The tile holds
+// 16 (RB + CB) rows.
+template <int DT, int RB, int CB, int U>
+SIMSD_DEV void accum_lds_ab(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
+                            const uint32_t (&a_sn)[RB], rsrc_t rbx, uint32_t b_sn, int b_rows, int c0,
+                            int c1, uint32_t Kb, char* tile, f32x4_t (&acc)[RB][CB]) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, r = lane & 15;     // MFMA operand layout
+  const int lr = lane >> 4, lc = lane & 15;   // loader layout: row l/16 of 4, chunk l%16
+  for (int c = c0; c < c1; c += U) {
+    u32x4_t W[U][RB][4], X[U][CB][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = c + u < c1;
+      const uint32_t k = (uint32_t)(c + u) * kStep4Bytes + lc * kLaneBytes;
+      const bool kok = live && k < Kb;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          W[u][rb][q] = buf_load16<kAuxStream>(
+              ra[rb], kok ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = 16 * cb + 4 * q + lr;
+          X[u][cb][q] = buf_load16<kAuxKeep>(rbx, kok && row < b_rows ? (uint32_t)row * b_sn + k : kOob);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<u32x4_t*>(tile + (16 * rb + 4 * q + lr) * kLdsRow + lc * kLaneBytes) = W[u][rb][q];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<u32x4_t*>(tile + (16 * (RB + cb) + 4 * q + lr) * kLdsRow + lc * kLaneBytes) =
+              X[u][cb][q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x4_t A[RB], B[CB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          A[rb] = *reinterpret_cast<const u32x4_t*>(tile + (16 * rb + r) * kLdsRow + j * kStepBytes +
+                                                    g * kLaneBytes);
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          B[cb] = *reinterpret_cast<const u32x4_t*>(tile + (16 * (RB + cb) + r) * kLdsRow +
+                                                    j * kStepBytes + g * kLaneBytes);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = Mfma<DT>::step(A[rb], B[cb], acc[rb][cb]);
+      }
+    }
+  }
+}
+
 // Sum the per-wave accumulators of KS waves that split the reduction, in a
 // fixed wave order (bit-reproducible).  Wave 0 ends up with the total.
 template <int KS, int NFRAG>

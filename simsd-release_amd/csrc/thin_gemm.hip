@@ -22,6 +22,9 @@
 #ifndef SIMSD_THIN_U
 #define SIMSD_THIN_U 8   // k-steps per batch at one A and one B block
 #endif
+#ifndef SIMSD_LDS_X
+#define SIMSD_LDS_X 1    // 9..32 tokens: stage the activations through LDS too
+#endif
 
 
 namespace simsd {
@@ -302,7 +305,12 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int NF = RB * CB;
   constexpr int ROWS = 16 * RB;
-  __shared__ __attribute__((aligned(16))) char tile[KS][ROWS * kLdsRow];
+  // the waves' LDS tiles, reused for the cross-wave reduction once all waves
+  // are past their main loop
+  constexpr int kTileRows = ROWS + (SIMSD_LDS_X ? 16 * CB : 0);
+  constexpr int kTileBytes = KS * kTileRows * kLdsRow;
+  constexpr int kRedBytes = (KS > 1 ? (KS - 1) * NF * 4 * 64 : 1) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
   const int lane = threadIdx.x & 63;
   const int wk = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
@@ -343,10 +351,14 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
     boff[cb] = (uint32_t)(cb * 16 + r) * sxm_b;
     bok[cb] = cb * 16 + r < cols_valid;
   }
-  accum_lds<DT, RB, CB, U>(ra, a_row0, a_sn, rB, boff, bok, w0, w1, Kb, tile[wk], acc);
+  if (SIMSD_LDS_X)
+    accum_lds_ab<DT, RB, CB, U>(ra, a_row0, a_sn, rB, sxm_b, (int)cols_valid, w0, w1, Kb,
+                                smem + wk * kTileRows * kLdsRow, acc);
+  else
+    accum_lds<DT, RB, CB, U>(ra, a_row0, a_sn, rB, boff, bok, w0, w1, Kb, smem + wk * kTileRows * kLdsRow, acc);
 
-  __shared__ float red[KS > 1 ? (KS - 1) * NF * 4 * 64 : 1];
-  reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, red);
+  __syncthreads();   // every wave done with its tile before the partials overwrite it
+  reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, reinterpret_cast<float*>(smem));
   if (wk != 0) return;
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -438,7 +450,6 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
   if (rows != 4 && rows != 8 && rows != 16 && rows != 32)
     return set_error("thin_linear: block_n must be 4, 8, 16 or 32 (got %d)", block_n);
   if (kind == 2 && rows < 16) rows = 16;   // whole 16-row MFMA blocks
-  if (kind == 2 && pl.ks > 4) pl.ks = 4;   // per-wave LDS tiles
   pl.rows = rows;
   pl.rt = rows >= 16 ? 16 : rows;
   pl.rb = rows >= 16 ? rows / 16 : 1;
@@ -570,8 +581,11 @@ void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 
 template <int DT, int RB, int CB>
 void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  if (pl.ks == 2) launch_lds<DT, RB, CB, 2>(pl, args, stream);
-  else launch_lds<DT, RB, CB, 4>(pl, args, stream);
+  switch (pl.ks) {
+    case 2: launch_lds<DT, RB, CB, 2>(pl, args, stream); break;
+    case 8: launch_lds<DT, RB, CB, 8>(pl, args, stream); break;
+    default: launch_lds<DT, RB, CB, 4>(pl, args, stream); break;
+  }
 }
 
 template <int DT>
@@ -581,7 +595,7 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
       if (pl.ms == 1) gemv4_rows<DT, 1>(pl, args, stream);
       else gemv4_rows<DT, 2>(pl, args, stream);
     } else if (pl.kind == 2) {
-      const bool two_rows = pl.rows == 32;
+      const bool two_rows = pl.rows == 32;   // 16-row blocks x 16-token blocks
       if (pl.cb == 1) { if (two_rows) lds_ks<DT, 2, 1>(pl, args, stream); else lds_ks<DT, 1, 1>(pl, args, stream); }
       else { if (two_rows) lds_ks<DT, 2, 2>(pl, args, stream); else lds_ks<DT, 1, 2>(pl, args, stream); }
     }

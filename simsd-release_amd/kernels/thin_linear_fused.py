@@ -123,11 +123,11 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     (2048, 12288): (16, 16, 256, 1, 2, 2),    # merged gate+up     10.0 us
     # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
     (4096, 12288): (32, 32, 256, 1, 4, 2),    # gate_proj / up_proj
-    (4096, 4096): (32, 16, 256, 1, 4, 2),     # q_proj, o_proj      9.0 / 12.8 us (M=16 / 32)
+    (4096, 4096): (32, 16, 256, 1, 8, 2),     # q_proj, o_proj      8.7 / 11.2 us (M=16 / 32)
     (4096, 1024): (32, 16, 256, 4, 4, 2),     # k_proj, v_proj
-    (4096, 6144): (32, 32, 256, 1, 4, 2),     # merged qkv         12.1 / 16.4 us
-    (4096, 24576): (32, 32, 256, 1, 4, 2),    # merged gate+up     34.1 / 45.2 us
-    (12288, 4096): (32, 32, 256, 2, 4, 2),    # down_proj          21.6 / 27.4 us
+    (4096, 6144): (32, 32, 256, 1, 4, 2),     # merged qkv         12.3 / 15.7 us
+    (4096, 24576): (32, 32, 256, 1, 4, 2),    # merged gate+up     33.4 / 39.3 us
+    (12288, 4096): (32, 16, 256, 1, 8, 2),    # down_proj          21.5 / 25.8 us
     (4096, 151936): (32, 32, 256, 1, 4, 2),   # lm_head
 }
 
