@@ -350,6 +350,25 @@ def test_oracle_other_row_counts(M):
     _oracle_check(M, 2048, 1536, seed=M)
 
 
+@pytest.mark.parametrize("M", [1, 3, 4, 8, 9, 16, 32])
+def test_fp16_every_kernel(M):
+    """fp16 through the GEMV (M <= 8), the LDS kernel (M > 8) and the strided
+    path, against the oracle's exact sum rounded to fp16, within the
+    reference's 16-bit bound."""
+    from kernels.thin_linear_fused import thin_linear
+    for K, N in [(2048, 2048), (1000, 531)]:
+        x = rnd(M, K, dtype=torch.float16, seed=40 + M)
+        w = rnd(N, K, dtype=torch.float16, scale=0.02, seed=41 + K)
+        ref = othin.linear_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), dtype="fp16")
+        amax = float(np.abs(ref).max())
+        with torch.inference_mode():
+            for xv in (x, x.t().contiguous().t()):    # contiguous, then a strided view
+                got = thin_linear(xv, w).float().cpu().numpy()
+                err = float(np.abs(got - ref).max())
+                assert err <= othin.tolerance(amax, "fp16"), (M, K, N, err)
+                assert othin.max_abs_rel(got, ref) <= 1e-2
+
+
 # ───────────────────────────────────────────── size-independent properties ───
 def test_properties_at_full_size():
     from kernels.thin_linear_fused import thin_linear
