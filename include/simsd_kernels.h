@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 3
+#define SIMSD_ABI_VERSION 4
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -77,6 +77,27 @@ int64_t simsd_thin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K, int d
  * pick_config / _heuristic_config, kernels/thin_linear_fused.py:217-262. */
 int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype, int block_n,
                            int split_k, int num_waves, int* out4);
+
+/* ---- gated projection ----------------------------------------------------
+ * h[m, i] = dtype( dtype(silu(dtype(g))) * dtype(u) ),
+ *   g = sum_k x[m, k] w_gate[i, k],  u = sum_k x[m, k] w_up[i, k]  (fp32 sums)
+ * -- the rounding points of a bf16/fp16 act_fn(gate_proj(x)) * up_proj(x) in
+ * PyTorch -- in one pass over both weights, with no [M, 2I] intermediate.
+ * Fuses the gate and up projections of an MLP block with its SiLU and
+ * product, modeling_sdar.py:113-119 (SDARMLP.forward, a caller of
+ * thin_linear); no single reference entry point.  A merged [2I, K] gate_up
+ * weight is w_gate = its first I rows and w_up = the rest.
+ *   bf16/fp16 only; x, w_gate and w_up K-contiguous, 16-byte aligned rows.
+ *   block_n: gate + up rows per workgroup (8, 16 or 32; 0 = automatic), i.e.
+ *            block_n / 2 output columns; other arguments as simsd_thin_linear;
+ *   workspace (split_k > 1): simsd_thin_linear_workspace_bytes(M, 2*I, K, ...). */
+int simsd_thin_linear_silu_mul(const void* x, int64_t stride_xm, int64_t stride_xk,
+                               const void* w_gate, int64_t stride_gn, int64_t stride_gk,
+                               const void* w_up, int64_t stride_un, int64_t stride_uk,
+                               void* h, int64_t stride_hm, int64_t stride_hn,
+                               int64_t M, int64_t I, int64_t K, int dtype,
+                               int block_n, int block_k, int split_k, int num_waves,
+                               void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- MoE: routing ------------------------------------------------------
  * ids_out[t, j] (int64) = index of the j-th largest logit of row t (ties to

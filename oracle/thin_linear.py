@@ -11,6 +11,9 @@ plus bias (``y += bias`` after the GEMM, kernels/thin_linear_fused.py:343-344).
 ``linear_cpu_torch``  torch's CPU ``F.linear`` in the input dtype -- the
                       reference's own oracle run on the host; also the timed
                       CPU path of the benchmark.
+``gated_exact``       silu(x w_gate^T) * (x w_up^T) with the rounding points of
+                      a bf16/fp16 SDARMLP (modeling_sdar.py:113-119): each
+                      projection, the SiLU and the product rounded to the dtype.
 ``tolerance``         the reference's bounds (thin_linear_fused_test.py:28-32).
 """
 from __future__ import annotations
@@ -33,6 +36,15 @@ def linear_exact(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None,
     if bias is not None:
         y = ROUNDERS[dtype](y + np.asarray(bias, dtype=np.float64)[None, :])
     return y
+
+
+def gated_exact(x: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """h = rnd(rnd(silu(g)) * u) with g = linear_exact(x, w_gate), u = linear_exact(x, w_up);
+    the SiLU in fp64 (v / (1 + e^-v)) before its rounding."""
+    rnd = ROUNDERS[dtype]
+    g = linear_exact(x, w_gate, dtype=dtype)
+    u = linear_exact(x, w_up, dtype=dtype)
+    return rnd(rnd(g / (1.0 + np.exp(-g))) * u)
 
 
 def linear_cpu_torch(x, w, bias=None):

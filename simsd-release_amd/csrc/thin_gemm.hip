@@ -38,8 +38,10 @@ struct ThinArgs {
   int64_t sb;
   char* y;
   int64_t sym, syn;
-  float* part;               // [split][M][N] fp32 partials when split > 1
-  int64_t M, N, K;
+  float* part;               // [split][M][N] fp32 partials when split > 1 ([split][M][2N] gated)
+  const char* w2;            // gated (SiLU-mul) kernels: the up matrix, row stride sw2n
+  int64_t sw2n;
+  int64_t M, N, K;           // gated: N = output columns (rows of each of w, w2)
   int steps;                 // ceil(K * esize / 64)
   int steps_per_split;
 };
@@ -149,6 +151,31 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
 //   CH  load steps (128 k elements each) whose activations are held at once
 //   GB  row groups whose loads are issued together
 
+// Gated output: h = dtype(dtype(silu(dtype(g))) * dtype(u)), the rounding
+// points of a bf16 act_fn(gate_proj(x)) * up_proj(x) in PyTorch.
+template <int DT>
+SIMSD_DEV float silu_mul(float g, float u) {
+  const float gr = round_to<DT>(g);
+  const float sv = round_to<DT>(gr / (1.f + expf(-gr)));
+  return sv * round_to<DT>(u);
+}
+
+// Write one output (or its split partial).  Gated: g at column n, u at
+// column N + n of the partial row.
+template <int DT, bool PARTIAL, bool GLU>
+SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, float v, float u) {
+  if (PARTIAL) {
+    const int64_t row = ((int64_t)split_id * a.M + m) * (GLU ? 2 * a.N : a.N);
+    a.part[row + n] = v;
+    if (GLU) a.part[row + a.N + n] = u;
+  } else if (GLU) {
+    store_elem<DT>(a.y, m * a.sym + n * a.syn, silu_mul<DT>(v, u));
+  } else {
+    if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+    store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
+  }
+}
+
 // Sum NV per-lane values over lane bits 5, 4 and the row bits from log2(LO)
 // up to 3.  Bits 5 and 4 by reduce-scatter on the gfx950 lane swaps:
 // v_permlane32_swap(a, b) leaves [a.lo, b.lo] / [a.hi, b.hi], so one swap and
@@ -186,16 +213,19 @@ __device__ __forceinline__ void reduce_lanes(float (&val)[NV]) {
   }
 }
 
-template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL>
+template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU>
 __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int G = RW / 4;
   static_assert(RW % 4 == 0 && G % GB == 0, "row groups");
+  static_assert(!GLU || (G % 2 == 0 && (G / 2) % GB == 0), "gated: gate and up halves of whole batches");
+  // gated: groups [0, G/2) are gate rows, [G/2, G) the same rows of up
+  constexpr int OUT = GLU ? RW / 2 : RW;   // output columns per workgroup
   const int lane = threadIdx.x & 63;
   const int wk = threadIdx.x >> 6;
   const int i4 = lane & 3;          // A row / B column within a block
   const int b4 = lane >> 2;         // 4x4x4 block = 8-element k chunk of a load step
-  const int64_t n_tile = (int64_t)blockIdx.x * RW;
+  const int64_t n_tile = (int64_t)blockIdx.x * OUT;
   const int64_t m_tile = (int64_t)blockIdx.z * (4 * MS);
   const int split_id = blockIdx.y;
 
@@ -208,9 +238,12 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
 
   const uint32_t Kb = (uint32_t)(a.K * ES);
   const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
-  const int64_t rows_valid = min((int64_t)RW, a.N - n_tile);
+  const uint32_t sw2n_b = (uint32_t)(a.sw2n * ES);
+  const int64_t rows_valid = min((int64_t)OUT, a.N - n_tile);
   const int64_t cols_valid = min((int64_t)(4 * MS), a.M - m_tile);
   const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
+  const rsrc_t rA2 = GLU ? make_rsrc(a.w2 + n_tile * a.sw2n * ES, (uint32_t)(rows_valid - 1) * sw2n_b + Kb)
+                         : rA;
   const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
   const uint32_t lane_k = (uint32_t)(b4 * kLaneBytes);
 
@@ -239,12 +272,13 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
       u32x4_t A[GB][CH];
 #pragma unroll
       for (int gg = 0; gg < GB; ++gg) {
-        const uint32_t roff = (uint32_t)(4 * (g0 + gg) + i4) * swn_b;
+        const bool up = GLU && g0 + gg >= G / 2;
+        const uint32_t roff = (uint32_t)(4 * (up ? g0 + gg - G / 2 : g0 + gg) + i4) * (up ? sw2n_b : swn_b);
 #pragma unroll
         for (int s = 0; s < CH; ++s) {
           const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
           const bool ok = (c0 + s < c_lim) && (k < Kb);
-          A[gg][s] = buf_load16<kAuxStream>(rA, ok ? roff + k : kOob);
+          A[gg][s] = buf_load16<kAuxStream>(up ? rA2 : rA, ok ? roff + k : kOob);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -278,19 +312,16 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
     for (int p = 0; p < NV / 4; ++p) red[(wk * NV + q0 + p) * 4 + i4] = val[p];
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < G * MS * 16; e += 64 * KS) {
+  for (int e = threadIdx.x; e < (GLU ? G / 2 : G) * MS * 16; e += 64 * KS) {
     const int j = e & 3, v = (e >> 2) & 3, c = (e >> 4) % MS, g = (e >> 4) / MS;
     const int64_t n = n_tile + 4 * g + v;
     const int64_t m = m_tile + 4 * c + j;
     if (n < a.N && m < a.M) {
-      float t = 0.f;
+      float t = 0.f, u = 0.f;
       for (int w = 0; w < KS; ++w) t += red[((w * G + g) * MS + c) * 16 + v * 4 + j];
-      if (PARTIAL) {
-        a.part[((int64_t)split_id * a.M + m) * a.N + n] = t;
-      } else {
-        if (a.bias != nullptr) t += load_elem<DT>(a.bias, n * a.sb);
-        store_elem<DT>(a.y, m * a.sym + n * a.syn, t);
-      }
+      if (GLU)
+        for (int w = 0; w < KS; ++w) u += red[((w * G + g + G / 2) * MS + c) * 16 + v * 4 + j];
+      put_out<DT, PARTIAL, GLU>(a, split_id, m, n, t, u);
     }
   }
 }
@@ -300,11 +331,13 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
 // 256 bytes per instruction, the GEMV's access pattern) through a per-wave LDS
 // tile (accum_lds).  Activations are the B operand as in thin_gemm_kernel.
 
-template <int DT, int RB, int CB, int KS, int U, bool PARTIAL>
+template <int DT, int RB, int CB, int KS, int U, bool PARTIAL, bool GLU>
 __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int NF = RB * CB;
   constexpr int ROWS = 16 * RB;
+  static_assert(!GLU || RB == 2, "gated: block 0 = gate rows, block 1 = the same rows of up");
+  constexpr int OUT = GLU ? 16 : ROWS;   // output columns per workgroup
   // the waves' LDS tiles, reused for the cross-wave reduction once all waves
   // are past their main loop
   constexpr int kTileRows = ROWS + (SIMSD_LDS_X ? 16 * CB : 0);
@@ -314,7 +347,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
   const int lane = threadIdx.x & 63;
   const int wk = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int64_t n_tile = (int64_t)blockIdx.x * ROWS;
+  const int64_t n_tile = (int64_t)blockIdx.x * OUT;
   const int64_t m_tile = (int64_t)blockIdx.z * (CB * 16);
   const int split_id = blockIdx.y;
 
@@ -328,7 +361,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
 
   const uint32_t Kb = (uint32_t)(a.K * ES);
   const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
-  const int64_t rows_valid = min((int64_t)ROWS, a.N - n_tile);
+  const int64_t rows_valid = min((int64_t)OUT, a.N - n_tile);
   const int64_t cols_valid = min((int64_t)(CB * 16), a.M - m_tile);
   const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
   const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
@@ -346,6 +379,12 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
     a_row0[rb] = (uint32_t)(16 * rb) * swn_b;
     a_sn[rb] = swn_b;
   }
+  if (GLU) {
+    const uint32_t sw2n_b = (uint32_t)(a.sw2n * ES);
+    ra[RB - 1] = make_rsrc(a.w2 + n_tile * a.sw2n * ES, (uint32_t)(rows_valid - 1) * sw2n_b + Kb);
+    a_row0[RB - 1] = 0u;
+    a_sn[RB - 1] = sw2n_b;
+  }
 #pragma unroll
   for (int cb = 0; cb < CB; ++cb) {
     boff[cb] = (uint32_t)(cb * 16 + r) * sxm_b;
@@ -361,7 +400,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
   reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, reinterpret_cast<float*>(smem));
   if (wk != 0) return;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int rb = 0; rb < (GLU ? 1 : RB); ++rb)
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
       const int64_t m = m_tile + cb * 16 + r;
@@ -370,15 +409,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t n = nb + j;
-          if (n < a.N) {
-            float v = acc[rb][cb][j];
-            if (PARTIAL) {
-              a.part[((int64_t)split_id * a.M + m) * a.N + n] = v;
-            } else {
-              if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
-              store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
-            }
-          }
+          if (n < a.N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
         }
       }
     }
@@ -390,10 +421,20 @@ template <int DT>
 __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restrict__ part, int split,
                                                           int64_t M, int64_t N,
                                                           const char* bias, int64_t sb, char* y,
-                                                          int64_t sym, int64_t syn) {
+                                                          int64_t sym, int64_t syn, int glu) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= M * N) return;
   const int64_t m = e / N, n = e % N;
+  if (glu) {   // partial rows hold g in [0, N) and u in [N, 2N)
+    float g = 0.f, u = 0.f;
+    for (int s = 0; s < split; ++s) {
+      const float* row = part + ((int64_t)s * M + m) * 2 * N;
+      g += row[n];
+      u += row[N + n];
+    }
+    store_elem<DT>(y, m * sym + n * syn, silu_mul<DT>(g, u));
+    return;
+  }
   float v = 0.f;
   for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + e];
   if (bias != nullptr) v += load_elem<DT>(bias, n * sb);
@@ -408,6 +449,7 @@ namespace {
 // kind 2: thin_gemm_lds_kernel (16x16x32 MFMA via LDS; M > 8, bf16/fp16, vector-capable)
 struct ThinPlan {
   int kind;
+  bool glu;                  // gated: rows are half gate, half up; outputs = rows / 2
   int rows, rt, rb, cb, ms, ks, ch, split;
   bool fast;
   int64_t tiles_n, tiles_m;
@@ -429,9 +471,10 @@ inline int fast_kind(int64_t M, int dtype) { return dtype == kF32 ? 0 : (M <= 8 
 // when even 4-row tiles leave more than half the CUs idle (0 = automatic),
 // keeping at least 256 bytes of every row per wave and split.
 int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int dtype, int block_n,
-                  int block_k, int num_waves, int split_k) {
+                  int block_k, int num_waves, int split_k, bool glu = false) {
   const int es = esize_of(dtype);
   pl.kind = kind;
+  pl.glu = glu;
   // GEMV activations held per chunk: 256 (2 load steps) or 1024 (8) k elements
   pl.ch = block_k >= 512 ? 8 : 2;
   pl.cb = M <= 16 ? 1 : 2;
@@ -450,6 +493,8 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
   if (rows != 4 && rows != 8 && rows != 16 && rows != 32)
     return set_error("thin_linear: block_n must be 4, 8, 16 or 32 (got %d)", block_n);
   if (kind == 2 && rows < 16) rows = 16;   // whole 16-row MFMA blocks
+  if (glu && kind == 1 && rows < 8) rows = 8;    // gated GEMV: a gate and an up row group
+  if (glu && kind == 2) rows = 32;               // gated LDS kernel: a gate and an up block
   pl.rows = rows;
   pl.rt = rows >= 16 ? 16 : rows;
   pl.rb = rows >= 16 ? rows / 16 : 1;
@@ -474,7 +519,7 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
 
 int make_plan(ThinPlan& pl, const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn,
               int64_t swk, int64_t M, int64_t N, int64_t K, int dtype, int block_n, int block_k,
-              int split_k, int num_waves) {
+              int split_k, int num_waves, bool glu = false) {
   const int es = esize_of(dtype);
   const bool w_vec = swk == 1 && aligned16(w) && ((swn * es) % 16 == 0 || N == 1) &&
                      (K * es) % 16 == 0;
@@ -487,10 +532,18 @@ int make_plan(ThinPlan& pl, const void* x, int64_t sxm, int64_t sxk, const void*
                     w_extent < (int64_t)kOob && x_extent < (int64_t)kOob;
   // The strided path has one shape: 16 rows per workgroup, 4 waves.
   if (plan_geometry(pl, fast ? fast_kind(M, dtype) : 0, M, N, K, dtype, fast ? block_n : 16,
-                    block_k, fast ? num_waves : 4, split_k) != 0)
+                    block_k, fast ? num_waves : 4, split_k, glu) != 0)
     return -1;
   pl.fast = fast;
   return 0;
+}
+
+// 16-byte loads, K-contiguous rows, 32-bit-addressable tiles: the operand
+// conditions of the fast kernels for a second weight matrix.
+bool weight_vec_ok(const void* w, int64_t swn, int64_t swk, int64_t N, int64_t K, int es) {
+  return w != nullptr && swk == 1 && aligned16(w) && ((swn * es) % 16 == 0 || N == 1) &&
+         (K * es) % 16 == 0 && (N == 1 || swn > 0) &&
+         (N > 1 ? 31 * swn * es : 0) + K * es < (int64_t)kOob;
 }
 
 template <bool PARTIAL, typename Kern>
@@ -536,35 +589,40 @@ void gemm_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 #define SIMSD_GEMV_CH_BIG 8   // load steps per chunk for block_k >= 512
 #endif
 
-template <int DT, int RW, int MS, int KS, int CH>
+template <int DT, int RW, int MS, int KS, int CH, bool GLU>
 void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  constexpr int GB = SIMSD_GEMV_GB_ALL ? RW / 4 : (RW >= 8 ? 2 : 1);
-  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true>, pl, args, stream);
-  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false>, pl, args, stream);
+  // gated: each batch of row groups stays inside the gate half or the up half
+  constexpr int G = RW / 4;
+  constexpr int GB = GLU ? (SIMSD_GEMV_GB_ALL ? G / 2 : (G >= 4 ? 2 : 1))
+                         : (SIMSD_GEMV_GB_ALL ? G : (RW >= 8 ? 2 : 1));
+  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU>, pl, args, stream);
+  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU>, pl, args, stream);
 }
 
-template <int DT, int RW, int MS, int KS>
+template <int DT, int RW, int MS, int KS, bool GLU>
 void launch_gemv4(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG>(pl, args, stream);
-  else launch_gemv4_ch<DT, RW, MS, KS, 2>(pl, args, stream);
+  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG, GLU>(pl, args, stream);
+  else launch_gemv4_ch<DT, RW, MS, KS, 2, GLU>(pl, args, stream);
 }
 
-template <int DT, int RW, int MS>
+template <int DT, int RW, int MS, bool GLU>
 void gemv4_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.ks) {
-    case 2: launch_gemv4<DT, RW, MS, 2>(pl, args, stream); break;
-    case 8: launch_gemv4<DT, RW, MS, 8>(pl, args, stream); break;
-    default: launch_gemv4<DT, RW, MS, 4>(pl, args, stream); break;
+    case 2: launch_gemv4<DT, RW, MS, 2, GLU>(pl, args, stream); break;
+    case 8: launch_gemv4<DT, RW, MS, 8, GLU>(pl, args, stream); break;
+    default: launch_gemv4<DT, RW, MS, 4, GLU>(pl, args, stream); break;
   }
 }
 
-template <int DT, int MS>
+template <int DT, int MS, bool GLU>
 void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.rows) {
-    case 4: gemv4_ks<DT, 4, MS>(pl, args, stream); break;
-    case 8: gemv4_ks<DT, 8, MS>(pl, args, stream); break;
-    case 32: gemv4_ks<DT, 32, MS>(pl, args, stream); break;
-    default: gemv4_ks<DT, 16, MS>(pl, args, stream); break;
+    case 4:
+      if constexpr (!GLU) gemv4_ks<DT, 4, MS, false>(pl, args, stream);   // gated plans use >= 8
+      break;
+    case 8: gemv4_ks<DT, 8, MS, GLU>(pl, args, stream); break;
+    case 32: gemv4_ks<DT, 32, MS, GLU>(pl, args, stream); break;
+    default: gemv4_ks<DT, 16, MS, GLU>(pl, args, stream); break;
   }
 }
 
@@ -572,28 +630,37 @@ void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 #define SIMSD_LDS_U 4
 #endif
 
-template <int DT, int RB, int CB, int KS>
+template <int DT, int RB, int CB, int KS, bool GLU>
 void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = (RB * CB == 1) ? SIMSD_LDS_U : (SIMSD_LDS_U + 1) / 2;
-  if (pl.split > 1) launch<true>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true>, pl, args, stream);
-  else launch<false>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false>, pl, args, stream);
+  if (pl.split > 1) launch<true>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
+  else launch<false>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
 }
 
-template <int DT, int RB, int CB>
+template <int DT, int RB, int CB, bool GLU = false>
 void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.ks) {
-    case 2: launch_lds<DT, RB, CB, 2>(pl, args, stream); break;
-    case 8: launch_lds<DT, RB, CB, 8>(pl, args, stream); break;
-    default: launch_lds<DT, RB, CB, 4>(pl, args, stream); break;
+    case 2: launch_lds<DT, RB, CB, 2, GLU>(pl, args, stream); break;
+    case 8: launch_lds<DT, RB, CB, 8, GLU>(pl, args, stream); break;
+    default: launch_lds<DT, RB, CB, 4, GLU>(pl, args, stream); break;
   }
 }
 
 template <int DT>
 void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   if constexpr (DT != kF32) {
-    if (pl.kind == 1) {
-      if (pl.ms == 1) gemv4_rows<DT, 1>(pl, args, stream);
-      else gemv4_rows<DT, 2>(pl, args, stream);
+    if (pl.glu) {
+      if (pl.kind == 1) {
+        if (pl.ms == 1) gemv4_rows<DT, 1, true>(pl, args, stream);
+        else gemv4_rows<DT, 2, true>(pl, args, stream);
+      } else if (pl.cb == 1) {
+        lds_ks<DT, 2, 1, true>(pl, args, stream);
+      } else {
+        lds_ks<DT, 2, 2, true>(pl, args, stream);
+      }
+    } else if (pl.kind == 1) {
+      if (pl.ms == 1) gemv4_rows<DT, 1, false>(pl, args, stream);
+      else gemv4_rows<DT, 2, false>(pl, args, stream);
     } else if (pl.kind == 2) {
       const bool two_rows = pl.rows == 32;   // 16-row blocks x 16-token blocks
       if (pl.cb == 1) { if (two_rows) lds_ks<DT, 2, 1>(pl, args, stream); else lds_ks<DT, 1, 1>(pl, args, stream); }
@@ -608,7 +675,7 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
     const int64_t total = args.M * args.N;
     hipLaunchKernelGGL((thin_reduce_kernel<DT>), dim3((unsigned)cdiv(total, 256)), dim3(256), 0,
                        stream, args.part, pl.split, args.M, args.N, args.bias, args.sb, args.y,
-                       args.sym, args.syn);
+                       args.sym, args.syn, pl.glu ? 1 : 0);
   }
 }
 
@@ -690,4 +757,54 @@ extern "C" int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype
   out4[2] = pl.ks;
   out4[3] = pl.split;
   return 0;
+}
+
+extern "C" int simsd_thin_linear_silu_mul(const void* x, int64_t sxm, int64_t sxk, const void* w_gate,
+                                          int64_t sgn, int64_t sgk, const void* w_up, int64_t sun,
+                                          int64_t suk, void* h, int64_t shm, int64_t shn, int64_t M,
+                                          int64_t I, int64_t K, int dtype, int block_n, int block_k,
+                                          int split_k, int num_waves, void* workspace,
+                                          int64_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16)
+    return set_error("thin_linear_silu_mul: dtype must be bf16 or fp16 (got code %d)", dtype);
+  if (M < 0 || I < 0 || K < 0) return set_error("thin_linear_silu_mul: negative size");
+  if (M == 0 || I == 0) return 0;
+  if (K == 0) return set_error("thin_linear_silu_mul: K == 0 must be handled by the caller");
+  if (x == nullptr || w_gate == nullptr || w_up == nullptr || h == nullptr)
+    return set_error("thin_linear_silu_mul: null pointer");
+  const int es = esize_of(dtype);
+  if (K * (int64_t)es > ((int64_t)1 << 31) - 64)
+    return set_error("thin_linear_silu_mul: K=%lld too large", (long long)K);
+  ThinPlan pl{};
+  // planned as one linear over the 2I stacked gate and up rows
+  if (make_plan(pl, x, sxm, sxk, w_gate, sgn, sgk, M, 2 * I, K, dtype, block_n, block_k, split_k,
+                num_waves, true) != 0)
+    return -1;
+  if (!pl.fast || !weight_vec_ok(w_up, sun, suk, I, K, es))
+    return set_error("thin_linear_silu_mul: needs 16-byte aligned, K-contiguous x, w_gate and w_up");
+  if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535 || cdiv(M * I, 256) > 0x7fffffff)
+    return set_error("thin_linear_silu_mul: grid too large (I=%lld, M=%lld)", (long long)I, (long long)M);
+  ThinArgs args{};
+  args.x = static_cast<const char*>(x);
+  args.sxm = sxm; args.sxk = sxk;
+  args.w = static_cast<const char*>(w_gate);
+  args.swn = sgn; args.swk = sgk;
+  args.w2 = static_cast<const char*>(w_up);
+  args.sw2n = sun;
+  args.y = static_cast<char*>(h);
+  args.sym = shm; args.syn = shn;
+  args.M = M; args.N = I; args.K = K;
+  args.steps = pl.steps;
+  args.steps_per_split = pl.steps_per_split;
+  if (pl.split > 1) {
+    if (workspace == nullptr || workspace_bytes < pl.part_bytes)
+      return set_error("thin_linear_silu_mul: split_k=%d needs a %lld-byte workspace (got %lld)",
+                       pl.split, (long long)pl.part_bytes, (long long)workspace_bytes);
+    if (!aligned16(workspace)) return set_error("thin_linear_silu_mul: workspace must be 16-byte aligned");
+    args.part = static_cast<float*>(workspace);
+  }
+  if (dtype == kBF16) dispatch_dt<kBF16>(pl, args, stream);
+  else dispatch_dt<kF16>(pl, args, stream);
+  return check_launch("thin_linear_silu_mul");
 }

@@ -3,7 +3,9 @@
 Same API and behaviour as kernels/fused_toggle.py (reference, lines 30-202):
 ``DEFAULT_TARGETS``, ``ALL_TARGETS``, ``apply_to_model``, ``is_applied``, the
 ``fused_linear`` context manager, ``warmup``, ``apply_moe_to_model`` and
-``is_moe_applied``.  The model code is third-party (loaded through
+``is_moe_applied``; added: ``apply_gated_mlp_to_model`` /
+``is_gated_mlp_applied`` (gate and up projections with SiLU·mul in one
+kernel).  The model code is third-party (loaded through
 ``trust_remote_code``), so the switch patches modules in place rather than
 editing call sites: target linears are swapped for ``ThinLinear`` (which
 aliases the original parameters), and LLaDA2's MoE block gets a class-level
@@ -164,3 +166,67 @@ def apply_moe_to_model(model: nn.Module, enable: bool = True) -> int:
 
 def is_moe_applied(model: nn.Module) -> bool:
     return any(getattr(m, _MOE_ATTR, None) is not None for m in model.modules())
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# SiLU-gated MLP blocks (gate_proj / up_proj / down_proj, modeling_sdar.py:113-119)
+# ─────────────────────────────────────────────────────────────────────────────
+_GATED: dict[int, list[nn.Module]] = {}   # id(model) -> blocks whose forward is patched
+
+
+def _is_silu(act) -> bool:
+    if isinstance(act, nn.SiLU):
+        return True
+    return getattr(act, "__name__", "") == "silu" or act.__class__.__name__ in ("SiLU", "SiLUActivation")
+
+
+def _gated_blocks(model: nn.Module):
+    for mod in model.modules():
+        parts = [getattr(mod, n, None) for n in ("gate_proj", "up_proj", "down_proj")]
+        if all(p is not None and hasattr(p, "weight") for p in parts) and _is_silu(getattr(mod, "act_fn", None)):
+            yield mod
+
+
+def apply_gated_mlp_to_model(model: nn.Module, enable: bool = True) -> int:
+    """Route SiLU-gated MLP blocks through ``thin_linear_silu_mul`` (or restore them).
+
+    A block qualifies when it has ``gate_proj``, ``up_proj``, ``down_proj``
+    (``nn.Linear`` or ``ThinLinear``) and a SiLU ``act_fn``, as SDAR's and
+    Qwen's MLPs do.  Its forward becomes ``down_proj(thin_linear_silu_mul(x,
+    gate.weight, up.weight))`` when the merged gate_up shape is inside the
+    fused envelope (``should_fuse(M, 2I, K)``), and the stock forward
+    otherwise.  No bias on gate/up (else the block is left alone).  Idempotent
+    both ways; returns how many blocks were switched or restored.
+    """
+    from .thin_linear_fused import should_fuse, thin_linear_silu_mul
+
+    key = id(model)
+    if not enable:
+        blocks = _GATED.pop(key, [])
+        for mod in blocks:
+            mod.__dict__.pop("forward", None)   # back to the class's forward
+        return len(blocks)
+    done = _GATED.setdefault(key, [])
+    n = 0
+    for mod in _gated_blocks(model):
+        if any(m is mod for m in done):
+            continue
+        if getattr(mod.gate_proj, "bias", None) is not None or getattr(mod.up_proj, "bias", None) is not None:
+            continue
+        stock = mod.forward
+
+        def forward(x, _mod=mod, _stock=stock):
+            wg, wu = _mod.gate_proj.weight, _mod.up_proj.weight
+            M = x.numel() // x.shape[-1]
+            if not should_fuse(M, 2 * wg.shape[0], wg.shape[1]):
+                return _stock(x)
+            return _mod.down_proj(thin_linear_silu_mul(x, wg, wu))
+
+        mod.forward = forward
+        done.append(mod)
+        n += 1
+    return n
+
+
+def is_gated_mlp_applied(model: nn.Module) -> bool:
+    return bool(_GATED.get(id(model)))

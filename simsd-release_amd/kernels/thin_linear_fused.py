@@ -6,7 +6,9 @@ Same public surface as the reference module (kernels/thin_linear_fused.py:57-419
 the ``TARGET_CTAS`` / ``MAX_SPLIT_K`` / ``MIN_K_PER_SPLIT`` knobs, with the same
 argument meaning and the same exceptions.  The arithmetic runs in a
 hand-written gfx950 HIP kernel (``libsimsd_kernels.so``, C ABI in
-``include/simsd_kernels.h``) instead of Triton.
+``include/simsd_kernels.h``) instead of Triton.  Added on top:
+``thin_linear_silu_mul``, an MLP's gate and up projections with the SiLU and
+product in the same kernel.
 
 How the MI355X kernels work (``csrc/thin_gemm.hip``)
 -----------------------------------------------------
@@ -272,6 +274,90 @@ def thin_linear(x: torch.Tensor, w: torch.Tensor,
     if bias is not None and not fuse_bias:
         y += bias
     return y.view(out_shape)
+
+
+def _vec_rows(t: torch.Tensor) -> bool:
+    """K-contiguous, 16-byte aligned rows (the fused kernels' operand form)."""
+    es = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and (t.shape[-1] * es) % 16 == 0
+            and (t.shape[0] == 1 or (t.stride(0) * es) % 16 == 0))
+
+
+def thin_linear_silu_mul(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                         config: tuple[int, ...] | None = None,
+                         num_warps: int | None = None) -> torch.Tensor:
+    """``F.silu(F.linear(x, w_gate)) * F.linear(x, w_up)`` in one kernel.
+
+    The gate and up projections of a SiLU-gated MLP (modeling_sdar.py:113-119)
+    with the SiLU and the product in the epilogue: one pass over both weights
+    and no [M, 2I] intermediate.  Rounding points as in PyTorch at the input
+    dtype (each projection, the SiLU and the product rounded to it).  A merged
+    gate_up weight [2I, K] is passed as its two halves (views, no copy).
+    bf16/fp16 with K-contiguous 16-byte-aligned operands use the fused
+    kernel; anything else runs the two projections through ``thin_linear``
+    and the epilogue in PyTorch.  ``config`` is the merged (K, 2I) shape's.
+    """
+    if torch.is_grad_enabled() and (x.requires_grad or w_gate.requires_grad or w_up.requires_grad):
+        raise RuntimeError(
+            "thin_linear_silu_mul is a forward-only inference kernel; call it under "
+            "torch.no_grad() / torch.inference_mode()")
+    if not (x.dtype == w_gate.dtype == w_up.dtype):
+        raise TypeError(f"dtype mismatch: x={x.dtype} w_gate={w_gate.dtype} w_up={w_up.dtype}")
+    if w_gate.ndim != 2 or w_up.shape != w_gate.shape:
+        raise ValueError(f"w_gate and w_up must both be [I, K], got {tuple(w_gate.shape)} "
+                         f"and {tuple(w_up.shape)}")
+    I, K = w_gate.shape
+    if x.shape[-1] != K:
+        raise ValueError(f"K mismatch: x[..., {x.shape[-1]}] vs w[{I}, {K}]")
+    out_shape = (*x.shape[:-1], I)
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    dev = _native.require_device(x2, w_gate, w_up)
+    code = _native.DTYPE_CODES.get(x.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {x.dtype} (bf16, fp16 or fp32)")
+    if M == 0 or I == 0:
+        return torch.zeros(out_shape, device=dev, dtype=x.dtype)
+    if (code == _native.DTYPE_CODES[torch.float32] or K == 0
+            or not (_vec_rows(x2) and _vec_rows(w_gate) and _vec_rows(w_up))):
+        g = thin_linear(x2, w_gate)
+        return (torch.nn.functional.silu(g) * thin_linear(x2, w_up)).view(out_shape)
+
+    h = torch.empty((M, I), device=dev, dtype=x.dtype)
+    if config is not None:
+        block_n, block_k, split_k = int(config[1]), int(config[2]), int(config[3])
+        waves = num_warps or _DEFAULT_WAVES
+    else:
+        tuned = _tuned_for(M, 2 * I, K)
+        if tuned is not None:
+            _, block_n, block_k, split_k, waves, _ = tuned
+        else:
+            _, block_n, block_k, split_k = _heuristic_config(M, 2 * I, K, x.element_size())
+            waves = _DEFAULT_WAVES
+        waves = num_warps or waves
+    if split_k < 1:
+        raise ValueError(f"SPLIT_K must be >= 1, got {split_k}")
+    block_n = _rows_for(block_n)
+    waves = 2 if waves <= 2 else (4 if waves <= 4 else 8)
+    lib = _native.lib()
+    ws, ws_bytes = None, 0
+    if split_k > 1:
+        need = lib.simsd_thin_linear_workspace_bytes(M, 2 * I, K, code, block_n, split_k, waves)
+        if need < 0:
+            _native.check(-1, "thin_linear_silu_mul")
+        ws = _partials(dev, need)
+        ws_bytes = ws.numel()
+    with _native.device_guard(dev):
+        status = lib.simsd_thin_linear_silu_mul(
+            x2.data_ptr(), x2.stride(0), x2.stride(1),
+            w_gate.data_ptr(), w_gate.stride(0), w_gate.stride(1),
+            w_up.data_ptr(), w_up.stride(0), w_up.stride(1),
+            h.data_ptr(), h.stride(0), h.stride(1),
+            M, I, K, code, block_n, block_k, split_k, waves,
+            ws.data_ptr() if ws is not None else None, ws_bytes,
+            _native.stream_of(dev))
+    _native.check(status, "thin_linear_silu_mul")
+    return h.view(out_shape)
 
 
 def should_fuse(M: int, N: int, K: int) -> bool:

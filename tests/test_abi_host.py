@@ -285,3 +285,34 @@ def test_apply_moe_to_model_host():
     ex = nn.ModuleList(_Expert(16, 8) for _ in range(3))
     a, b, c = stack_expert_weights(ex, free_originals=False)
     assert a.is_contiguous() and ex[0].gate_proj.weight.numel() == 128
+
+
+def test_gated_mlp_toggle_host():
+    """apply_gated_mlp_to_model patches SiLU-gated blocks only, is idempotent,
+    skips biased gate/up, and restores the class forward."""
+    import torch.nn as nn
+    from kernels.fused_toggle import apply_gated_mlp_to_model, is_gated_mlp_applied
+
+    class MLP(nn.Module):
+        def __init__(self, bias=False, act=None):
+            super().__init__()
+            self.gate_proj = nn.Linear(16, 8, bias=bias)
+            self.up_proj = nn.Linear(16, 8, bias=bias)
+            self.down_proj = nn.Linear(8, 16, bias=False)
+            self.act_fn = act if act is not None else nn.SiLU()
+
+        def forward(self, x):
+            return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+
+    model = nn.Sequential(MLP(), MLP(bias=True), MLP(act=nn.GELU()), MLP())
+    assert apply_gated_mlp_to_model(model) == 2
+    assert is_gated_mlp_applied(model)
+    assert "forward" in model[0].__dict__ and "forward" not in model[1].__dict__
+    assert "forward" not in model[2].__dict__
+    assert apply_gated_mlp_to_model(model) == 0            # idempotent
+    assert apply_gated_mlp_to_model(model, enable=False) == 2
+    assert not is_gated_mlp_applied(model)
+    assert all("forward" not in m.__dict__ for m in model)
+    x = torch.randn(3, 16)
+    with torch.no_grad():                                   # the stock CPU path is back
+        assert model(x).shape == (3, 16)

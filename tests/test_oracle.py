@@ -94,6 +94,32 @@ def test_linear_exact_vs_torch_cpu_linear():
         assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
+def test_gated_exact_vs_torch_cpu_composition():
+    """gated_exact against torch CPU F.silu(F.linear) * F.linear at the same
+    dtype (PyTorch's own rounding points), and planted slips fail."""
+    from oracle.numerics import round_bf16
+    g = torch.Generator().manual_seed(5)
+    for dt, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        for M, K, I in [(1, 256, 64), (4, 2048, 96), (16, 1000, 33)]:
+            x = torch.randn(M, K, generator=g).to(dt)
+            wg = (torch.randn(I, K, generator=g) * 0.03).to(dt)
+            wu = (torch.randn(I, K, generator=g) * 0.03).to(dt)
+            ref = othin.gated_exact(x.float().numpy(), wg.float().numpy(), wu.float().numpy(), dtype=name)
+            t = (torch.nn.functional.silu(torch.nn.functional.linear(x, wg))
+                 * torch.nn.functional.linear(x, wu)).float().numpy()
+            assert float(np.abs(ref - t).max()) <= othin.tolerance(float(np.abs(ref).max()), name)
+    x = torch.randn(4, 512, generator=g).bfloat16().float().numpy()
+    wg = (torch.randn(64, 512, generator=g) * 0.05).bfloat16().float().numpy()
+    wu = (torch.randn(64, 512, generator=g) * 0.05).bfloat16().float().numpy()
+    ref = othin.gated_exact(x, wg, wu)
+    lin = lambda w: othin.linear_exact(x, w)
+    slips = {"gate and up swapped": othin.gated_exact(x, wu, wg),
+             "no SiLU": round_bf16(lin(wg) * lin(wu)),
+             "sigmoid for SiLU": round_bf16(round_bf16(1 / (1 + np.exp(-lin(wg)))) * lin(wu))}
+    for name, bad in slips.items():
+        assert not np.array_equal(bad, ref), name
+
+
 # ─────────────────────────────────────────────────────────────── route ───
 def test_route_ids_golden(golden):
     d = golden("route")

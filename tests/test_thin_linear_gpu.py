@@ -369,6 +369,92 @@ def test_fp16_every_kernel(M):
                 assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
+# ──────────────────────────────────────────── gated (SiLU-mul) projection ───
+@pytest.mark.parametrize("M", [1, 4, 8, 9, 16, 32])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_silu_mul_vs_oracle(M, dtype):
+    """thin_linear_silu_mul against the oracle's exact gated projection, on the
+    draft MLP shape, odd dims, and the halves of a merged gate_up weight."""
+    from kernels.thin_linear_fused import thin_linear_silu_mul
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    for K, I in [(2048, 6144), (1000, 531)]:
+        x = rnd(M, K, dtype=tdt, seed=50 + M)
+        merged = rnd(2 * I, K, dtype=tdt, scale=0.02, seed=51 + K)
+        wg, wu = merged[:I], merged[I:]
+        ref = othin.gated_exact(x.float().cpu().numpy(), wg.float().cpu().numpy(),
+                                wu.float().cpu().numpy(), dtype=dtype)
+        with torch.inference_mode():
+            got = thin_linear_silu_mul(x, wg, wu).float().cpu().numpy()
+        amax = float(np.abs(ref).max())
+        err = float(np.abs(got - ref).max())
+        assert err <= othin.tolerance(amax, dtype), (M, K, I, err)
+        assert othin.max_abs_rel(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_silu_mul_every_launch_shape(M):
+    from kernels.thin_linear_fused import thin_linear_silu_mul
+    x = rnd(M, 1000, seed=60 + M)
+    wg, wu = rnd(261, 1000, scale=0.03, seed=61), rnd(261, 1000, scale=0.03, seed=62)
+    with torch.inference_mode():
+        ref = F.silu(F.linear(x, wg)) * F.linear(x, wu)
+        for rows in (8, 16, 32):
+            for waves in (2, 4, 8):
+                for split in (1, 3):
+                    got = thin_linear_silu_mul(x, wg, wu, config=(16, rows, 256, split), num_warps=waves)
+                    err = float((got.float() - ref.float()).abs().max())
+                    assert err <= tol(ref), (rows, waves, split, err)
+        first = thin_linear_silu_mul(x, wg, wu, config=(16, 16, 256, 3))
+        assert torch.equal(thin_linear_silu_mul(x, wg, wu, config=(16, 16, 256, 3)), first)
+
+
+def test_silu_mul_fallbacks_and_errors():
+    from kernels.thin_linear_fused import thin_linear_silu_mul
+    x = rnd(4, 512, seed=70)
+    wg, wu = rnd(64, 512, scale=0.03, seed=71), rnd(64, 512, scale=0.03, seed=72)
+    with torch.inference_mode():
+        ref = F.silu(F.linear(x, wg)) * F.linear(x, wu)
+        for xv, g, u in [(x.t().contiguous().t(), wg, wu),                 # strided x
+                         (x.float(), wg.float(), wu.float())]:              # fp32
+            got = thin_linear_silu_mul(xv, g, u)
+            r = F.silu(F.linear(xv, g)) * F.linear(xv, u)
+            assert float((got.float() - r.float()).abs().max()) <= tol(r)
+        assert thin_linear_silu_mul(x.view(2, 2, 512), wg, wu).shape == (2, 2, 64)
+    with pytest.raises(TypeError):
+        thin_linear_silu_mul(x, wg.float(), wu)
+    with pytest.raises(ValueError):
+        thin_linear_silu_mul(x, wg, wu[:32])
+    with pytest.raises(RuntimeError, match="forward-only"):
+        thin_linear_silu_mul(x.requires_grad_(True), wg, wu)
+
+
+def test_gated_mlp_toggle_end_to_end():
+    from kernels.fused_toggle import apply_gated_mlp_to_model
+
+    class MLP(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = nn.Linear(2048, 6144, bias=False)
+            self.up_proj = nn.Linear(2048, 6144, bias=False)
+            self.down_proj = nn.Linear(6144, 2048, bias=False)
+            self.act_fn = nn.SiLU()
+
+        def forward(self, x):
+            return self.down_proj(self.act_fn(self.gate_proj(x)) * self.up_proj(x))
+
+    m = MLP().to(DEV, torch.bfloat16).eval()
+    x = rnd(4, 2048, seed=80)
+    with torch.inference_mode():
+        stock = m(x)
+        assert apply_gated_mlp_to_model(m) == 1
+        fused = m(x)
+        big = m(rnd(64, 2048, seed=81))            # outside the envelope: stock forward
+        assert big.shape == (64, 2048)
+        assert apply_gated_mlp_to_model(m, enable=False) == 1
+        assert torch.equal(m(x), stock)
+    assert float((fused.float() - stock.float()).abs().max()) <= tol(stock)
+
+
 # ───────────────────────────────────────────── size-independent properties ───
 def test_properties_at_full_size():
     from kernels.thin_linear_fused import thin_linear
