@@ -13,6 +13,10 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
   c3m16 / c3m32
           8B-shape target verify set, 36 layers x {qkv 4096->6144, o 4096->4096,
           gate_up 4096->24576, down 12288->4096} + lm_head 4096->151936, M=16/32.
+  mlp4 / mlp16 / mlp32
+          the gated MLP block per layer (28 draft layers at M=4, 36 target
+          layers at M=16/32): gate and up projections with SiLU-mul fused
+          (thin_linear_silu_mul), then down; also times the unfused sequence.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
@@ -264,6 +268,72 @@ def run_linear(args, torch, dev):
     return result, M
 
 
+# ─────────────────────────────────────────────────────── gated MLP block ───
+def run_mlp(args, torch, dev):
+    """The MLP half of each layer: h = silu(x Wg^T) * (x Wu^T) in one kernel,
+    then down.  Also times the unfused sequence (merged gate_up linear,
+    PyTorch SiLU and product, down) on the same weights."""
+    from kernels.thin_linear_fused import thin_linear, thin_linear_silu_mul
+
+    M = {"mlp4": 4, "mlp16": 16, "mlp32": 32}[args.workload]
+    H, I, L = (2048, 6144, 28) if M == 4 else (4096, 12288, 36)
+    layers = []
+    for layer in range(L):
+        g = torch.Generator(device=dev).manual_seed(4000 + layer)
+        mk = lambda *sh, s=1.0: (torch.randn(*sh, device=dev, generator=g) * s).to(torch.bfloat16)
+        layers.append((mk(M, H), mk(2 * I, H, s=0.02), mk(H, I, s=0.02)))
+    step_bytes = L * (2 * I * H * 2 + H * I * 2 + M * H * 2 * 2 + M * I * 2 * 2)
+
+    def fused():
+        return [thin_linear(thin_linear_silu_mul(x, gu[:I], gu[I:]), wd) for x, gu, wd in layers]
+
+    def unfused():
+        outs = []
+        for x, gu, wd in layers:
+            y = thin_linear(x, gu)
+            outs.append(thin_linear(torch.nn.functional.silu(y[:, :I]) * y[:, I:], wd))
+        return outs
+
+    with torch.inference_mode():
+        fused()
+        unfused()
+        torch.cuda.synchronize()
+        us_unfused = graph_us_per_call(torch, [unfused], reps=max(5, args.steps // 5))
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fused()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fused()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / args.steps
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"gated-mlp-{L}L-H{H}-I{I}-M{M}", "M": M,
+                   "algorithmic_bytes_per_step": step_bytes, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "thin_linear_silu_mul + thin_linear (down), per layer"},
+        "unfused_ms_per_step": round(us_unfused / 1e3, 4),
+        "fused_speedup": round(us_unfused / 1e3 / ms, 3),
+    }, M
+
+
 # ────────────────────────────────────────────────────────────────── MoE ───
 def run_moe(args, torch, dev):
     from kernels.moe_dispatch_fused import moe_forward, moe_route
@@ -398,7 +468,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "copy"])
+                    choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
+                             "mlp32", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -415,6 +486,11 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
+    if args.workload.startswith("mlp"):
+        result, _ = run_mlp(args, torch, dev)
+        result["device"] = torch.cuda.get_device_name(dev)
+        print(json.dumps(result), flush=True)
         return
     if args.workload.startswith("c4"):
         result, T = run_moe(args, torch, dev)
