@@ -17,6 +17,10 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           the gated MLP block per layer (28 draft layers at M=4, 36 target
           layers at M=16/32): gate and up projections with SiLU-mul fused
           (thin_linear_silu_mul), then down; also times the unfused sequence.
+  layer4 / layer16 / layer32
+          the linear path of each decoder layer with the fused epilogues:
+          RMSNorm + qkv, o, RMSNorm + gate/up + SiLU-mul, down (four launches),
+          against the unfused sequence with the stock PyTorch RMSNorm.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
@@ -334,6 +338,80 @@ def run_mlp(args, torch, dev):
     }, M
 
 
+# ───────────────────────────────────── decoder-layer linear path, fused ───
+def run_layer(args, torch, dev):
+    """Per layer: RMSNorm + qkv, o, RMSNorm + gate/up + SiLU-mul, down -- four
+    launches with the norms and the gate epilogue fused -- against the
+    unfused sequence (stock five-op RMSNorm in PyTorch, merged linears,
+    PyTorch SiLU and product)."""
+    from kernels.thin_linear_fused import (thin_linear, thin_rmsnorm_linear,
+                                           thin_rmsnorm_linear_silu_mul)
+
+    M = {"layer4": 4, "layer16": 16, "layer32": 32}[args.workload]
+    if M == 4:
+        H, QKV, I, L = 2048, 4096, 6144, 28
+    else:
+        H, QKV, I, L = 4096, 6144, 12288, 36
+    eps = 1e-6
+    layers = []
+    for layer in range(L):
+        g = torch.Generator(device=dev).manual_seed(6000 + layer)
+        mk = lambda *sh, s=1.0: (torch.randn(*sh, device=dev, generator=g) * s).to(torch.bfloat16)
+        layers.append(dict(x=mk(M, H), n1=(1 + 0.1 * torch.randn(H, device=dev, generator=g)).bfloat16(),
+                           qkv=mk(QKV, H, s=0.02), o=mk(H, H, s=0.02), a=mk(M, H),
+                           n2=(1 + 0.1 * torch.randn(H, device=dev, generator=g)).bfloat16(),
+                           gu=mk(2 * I, H, s=0.02), down=mk(H, I, s=0.02)))
+    wbytes = (QKV * H + H * H + 2 * I * H + H * I) * 2
+    abytes = M * 2 * (H + QKV + H + H + H + H + I + I + H)
+    step_bytes = L * (wbytes + abytes)
+
+    def stock_norm(x, w):
+        x32 = x.float()
+        return w * (x32 * torch.rsqrt(x32.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype)
+
+    def fused():
+        out = []
+        for d in layers:
+            q = thin_rmsnorm_linear(d["x"], d["n1"], eps, d["qkv"])
+            o = thin_linear(d["a"], d["o"])
+            h = thin_rmsnorm_linear_silu_mul(d["x"], d["n2"], eps, d["gu"][:I], d["gu"][I:])
+            out.append((q, o, thin_linear(h, d["down"])))
+        return out
+
+    def unfused():
+        out = []
+        for d in layers:
+            q = thin_linear(stock_norm(d["x"], d["n1"]), d["qkv"])
+            o = thin_linear(d["a"], d["o"])
+            y = thin_linear(stock_norm(d["x"], d["n2"]), d["gu"])
+            h = torch.nn.functional.silu(y[:, :I]) * y[:, I:]
+            out.append((q, o, thin_linear(h, d["down"])))
+        return out
+
+    with torch.inference_mode():
+        fused()
+        unfused()
+        torch.cuda.synchronize()
+        us_unfused = graph_us_per_call(torch, [unfused], reps=max(5, args.steps // 5))
+        us_fused = graph_us_per_call(torch, [fused], reps=args.steps)
+    ms = us_fused / 1e3
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": 1, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"decoder-layer-linears-fused-{L}L-H{H}-M{M}", "M": M,
+                   "launches_per_layer": 4, "algorithmic_bytes_per_step": step_bytes,
+                   "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "RMSNorm+qkv, o, RMSNorm+gate/up+SiLU-mul, down per layer"},
+        "unfused_ms_per_step": round(us_unfused / 1e3, 4),
+        "fused_speedup": round(us_unfused / us_fused, 3),
+    }, M
+
+
 # ────────────────────────────────────────────────────────────────── MoE ───
 def run_moe(args, torch, dev):
     from kernels.moe_dispatch_fused import moe_forward, moe_route
@@ -469,7 +547,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -487,8 +565,8 @@ def main():
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
         return
-    if args.workload.startswith("mlp"):
-        result, _ = run_mlp(args, torch, dev)
+    if args.workload.startswith("mlp") or args.workload.startswith("layer"):
+        result, _ = (run_mlp if args.workload.startswith("mlp") else run_layer)(args, torch, dev)
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)
         return

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 4
+#define SIMSD_ABI_VERSION 5
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -98,6 +98,42 @@ int simsd_thin_linear_silu_mul(const void* x, int64_t stride_xm, int64_t stride_
                                int64_t M, int64_t I, int64_t K, int dtype,
                                int block_n, int block_k, int split_k, int num_waves,
                                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- RMSNorm and the RMSNorm prologue -------------------------------------
+ * y[m, k] = dtype( gamma[k] * dtype( x[m, k] * r_m ) ),
+ *   r_m = 1 / sqrt( sum_k x[m, k]^2 / K + eps )  (fp32)
+ * -- the stock PyTorch RMSNorm the reference's runner installs
+ * (sdar/run_native_tp2.py:34-51; SDARRMSNorm, modeling_sdar.py:74-92), in one
+ * launch.  x and y K-contiguous (row strides in elements), gamma [K]
+ * contiguous in the same dtype. */
+int simsd_rmsnorm(const void* x, int64_t stride_xm, const void* gamma, float eps, void* y,
+                  int64_t stride_ym, int64_t M, int64_t K, int dtype, void* stream);
+
+/* RMSNorm(x) followed by simsd_thin_linear / simsd_thin_linear_silu_mul on
+ * it.  At <= 8 tokens (bf16/fp16, vector-aligned operands, 16-byte aligned
+ * gamma) the norm runs inside the GEMV: every workgroup derives its tokens'
+ * scale and normalises the activations as it loads them, so the normalised
+ * rows never go to memory.  Otherwise the norm is written to the workspace
+ * and the linear reads it.  workspace: simsd_rmsnorm_linear_workspace_bytes
+ * (N_rows = N, or 2*I for the gated form). */
+int64_t simsd_rmsnorm_linear_workspace_bytes(int64_t M, int64_t N_rows, int64_t K, int dtype,
+                                             int block_n, int split_k, int num_waves);
+int simsd_rmsnorm_thin_linear(const void* x, int64_t stride_xm, int64_t stride_xk,
+                              const void* gamma, float eps,
+                              const void* w, int64_t stride_wn, int64_t stride_wk,
+                              const void* bias, int64_t stride_b,
+                              void* y, int64_t stride_ym, int64_t stride_yn,
+                              int64_t M, int64_t N, int64_t K, int dtype,
+                              int block_n, int block_k, int split_k, int num_waves,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+int simsd_rmsnorm_thin_linear_silu_mul(const void* x, int64_t stride_xm, int64_t stride_xk,
+                                       const void* gamma, float eps,
+                                       const void* w_gate, int64_t stride_gn, int64_t stride_gk,
+                                       const void* w_up, int64_t stride_un, int64_t stride_uk,
+                                       void* h, int64_t stride_hm, int64_t stride_hn,
+                                       int64_t M, int64_t I, int64_t K, int dtype,
+                                       int block_n, int block_k, int split_k, int num_waves,
+                                       void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- MoE: routing ------------------------------------------------------
  * ids_out[t, j] (int64) = index of the j-th largest logit of row t (ties to

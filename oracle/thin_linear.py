@@ -14,6 +14,9 @@ plus bias (``y += bias`` after the GEMM, kernels/thin_linear_fused.py:343-344).
 ``gated_exact``       silu(x w_gate^T) * (x w_up^T) with the rounding points of
                       a bf16/fp16 SDARMLP (modeling_sdar.py:113-119): each
                       projection, the SiLU and the product rounded to the dtype.
+``rmsnorm_exact``     the stock RMSNorm (sdar/run_native_tp2.py:42-47): the
+                      mean of squares in fp64, x * r rounded to the dtype, times
+                      the weight, rounded again.
 ``tolerance``         the reference's bounds (thin_linear_fused_test.py:28-32).
 """
 from __future__ import annotations
@@ -45,6 +48,14 @@ def gated_exact(x: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray, dtype: str 
     g = linear_exact(x, w_gate, dtype=dtype)
     u = linear_exact(x, w_up, dtype=dtype)
     return rnd(rnd(g / (1.0 + np.exp(-g))) * u)
+
+
+def rmsnorm_exact(x: np.ndarray, weight: np.ndarray, eps: float, dtype: str = "bf16") -> np.ndarray:
+    """rnd(weight * rnd(x * r)), r = 1 / sqrt(mean(x^2) + eps) per row."""
+    rnd = ROUNDERS[dtype]
+    x64 = np.asarray(x, dtype=np.float64)
+    r = 1.0 / np.sqrt((x64 * x64).mean(axis=-1, keepdims=True) + eps)
+    return rnd(np.asarray(weight, dtype=np.float64) * rnd(x64 * r))
 
 
 def linear_cpu_torch(x, w, bias=None):

@@ -83,6 +83,67 @@ template <> SIMSD_DEV float round_to<kBF16>(float v) {
 template <> SIMSD_DEV float round_to<kF16>(float v) { return (float)(_Float16)v; }
 template <> SIMSD_DEV float round_to<kF32>(float v) { return v; }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// 16-bit storage element <-> float (the low half of a packed pair first).
+template <int DT> SIMSD_DEV float h16_to_f32(uint32_t h);
+template <> SIMSD_DEV float h16_to_f32<kBF16>(uint32_t h) { return bf16_bits_to_f32(h & 0xffffu); }
+template <> SIMSD_DEV float h16_to_f32<kF16>(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xffffu));
+}
+template <int DT> SIMSD_DEV uint32_t f32_to_h16(float v);
+template <> SIMSD_DEV uint32_t f32_to_h16<kBF16>(float v) { return f32_to_bf16_bits(v); }
+template <> SIMSD_DEV uint32_t f32_to_h16<kF16>(float v) {
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// RMSNorm of 8 packed 16-bit values: out = dtype(gamma * dtype(x * r)), the
+// rounding points of the stock PyTorch RMSNorm (x * rsqrt(mean(x^2) + eps)
+// in fp32, cast to the input dtype, times the weight in that dtype).
+template <int DT>
+SIMSD_DEV u32x4_t rms_scale8(u32x4_t x, u32x4_t g, float r) {
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w}, gv[4] = {g.x, g.y, g.z, g.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = round_to<DT>(h16_to_f32<DT>(gv[i]) * round_to<DT>(h16_to_f32<DT>(xv[i]) * r));
+    const float hi = round_to<DT>(h16_to_f32<DT>(gv[i] >> 16) * round_to<DT>(h16_to_f32<DT>(xv[i] >> 16) * r));
+    o[i] = f32_to_h16<DT>(lo) | (f32_to_h16<DT>(hi) << 16);
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// bf16: both roundings of a pair in one v_cvt_pk_bf16_f32 each (round to
+// nearest even, as the software rounding above).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <>
+SIMSD_DEV u32x4_t rms_scale8<kBF16>(u32x4_t x, u32x4_t g, float r) {
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w}, gv[4] = {g.x, g.y, g.z, g.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t xf = {__uint_as_float(xv[i] << 16), __uint_as_float(xv[i] & 0xffff0000u)};
+    const uint32_t t = __builtin_bit_cast(uint32_t, __builtin_convertvector(xf * r, bf16x2_t));
+    const f32x2_t tf = {__uint_as_float(t << 16), __uint_as_float(t & 0xffff0000u)};
+    const f32x2_t gf = {__uint_as_float(gv[i] << 16), __uint_as_float(gv[i] & 0xffff0000u)};
+    o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(gf * tf, bf16x2_t));
+  }
+  return u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// Sum of squares of 8 packed 16-bit values, in element order.
+template <int DT>
+SIMSD_DEV float sumsq8(u32x4_t x, float acc) {
+  const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = h16_to_f32<DT>(xv[i]), hi = h16_to_f32<DT>(xv[i] >> 16);
+    acc += lo * lo;
+    acc += hi * hi;
+  }
+  return acc;
+}
+
 // ---------------------------------------------------------------- MFMA k-step
 template <int DT> struct Mfma;
 template <> struct Mfma<kBF16> {

@@ -41,6 +41,8 @@ struct ThinArgs {
   float* part;               // [split][M][N] fp32 partials when split > 1 ([split][M][2N] gated)
   const char* w2;            // gated (SiLU-mul) kernels: the up matrix, row stride sw2n
   int64_t sw2n;
+  const char* gamma;         // RMSNorm prologue: weight [K] (contiguous), epsilon
+  float eps;
   int64_t M, N, K;           // gated: N = output columns (rows of each of w, w2)
   int steps;                 // ceil(K * esize / 64)
   int steps_per_split;
@@ -213,7 +215,7 @@ __device__ __forceinline__ void reduce_lanes(float (&val)[NV]) {
   }
 }
 
-template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU>
+template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU, bool NORM>
 __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int G = RW / 4;
@@ -247,6 +249,58 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
   const uint32_t lane_k = (uint32_t)(b4 * kLaneBytes);
 
+  // RMSNorm prologue: every workgroup derives the scale of its <= 8 tokens
+  // from their whole rows (L2-resident after the first workgroup), then
+  // normalises the activations as they are loaded.  rr[c]: this lane's token
+  // 4c + i4.
+  float rr[MS];
+  rsrc_t rG{};
+  // weight rows of this wave's first chunk: A operands for group g, step s
+  auto load_a = [&](int c0, int g, int s) {
+    const int c_lim = min(w1, c0 + CH);
+    const bool up = GLU && g >= G / 2;
+    const uint32_t roff = (uint32_t)(4 * (up ? g - G / 2 : g) + i4) * (up ? sw2n_b : swn_b);
+    const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
+    const bool ok = (c0 + s < c_lim) && (k < Kb);
+    return buf_load16<kAuxStream>(up ? rA2 : rA, ok ? roff + k : kOob);
+  };
+  // with the norm prologue, the first chunk's weights are requested before
+  // the prologue so that their latency overlaps the norm's
+  u32x4_t A0[NORM ? G : 1][NORM ? CH : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int st = 0; st < CH; ++st) A0[g][st] = load_a(w0, g, st);
+  }
+  if constexpr (NORM) {
+    rG = make_rsrc(a.gamma, Kb);
+    constexpr int MT = 4 * MS;
+    __shared__ float ssq_red[KS][MT];
+    float ssq[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) ssq[j] = 0.f;
+    for (uint32_t off = (uint32_t)threadIdx.x * kLaneBytes; off < Kb; off += 64 * KS * kLaneBytes) {
+      u32x4_t v[MT];
+#pragma unroll
+      for (int j = 0; j < MT; ++j) v[j] = buf_load16<kAuxKeep>(rB, j < cols_valid ? (uint32_t)j * sxm_b + off : kOob);
+#pragma unroll
+      for (int j = 0; j < MT; ++j) ssq[j] = sumsq8<DT>(v[j], ssq[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+      const float t = wave_sum(ssq[j]);
+      if (lane == 0) ssq_red[wk][j] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < MS; ++c) {
+      float t = 0.f;
+      for (int w = 0; w < KS; ++w) t += ssq_red[w][4 * c + i4];
+      rr[c] = 1.f / sqrtf(t / (float)a.K + a.eps);
+    }
+  }
+
   f32x4_t acc[G][MS];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -266,21 +320,23 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
         const bool col_ok = 4 * c + i4 < cols_valid;
         B[s][c] = buf_load16<kAuxKeep>(rB, (ok && col_ok) ? (uint32_t)(4 * c + i4) * sxm_b + k : kOob);
       }
+      if constexpr (NORM) {
+        const u32x4_t gm = buf_load16<kAuxKeep>(rG, ok ? k : kOob);
+#pragma unroll
+        for (int c = 0; c < MS; ++c) B[s][c] = rms_scale8<DT>(B[s][c], gm, rr[c]);
+      }
     }
+    const bool pre = NORM && c0 == w0;   // weights already requested before the prologue
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GB) {
       u32x4_t A[GB][CH];
 #pragma unroll
-      for (int gg = 0; gg < GB; ++gg) {
-        const bool up = GLU && g0 + gg >= G / 2;
-        const uint32_t roff = (uint32_t)(4 * (up ? g0 + gg - G / 2 : g0 + gg) + i4) * (up ? sw2n_b : swn_b);
+      for (int gg = 0; gg < GB; ++gg)
 #pragma unroll
         for (int s = 0; s < CH; ++s) {
-          const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
-          const bool ok = (c0 + s < c_lim) && (k < Kb);
-          A[gg][s] = buf_load16<kAuxStream>(up ? rA2 : rA, ok ? roff + k : kOob);
+          if constexpr (NORM) A[gg][s] = pre ? A0[g0 + gg][s] : load_a(c0, g0 + gg, s);
+          else A[gg][s] = load_a(c0, g0 + gg, s);
         }
-      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int gg = 0; gg < GB; ++gg)
@@ -415,6 +471,32 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm, one workgroup per token row: y = dtype(gamma * dtype(x * r)),
+// r = 1 / sqrt(sum(x^2) / K + eps) in fp32 -- the stock PyTorch RMSNorm
+// (sdar/run_native_tp2.py:42-47).  Sum order fixed (strided per thread, then
+// waves in order): bit-reproducible.
+template <int DT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const char* __restrict__ x, int64_t sxm,
+                                                      const char* __restrict__ gamma, float eps,
+                                                      char* __restrict__ y, int64_t sym, int64_t K) {
+  __shared__ float part[4];
+  const int64_t m = blockIdx.x;
+  const char* xr = x + m * sxm * DTypeInfo<DT>::kSize;
+  float acc = 0.f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) {
+    const float v = load_elem<DT>(xr, k);
+    acc += v * v;
+  }
+  const float t = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = t;
+  __syncthreads();
+  const float r = 1.f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)K + eps);
+  char* yr = y + m * sym * DTypeInfo<DT>::kSize;
+  for (int64_t k = threadIdx.x; k < K; k += 256)
+    store_elem<DT>(yr, k, load_elem<DT>(gamma, k) * round_to<DT>(load_elem<DT>(xr, k) * r));
+}
+
 // Sum the split partials in split order (fixed: bit-reproducible), add bias,
 // round to the output dtype.  One thread per output element.
 template <int DT>
@@ -450,6 +532,7 @@ namespace {
 struct ThinPlan {
   int kind;
   bool glu;                  // gated: rows are half gate, half up; outputs = rows / 2
+  bool norm;                 // RMSNorm prologue in the GEMV
   int rows, rt, rb, cb, ms, ks, ch, split;
   bool fast;
   int64_t tiles_n, tiles_m;
@@ -589,40 +672,40 @@ void gemm_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 #define SIMSD_GEMV_CH_BIG 8   // load steps per chunk for block_k >= 512
 #endif
 
-template <int DT, int RW, int MS, int KS, int CH, bool GLU>
+template <int DT, int RW, int MS, int KS, int CH, bool GLU, bool NORM>
 void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   // gated: each batch of row groups stays inside the gate half or the up half
   constexpr int G = RW / 4;
   constexpr int GB = GLU ? (SIMSD_GEMV_GB_ALL ? G / 2 : (G >= 4 ? 2 : 1))
                          : (SIMSD_GEMV_GB_ALL ? G : (RW >= 8 ? 2 : 1));
-  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU>, pl, args, stream);
-  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU>, pl, args, stream);
+  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>, pl, args, stream);
+  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>, pl, args, stream);
 }
 
-template <int DT, int RW, int MS, int KS, bool GLU>
+template <int DT, int RW, int MS, int KS, bool GLU, bool NORM>
 void launch_gemv4(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG, GLU>(pl, args, stream);
-  else launch_gemv4_ch<DT, RW, MS, KS, 2, GLU>(pl, args, stream);
+  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG, GLU, NORM>(pl, args, stream);
+  else launch_gemv4_ch<DT, RW, MS, KS, 2, GLU, NORM>(pl, args, stream);
 }
 
-template <int DT, int RW, int MS, bool GLU>
+template <int DT, int RW, int MS, bool GLU, bool NORM>
 void gemv4_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.ks) {
-    case 2: launch_gemv4<DT, RW, MS, 2, GLU>(pl, args, stream); break;
-    case 8: launch_gemv4<DT, RW, MS, 8, GLU>(pl, args, stream); break;
-    default: launch_gemv4<DT, RW, MS, 4, GLU>(pl, args, stream); break;
+    case 2: launch_gemv4<DT, RW, MS, 2, GLU, NORM>(pl, args, stream); break;
+    case 8: launch_gemv4<DT, RW, MS, 8, GLU, NORM>(pl, args, stream); break;
+    default: launch_gemv4<DT, RW, MS, 4, GLU, NORM>(pl, args, stream); break;
   }
 }
 
-template <int DT, int MS, bool GLU>
+template <int DT, int MS, bool GLU, bool NORM = false>
 void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.rows) {
     case 4:
-      if constexpr (!GLU) gemv4_ks<DT, 4, MS, false>(pl, args, stream);   // gated plans use >= 8
+      if constexpr (!GLU) gemv4_ks<DT, 4, MS, false, NORM>(pl, args, stream);   // gated plans use >= 8
       break;
-    case 8: gemv4_ks<DT, 8, MS, GLU>(pl, args, stream); break;
-    case 32: gemv4_ks<DT, 32, MS, GLU>(pl, args, stream); break;
-    default: gemv4_ks<DT, 16, MS, GLU>(pl, args, stream); break;
+    case 8: gemv4_ks<DT, 8, MS, GLU, NORM>(pl, args, stream); break;
+    case 32: gemv4_ks<DT, 32, MS, GLU, NORM>(pl, args, stream); break;
+    default: gemv4_ks<DT, 16, MS, GLU, NORM>(pl, args, stream); break;
   }
 }
 
@@ -649,7 +732,15 @@ void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 template <int DT>
 void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   if constexpr (DT != kF32) {
-    if (pl.glu) {
+    if (pl.norm) {   // RMSNorm prologue: GEMV plans only
+      if (pl.glu) {
+        if (pl.ms == 1) gemv4_rows<DT, 1, true, true>(pl, args, stream);
+        else gemv4_rows<DT, 2, true, true>(pl, args, stream);
+      } else {
+        if (pl.ms == 1) gemv4_rows<DT, 1, false, true>(pl, args, stream);
+        else gemv4_rows<DT, 2, false, true>(pl, args, stream);
+      }
+    } else if (pl.glu) {
       if (pl.kind == 1) {
         if (pl.ms == 1) gemv4_rows<DT, 1, true>(pl, args, stream);
         else gemv4_rows<DT, 2, true>(pl, args, stream);
@@ -807,4 +898,158 @@ extern "C" int simsd_thin_linear_silu_mul(const void* x, int64_t sxm, int64_t sx
   if (dtype == kBF16) dispatch_dt<kBF16>(pl, args, stream);
   else dispatch_dt<kF16>(pl, args, stream);
   return check_launch("thin_linear_silu_mul");
+}
+
+namespace {
+// Shared tail of the entry points: workspace check, dispatch, launch check.
+int run_planned(ThinPlan& pl, ThinArgs& args, int dtype, void* workspace, int64_t workspace_bytes,
+                hipStream_t stream, const char* what) {
+  if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535 || cdiv(args.M * args.N, 256) > 0x7fffffff)
+    return set_error("%s: grid too large (N=%lld, M=%lld)", what, (long long)args.N, (long long)args.M);
+  if (pl.split > 1) {
+    if (workspace == nullptr || workspace_bytes < pl.part_bytes)
+      return set_error("%s: split_k=%d needs a %lld-byte workspace (got %lld)", what, pl.split,
+                       (long long)pl.part_bytes, (long long)workspace_bytes);
+    if (!aligned16(workspace)) return set_error("%s: workspace must be 16-byte aligned", what);
+    args.part = static_cast<float*>(workspace);
+  }
+  switch (dtype) {
+    case kBF16: dispatch_dt<kBF16>(pl, args, stream); break;
+    case kF16: dispatch_dt<kF16>(pl, args, stream); break;
+    default: dispatch_dt<kF32>(pl, args, stream); break;
+  }
+  return check_launch(what);
+}
+
+int launch_rmsnorm(const void* x, int64_t sxm, const void* gamma, float eps, void* y, int64_t sym,
+                   int64_t M, int64_t K, int dtype, hipStream_t stream) {
+  const dim3 grid((unsigned)M), block(256);
+  const char* xc = static_cast<const char*>(x);
+  const char* gc = static_cast<const char*>(gamma);
+  char* yc = static_cast<char*>(y);
+  switch (dtype) {
+    case kBF16: hipLaunchKernelGGL(rmsnorm_kernel<kBF16>, grid, block, 0, stream, xc, sxm, gc, eps, yc, sym, K); break;
+    case kF16: hipLaunchKernelGGL(rmsnorm_kernel<kF16>, grid, block, 0, stream, xc, sxm, gc, eps, yc, sym, K); break;
+    default: hipLaunchKernelGGL(rmsnorm_kernel<kF32>, grid, block, 0, stream, xc, sxm, gc, eps, yc, sym, K); break;
+  }
+  return check_launch("rmsnorm");
+}
+
+inline int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" int simsd_rmsnorm(const void* x, int64_t sxm, const void* gamma, float eps, void* y,
+                             int64_t sym, int64_t M, int64_t K, int dtype, void* stream_) {
+  if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
+    return set_error("rmsnorm: unsupported dtype code %d", dtype);
+  if (M < 0 || K <= 0 || M > 0x7fffffff) return set_error("rmsnorm: bad sizes M=%lld K=%lld", (long long)M, (long long)K);
+  if (M == 0) return 0;
+  if (x == nullptr || gamma == nullptr || y == nullptr) return set_error("rmsnorm: null pointer");
+  return launch_rmsnorm(x, sxm, gamma, eps, y, sym, M, K, dtype, static_cast<hipStream_t>(stream_));
+}
+
+extern "C" int64_t simsd_rmsnorm_linear_workspace_bytes(int64_t M, int64_t N_rows, int64_t K, int dtype,
+                                                        int block_n, int split_k, int num_waves) {
+  const int64_t part = simsd_thin_linear_workspace_bytes(M, N_rows, K, dtype, block_n, split_k, num_waves);
+  if (part < 0) return -1;
+  return align256(M * K * esize_of(dtype)) + part;
+}
+
+extern "C" int simsd_rmsnorm_thin_linear(const void* x, int64_t sxm, int64_t sxk, const void* gamma,
+                                         float eps, const void* w, int64_t swn, int64_t swk,
+                                         const void* bias, int64_t sb, void* y, int64_t sym, int64_t syn,
+                                         int64_t M, int64_t N, int64_t K, int dtype, int block_n,
+                                         int block_k, int split_k, int num_waves, void* workspace,
+                                         int64_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
+    return set_error("rmsnorm_thin_linear: unsupported dtype code %d", dtype);
+  if (M < 0 || N < 0 || K <= 0) return set_error("rmsnorm_thin_linear: bad sizes");
+  if (M == 0 || N == 0) return 0;
+  if (x == nullptr || gamma == nullptr || w == nullptr || y == nullptr)
+    return set_error("rmsnorm_thin_linear: null pointer");
+  if (sxk != 1) return set_error("rmsnorm_thin_linear: x must be K-contiguous");
+  const int es = esize_of(dtype);
+  if (K * (int64_t)es > ((int64_t)1 << 31) - 64) return set_error("rmsnorm_thin_linear: K too large");
+  const int64_t xn_bytes = align256(M * K * es);
+  ThinPlan pl{};
+  if (make_plan(pl, x, sxm, sxk, w, swn, swk, M, N, K, dtype, block_n, block_k, split_k, num_waves) != 0)
+    return -1;
+  ThinArgs args{};
+  args.sxk = 1;
+  args.w = static_cast<const char*>(w); args.swn = swn; args.swk = swk;
+  args.bias = static_cast<const char*>(bias); args.sb = sb;
+  args.y = static_cast<char*>(y); args.sym = sym; args.syn = syn;
+  args.M = M; args.N = N; args.K = K;
+  if (pl.fast && pl.kind == 1 && aligned16(gamma)) {   // the norm runs inside the GEMV
+    pl.norm = true;
+    args.x = static_cast<const char*>(x); args.sxm = sxm;
+    args.gamma = static_cast<const char*>(gamma); args.eps = eps;
+    args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
+    return run_planned(pl, args, dtype, workspace, workspace_bytes, stream, "rmsnorm_thin_linear");
+  }
+  // otherwise: normalise into the workspace, then the plain linear on it
+  if (workspace == nullptr || workspace_bytes < xn_bytes || !aligned16(workspace))
+    return set_error("rmsnorm_thin_linear: needs a 16-byte aligned workspace of at least %lld bytes",
+                     (long long)xn_bytes);
+  char* xn = static_cast<char*>(workspace);
+  if (launch_rmsnorm(x, sxm, gamma, eps, xn, K, M, K, dtype, stream) != 0) return -1;
+  if (make_plan(pl, xn, K, 1, w, swn, swk, M, N, K, dtype, block_n, block_k, split_k, num_waves) != 0)
+    return -1;
+  args.x = xn; args.sxm = K;
+  args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
+  return run_planned(pl, args, dtype, xn + xn_bytes, workspace_bytes - xn_bytes, stream,
+                     "rmsnorm_thin_linear");
+}
+
+extern "C" int simsd_rmsnorm_thin_linear_silu_mul(const void* x, int64_t sxm, int64_t sxk,
+                                                  const void* gamma, float eps, const void* w_gate,
+                                                  int64_t sgn, int64_t sgk, const void* w_up, int64_t sun,
+                                                  int64_t suk, void* h, int64_t shm, int64_t shn,
+                                                  int64_t M, int64_t I, int64_t K, int dtype, int block_n,
+                                                  int block_k, int split_k, int num_waves, void* workspace,
+                                                  int64_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16)
+    return set_error("rmsnorm_thin_linear_silu_mul: dtype must be bf16 or fp16 (got code %d)", dtype);
+  if (M < 0 || I < 0 || K <= 0) return set_error("rmsnorm_thin_linear_silu_mul: bad sizes");
+  if (M == 0 || I == 0) return 0;
+  if (x == nullptr || gamma == nullptr || w_gate == nullptr || w_up == nullptr || h == nullptr)
+    return set_error("rmsnorm_thin_linear_silu_mul: null pointer");
+  if (sxk != 1) return set_error("rmsnorm_thin_linear_silu_mul: x must be K-contiguous");
+  const int es = esize_of(dtype);
+  if (K * (int64_t)es > ((int64_t)1 << 31) - 64) return set_error("rmsnorm_thin_linear_silu_mul: K too large");
+  const int64_t xn_bytes = align256(M * K * es);
+  ThinPlan pl{};
+  if (make_plan(pl, x, sxm, sxk, w_gate, sgn, sgk, M, 2 * I, K, dtype, block_n, block_k, split_k,
+                num_waves, true) != 0)
+    return -1;
+  if (!weight_vec_ok(w_up, sun, suk, I, K, es) || !weight_vec_ok(w_gate, sgn, sgk, I, K, es))
+    return set_error("rmsnorm_thin_linear_silu_mul: needs 16-byte aligned, K-contiguous w_gate and w_up");
+  ThinArgs args{};
+  args.sxk = 1;
+  args.w = static_cast<const char*>(w_gate); args.swn = sgn; args.swk = sgk;
+  args.w2 = static_cast<const char*>(w_up); args.sw2n = sun;
+  args.y = static_cast<char*>(h); args.sym = shm; args.syn = shn;
+  args.M = M; args.N = I; args.K = K;
+  if (pl.fast && pl.kind == 1 && aligned16(gamma)) {
+    pl.norm = true;
+    args.x = static_cast<const char*>(x); args.sxm = sxm;
+    args.gamma = static_cast<const char*>(gamma); args.eps = eps;
+    args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
+    return run_planned(pl, args, dtype, workspace, workspace_bytes, stream, "rmsnorm_thin_linear_silu_mul");
+  }
+  if (workspace == nullptr || workspace_bytes < xn_bytes || !aligned16(workspace))
+    return set_error("rmsnorm_thin_linear_silu_mul: needs a 16-byte aligned workspace of at least %lld bytes",
+                     (long long)xn_bytes);
+  char* xn = static_cast<char*>(workspace);
+  if (launch_rmsnorm(x, sxm, gamma, eps, xn, K, M, K, dtype, stream) != 0) return -1;
+  if (make_plan(pl, xn, K, 1, w_gate, sgn, sgk, M, 2 * I, K, dtype, block_n, block_k, split_k, num_waves,
+                true) != 0)
+    return -1;
+  if (!pl.fast) return set_error("rmsnorm_thin_linear_silu_mul: operands not vector-aligned");
+  args.x = xn; args.sxm = K;
+  args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
+  return run_planned(pl, args, dtype, xn + xn_bytes, workspace_bytes - xn_bytes, stream,
+                     "rmsnorm_thin_linear_silu_mul");
 }

@@ -5,7 +5,7 @@ Same API and behaviour as kernels/fused_toggle.py (reference, lines 30-202):
 ``fused_linear`` context manager, ``warmup``, ``apply_moe_to_model`` and
 ``is_moe_applied``; added: ``apply_gated_mlp_to_model`` /
 ``is_gated_mlp_applied`` (gate and up projections with SiLU·mul in one
-kernel).  The model code is third-party (loaded through
+kernel) and ``apply_rmsnorm_to_model`` (RMSNorm in one launch).  The model code is third-party (loaded through
 ``trust_remote_code``), so the switch patches modules in place rather than
 editing call sites: target linears are swapped for ``ThinLinear`` (which
 aliases the original parameters), and LLaDA2's MoE block gets a class-level
@@ -230,3 +230,43 @@ def apply_gated_mlp_to_model(model: nn.Module, enable: bool = True) -> int:
 
 def is_gated_mlp_applied(model: nn.Module) -> bool:
     return bool(_GATED.get(id(model)))
+
+
+# ─────────────────────────────────────────────────────────────────────────────
+# RMSNorm modules (SDARRMSNorm and its kind: .weight, .variance_epsilon)
+# ─────────────────────────────────────────────────────────────────────────────
+_NORMS: dict[int, list[nn.Module]] = {}
+
+
+def apply_rmsnorm_to_model(model: nn.Module, enable: bool = True) -> int:
+    """Run every RMSNorm module (class name ending in ``RMSNorm`` with
+    ``weight`` and ``variance_epsilon``) as one ``thin_rmsnorm`` launch instead
+    of the stock five-op form.  Idempotent both ways; returns how many modules
+    were switched or restored."""
+    from .thin_linear_fused import thin_rmsnorm
+
+    key = id(model)
+    if not enable:
+        mods = _NORMS.pop(key, [])
+        for mod in mods:
+            mod.__dict__.pop("forward", None)
+        return len(mods)
+    done = _NORMS.setdefault(key, [])
+    n = 0
+    for mod in model.modules():
+        if not (mod.__class__.__name__.endswith("RMSNorm") and hasattr(mod, "weight")
+                and hasattr(mod, "variance_epsilon")):
+            continue
+        if any(m is mod for m in done):
+            continue
+        stock = mod.forward
+
+        def forward(x, _mod=mod, _stock=stock):
+            if x.device.type != "cuda" or _mod.weight.dtype != x.dtype:
+                return _stock(x)
+            return thin_rmsnorm(x, _mod.weight, _mod.variance_epsilon)
+
+        mod.forward = forward
+        done.append(mod)
+        n += 1
+    return n

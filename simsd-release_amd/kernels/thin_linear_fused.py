@@ -8,7 +8,8 @@ argument meaning and the same exceptions.  The arithmetic runs in a
 hand-written gfx950 HIP kernel (``libsimsd_kernels.so``, C ABI in
 ``include/simsd_kernels.h``) instead of Triton.  Added on top:
 ``thin_linear_silu_mul``, an MLP's gate and up projections with the SiLU and
-product in the same kernel.
+product in the same kernel; ``thin_rmsnorm`` (one launch) and the RMSNorm
+prologue forms ``thin_rmsnorm_linear`` / ``thin_rmsnorm_linear_silu_mul``.
 
 How the MI355X kernels work (``csrc/thin_gemm.hip``)
 -----------------------------------------------------
@@ -357,6 +358,133 @@ def thin_linear_silu_mul(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tens
             ws.data_ptr() if ws is not None else None, ws_bytes,
             _native.stream_of(dev))
     _native.check(status, "thin_linear_silu_mul")
+    return h.view(out_shape)
+
+
+def _launch_config(M: int, N_rows: int, K: int, itemsize: int, config, num_warps):
+    """(block_n, block_k, split_k, waves) for a call: explicit config, else
+    TUNED for (K, N_rows), else the heuristic."""
+    if config is not None:
+        block_n, block_k, split_k = int(config[1]), int(config[2]), int(config[3])
+        waves = num_warps or _DEFAULT_WAVES
+    else:
+        tuned = _tuned_for(M, N_rows, K)
+        if tuned is not None:
+            _, block_n, block_k, split_k, waves, _ = tuned
+        else:
+            _, block_n, block_k, split_k = _heuristic_config(M, N_rows, K, itemsize)
+            waves = _DEFAULT_WAVES
+        waves = num_warps or waves
+    if split_k < 1:
+        raise ValueError(f"SPLIT_K must be >= 1, got {split_k}")
+    return _rows_for(block_n), block_k, split_k, (2 if waves <= 2 else (4 if waves <= 4 else 8))
+
+
+def _norm_args(x: torch.Tensor, weight: torch.Tensor):
+    if weight.ndim != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError(f"RMSNorm weight must be [{x.shape[-1]}], got {tuple(weight.shape)}")
+    if weight.dtype != x.dtype:
+        raise TypeError(f"RMSNorm weight dtype {weight.dtype} != x dtype {x.dtype}")
+    code = _native.DTYPE_CODES.get(x.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {x.dtype} (bf16, fp16 or fp32)")
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2, weight.contiguous(), code
+
+
+def thin_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm in one launch: ``weight * (x * rsqrt(mean(x^2) + eps)).to(x.dtype)``
+    with the fp32 statistics and the rounding points of the stock PyTorch
+    form (SDARRMSNorm, sdar/modeling_sdar.py:74-92; sdar/run_native_tp2.py:42-47)."""
+    x2, g, code = _norm_args(x, weight)
+    dev = _native.require_device(x2, g)
+    M, K = x2.shape
+    y = torch.empty((M, K), device=dev, dtype=x.dtype)
+    if M == 0:
+        return y.view(x.shape)
+    with _native.device_guard(dev):
+        st = _native.lib().simsd_rmsnorm(x2.data_ptr(), x2.stride(0), g.data_ptr(), float(eps),
+                                         y.data_ptr(), y.stride(0), M, K, code, _native.stream_of(dev))
+    _native.check(st, "rmsnorm")
+    return y.view(x.shape)
+
+
+def thin_rmsnorm_linear(x: torch.Tensor, weight: torch.Tensor, eps: float, w: torch.Tensor,
+                        bias: torch.Tensor | None = None, config=None, num_warps=None) -> torch.Tensor:
+    """``thin_linear(thin_rmsnorm(x, weight, eps), w, bias)``; at <= 8 tokens the
+    norm runs inside the GEMV and the normalised rows never reach memory."""
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad):
+        raise RuntimeError("thin_rmsnorm_linear is a forward-only inference kernel")
+    if w.ndim != 2 or w.shape[1] != x.shape[-1]:
+        raise ValueError(f"w must be [N, {x.shape[-1]}], got {tuple(w.shape)}")
+    if w.dtype != x.dtype:
+        raise TypeError(f"dtype mismatch: x={x.dtype} w={w.dtype}")
+    x2, g, code = _norm_args(x, weight)
+    dev = _native.require_device(x2, g, w)
+    (M, K), N = x2.shape, w.shape[0]
+    out_shape = (*x.shape[:-1], N)
+    if M == 0 or N == 0:
+        return torch.zeros(out_shape, device=dev, dtype=x.dtype)
+    block_n, block_k, split_k, waves = _launch_config(M, N, K, x.element_size(), config, num_warps)
+    fuse_bias = (bias is not None and bias.dtype == x.dtype and bias.ndim == 1
+                 and bias.shape[0] == N and bias.device == dev)
+    lib = _native.lib()
+    need = lib.simsd_rmsnorm_linear_workspace_bytes(M, N, K, code, block_n, split_k, waves)
+    if need < 0:
+        _native.check(-1, "rmsnorm_thin_linear")
+    ws = _partials(dev, need)
+    y = torch.empty((M, N), device=dev, dtype=x.dtype)
+    with _native.device_guard(dev):
+        st = lib.simsd_rmsnorm_thin_linear(
+            x2.data_ptr(), x2.stride(0), 1, g.data_ptr(), float(eps),
+            w.data_ptr(), w.stride(0), w.stride(1),
+            bias.data_ptr() if fuse_bias else None, bias.stride(0) if fuse_bias else 0,
+            y.data_ptr(), y.stride(0), y.stride(1), M, N, K, code, block_n, block_k, split_k, waves,
+            ws.data_ptr(), ws.numel(), _native.stream_of(dev))
+    _native.check(st, "rmsnorm_thin_linear")
+    if bias is not None and not fuse_bias:
+        y += bias
+    return y.view(out_shape)
+
+
+def thin_rmsnorm_linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                                 w_gate: torch.Tensor, w_up: torch.Tensor,
+                                 config=None, num_warps=None) -> torch.Tensor:
+    """``thin_linear_silu_mul(thin_rmsnorm(x, weight, eps), w_gate, w_up)``: an
+    MLP block's norm, gate and up projections, SiLU and product; at <= 8
+    tokens in one kernel.  bf16/fp16 with vector-aligned weights; other
+    inputs go through the two separate ops."""
+    if torch.is_grad_enabled() and (x.requires_grad or w_gate.requires_grad or w_up.requires_grad):
+        raise RuntimeError("thin_rmsnorm_linear_silu_mul is a forward-only inference kernel")
+    if not (x.dtype == w_gate.dtype == w_up.dtype):
+        raise TypeError(f"dtype mismatch: x={x.dtype} w_gate={w_gate.dtype} w_up={w_up.dtype}")
+    if w_gate.ndim != 2 or w_up.shape != w_gate.shape or w_gate.shape[1] != x.shape[-1]:
+        raise ValueError(f"w_gate and w_up must both be [I, {x.shape[-1]}]")
+    x2, g, code = _norm_args(x, weight)
+    dev = _native.require_device(x2, g, w_gate, w_up)
+    (M, K), I = x2.shape, w_gate.shape[0]
+    out_shape = (*x.shape[:-1], I)
+    if M == 0 or I == 0:
+        return torch.zeros(out_shape, device=dev, dtype=x.dtype)
+    if code == _native.DTYPE_CODES[torch.float32] or not (_vec_rows(w_gate) and _vec_rows(w_up)):
+        return thin_linear_silu_mul(thin_rmsnorm(x2, g, eps), w_gate, w_up).view(out_shape)
+    block_n, block_k, split_k, waves = _launch_config(M, 2 * I, K, x.element_size(), config, num_warps)
+    lib = _native.lib()
+    need = lib.simsd_rmsnorm_linear_workspace_bytes(M, 2 * I, K, code, block_n, split_k, waves)
+    if need < 0:
+        _native.check(-1, "rmsnorm_thin_linear_silu_mul")
+    ws = _partials(dev, need)
+    h = torch.empty((M, I), device=dev, dtype=x.dtype)
+    with _native.device_guard(dev):
+        st = lib.simsd_rmsnorm_thin_linear_silu_mul(
+            x2.data_ptr(), x2.stride(0), 1, g.data_ptr(), float(eps),
+            w_gate.data_ptr(), w_gate.stride(0), w_gate.stride(1),
+            w_up.data_ptr(), w_up.stride(0), w_up.stride(1),
+            h.data_ptr(), h.stride(0), h.stride(1), M, I, K, code, block_n, block_k, split_k, waves,
+            ws.data_ptr(), ws.numel(), _native.stream_of(dev))
+    _native.check(st, "rmsnorm_thin_linear_silu_mul")
     return h.view(out_shape)
 
 

@@ -316,3 +316,25 @@ def test_gated_mlp_toggle_host():
     x = torch.randn(3, 16)
     with torch.no_grad():                                   # the stock CPU path is back
         assert model(x).shape == (3, 16)
+
+
+def test_rmsnorm_toggle_host():
+    import torch.nn as nn
+    from kernels.fused_toggle import apply_rmsnorm_to_model
+
+    class TinyRMSNorm(nn.Module):
+        def __init__(self, n):
+            super().__init__()
+            self.weight = nn.Parameter(torch.ones(n))
+            self.variance_epsilon = 1e-6
+
+        def forward(self, x):
+            return x
+
+    model = nn.Sequential(TinyRMSNorm(8), nn.LayerNorm(8), TinyRMSNorm(8))
+    assert apply_rmsnorm_to_model(model) == 2
+    assert apply_rmsnorm_to_model(model) == 0
+    x = torch.randn(2, 8)
+    assert torch.equal(model[0](x), x)          # CPU tensors keep the stock forward
+    assert apply_rmsnorm_to_model(model, enable=False) == 2
+    assert "forward" not in model[0].__dict__

@@ -120,6 +120,39 @@ def test_gated_exact_vs_torch_cpu_composition():
         assert not np.array_equal(bad, ref), name
 
 
+def _stock_rmsnorm(x, w, eps):
+    x32 = x.float()
+    var = x32.pow(2).mean(-1, keepdim=True)
+    return w * (x32 * torch.rsqrt(var + eps)).to(x.dtype)
+
+
+def test_rmsnorm_exact_vs_torch_stock_form():
+    """rmsnorm_exact against the stock PyTorch RMSNorm on the CPU (the form
+    sdar/run_native_tp2.py installs); its fp64 statistics may move x * r by
+    one unit in the last place, which the product with the weight can carry
+    to two.  Planted slips fail."""
+    g = torch.Generator().manual_seed(9)
+    for dt, name in ((torch.bfloat16, "bf16"), (torch.float16, "fp16")):
+        for M, K in [(1, 2048), (4, 4096), (16, 1000)]:
+            x = (torch.randn(M, K, generator=g) * 3).to(dt)
+            w = (1 + 0.2 * torch.randn(K, generator=g)).to(dt)
+            ref = othin.rmsnorm_exact(x.float().numpy(), w.float().numpy(), 1e-6, dtype=name)
+            t = _stock_rmsnorm(x, w, 1e-6).float().numpy()
+            ulp = 2.0 ** (-7 if name == "bf16" else -10)
+            assert np.all(np.abs(ref - t) <= 2 * ulp * np.abs(ref) + 1e-30)
+            assert (ref != t).mean() < 0.01
+    x = (torch.randn(4, 512, generator=g) * 3).bfloat16()
+    w = (1 + 0.2 * torch.randn(512, generator=g)).bfloat16()
+    xf, wf = x.float().numpy().astype(np.float64), w.float().numpy().astype(np.float64)
+    ref = othin.rmsnorm_exact(xf, wf, 1e-6)
+    r = 1 / np.sqrt((xf * xf).mean(-1, keepdims=True) + 1e-6)
+    slips = {"one rounding": round_bf16(wf * xf * r),
+             "sum for mean": round_bf16(wf * round_bf16(xf / np.sqrt((xf * xf).sum(-1, keepdims=True) + 1e-6))),
+             "no weight": round_bf16(xf * r)}
+    for name, bad in slips.items():
+        assert not np.array_equal(bad, ref), name
+
+
 # ─────────────────────────────────────────────────────────────── route ───
 def test_route_ids_golden(golden):
     d = golden("route")

@@ -455,6 +455,88 @@ def test_gated_mlp_toggle_end_to_end():
     assert float((fused.float() - stock.float()).abs().max()) <= tol(stock)
 
 
+# ───────────────────────────────────────────────── RMSNorm and its prologue ───
+def _norm_case(M, K, dtype, seed):
+    x = rnd(M, K, dtype=dtype, scale=3.0, seed=seed)
+    w = (1 + 0.2 * torch.randn(K, generator=torch.Generator(device=DEV).manual_seed(seed + 1),
+                               device=DEV)).to(dtype)
+    return x, w
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
+def test_rmsnorm_vs_oracle(dtype):
+    from kernels.thin_linear_fused import thin_rmsnorm
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
+    ulp = {"bf16": 2.0 ** -7, "fp16": 2.0 ** -10, "fp32": 2.0 ** -20}[dtype]
+    for M, K in [(1, 2048), (4, 2048), (32, 4096), (100, 1000), (3, 77)]:
+        x, w = _norm_case(M, K, tdt, seed=M + K)
+        with torch.inference_mode():
+            got = thin_rmsnorm(x, w, 1e-6).float().cpu().numpy()
+        ref = othin.rmsnorm_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), 1e-6, dtype=dtype)
+        assert np.all(np.abs(got - ref) <= 2 * ulp * np.abs(ref) + 1e-30), (M, K)   # 2 ulp: see the oracle test
+    x, w = _norm_case(8, 512, tdt, seed=3)
+    with torch.inference_mode():
+        assert torch.equal(thin_rmsnorm(x, w, 1e-5), thin_rmsnorm(x, w, 1e-5))     # deterministic
+        assert thin_rmsnorm(x.view(2, 4, 512), w, 1e-5).shape == (2, 4, 512)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_rmsnorm_linear_vs_oracle(M, dtype):
+    """The fused norm + linear (norm inside the GEMV at M <= 8, a separate
+    launch above) against the oracle's norm then exact linear."""
+    from kernels.thin_linear_fused import thin_rmsnorm_linear, thin_rmsnorm_linear_silu_mul
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    for K, N in [(2048, 4096), (1000, 531)]:
+        x, g = _norm_case(M, K, tdt, seed=90 + M)
+        w = rnd(2 * N, K, dtype=tdt, scale=0.02, seed=91 + K)
+        xn = othin.rmsnorm_exact(x.float().cpu().numpy(), g.float().cpu().numpy(), 1e-6, dtype=dtype)
+        wn = w.float().cpu().numpy()
+        with torch.inference_mode():
+            y = thin_rmsnorm_linear(x, g, 1e-6, w[:N]).float().cpu().numpy()
+            h = thin_rmsnorm_linear_silu_mul(x, g, 1e-6, w[:N], w[N:]).float().cpu().numpy()
+        ref_y = othin.linear_exact(xn, wn[:N], dtype=dtype)
+        ref_h = othin.gated_exact(xn, wn[:N], wn[N:], dtype=dtype)
+        for got, ref in ((y, ref_y), (h, ref_h)):
+            err = float(np.abs(got - ref).max())
+            assert err <= othin.tolerance(float(np.abs(ref).max()), dtype), (M, K, N, err)
+            assert othin.max_abs_rel(got, ref) <= 1e-2
+
+
+def test_rmsnorm_linear_configs_bias_and_toggle():
+    from kernels.fused_toggle import apply_rmsnorm_to_model
+    from kernels.thin_linear_fused import thin_rmsnorm, thin_rmsnorm_linear
+    x, g = _norm_case(4, 1000, torch.bfloat16, seed=7)
+    w, b = rnd(333, 1000, scale=0.03, seed=8), rnd(333, scale=0.5, seed=9)
+    with torch.inference_mode():
+        ref = F.linear(thin_rmsnorm(x, g, 1e-6), w, b)
+        for rows in (4, 8, 16, 32):
+            for split in (1, 3):
+                got = thin_rmsnorm_linear(x, g, 1e-6, w, b, config=(16, rows, 256, split))
+                assert float((got.float() - ref.float()).abs().max()) <= tol(ref), (rows, split)
+
+    class TinyRMSNorm(nn.Module):
+        def __init__(self, n):
+            super().__init__()
+            self.weight = nn.Parameter(torch.ones(n))
+            self.variance_epsilon = 1e-6
+
+        def forward(self, h):
+            h32 = h.float()
+            return self.weight * (h32 * torch.rsqrt(h32.pow(2).mean(-1, keepdim=True)
+                                                    + self.variance_epsilon)).to(h.dtype)
+
+    m = TinyRMSNorm(1000).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        m.weight.copy_(g)
+        stock = m(x)
+        assert apply_rmsnorm_to_model(m) == 1
+        fused = m(x)
+        apply_rmsnorm_to_model(m, enable=False)
+    ulp = 2.0 ** -7
+    assert torch.all((fused.float() - stock.float()).abs() <= 2 * ulp * stock.float().abs() + 1e-30)
+
+
 # ───────────────────────────────────────────── size-independent properties ───
 def test_properties_at_full_size():
     from kernels.thin_linear_fused import thin_linear
