@@ -21,6 +21,12 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           the linear path of each decoder layer with the fused epilogues:
           RMSNorm + qkv, o, RMSNorm + gate/up + SiLU-mul, down (four launches),
           against the unfused sequence with the stock PyTorch RMSNorm.
+  head4 / head32
+          the lm_head with its epilogue: the draft's denoise step on a 4-token
+          block (lm_head 2048->151936, softmax/argmax/confidence, masked
+          unmasking) and the target's verify pass over 32 rows (lm_head
+          4096->151936, softmax probabilities of the 16 mask rows), fused
+          against the reference's torch sequence.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
@@ -412,6 +418,89 @@ def run_layer(args, torch, dev):
     }, M
 
 
+# ─────────────────────────────────────────────── lm_head + its epilogue ───
+def run_head(args, torch, dev):
+    """The lm_head and what follows it, fused against the reference's torch
+    sequence.  head4: the draft's denoise step on a 4-token block (lm_head
+    2048 -> 151936, softmax, argmax, confidence, masked top-1 unmasking with
+    its step map and probability row; cache_aware.py:914-938).  head32: the
+    target's verify pass over 32 rows (lm_head 4096 -> 151936, then softmax
+    probabilities and argmax of the 16 mask rows; cache_aware.py:1197-1198)."""
+    from kernels.logits_fused import denoise_select, softmax_argmax
+    from kernels.thin_linear_fused import thin_linear
+    F = torch.nn.functional
+
+    M, K = (4, 2048) if args.workload == "head4" else (32, 4096)
+    V = 151936
+    mask_id = V - 1
+    g = torch.Generator(device=dev).manual_seed(77)
+    ws = [(torch.randn(V, K, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    xs = [torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16) for _ in range(2)]
+    cur0 = torch.full((M,), mask_id, dtype=torch.int64, device=dev)
+    cur = cur0.clone()
+    step_map = torch.zeros(M, dtype=torch.int64, device=dev)
+    ppp = torch.zeros(M, V, dtype=torch.float32, device=dev)
+    lin_bytes = V * K * 2 + M * K * 2 + M * V * 2
+
+    def fused():
+        out = []
+        for x, w in zip(xs, ws):
+            if M == 4:
+                cur.copy_(cur0)
+                out.append(denoise_select(thin_linear(x, w), cur, mask_id, 1, 0, step_map, ppp))
+            else:
+                out.append(softmax_argmax(thin_linear(x, w)[16:32], return_probs=True))
+        return out
+
+    def unfused():
+        out = []
+        for x, w in zip(xs, ws):
+            logits = thin_linear(x, w)
+            if M == 4:
+                cur.copy_(cur0)
+                probs = F.softmax(logits.float(), dim=-1)
+                pred = probs.argmax(dim=-1)
+                conf = probs.gather(1, pred.unsqueeze(-1)).squeeze(-1)
+                masked_conf = torch.where(cur == mask_id, conf, torch.full_like(conf, float("-inf")))
+                _, top = masked_conf.topk(1)
+                cur.scatter_(0, top, pred.gather(0, top))
+                step_map.scatter_(0, top, torch.full_like(top, 0))
+                ppp.index_copy_(0, top, probs.index_select(0, top))
+                out.append((pred, conf))
+            else:
+                probs = F.softmax(logits[16:32].float(), dim=-1)
+                out.append((probs.argmax(dim=-1), probs))
+        return out
+
+    with torch.inference_mode():
+        fused()
+        unfused()
+        torch.cuda.synchronize()
+        us_unfused = graph_us_per_call(torch, [unfused], reps=max(5, args.steps // 5)) / len(ws)
+        us_fused = graph_us_per_call(torch, [fused], reps=args.steps) / len(ws)
+        us_linear = graph_us_per_call(torch, [lambda x=x, w=w: thin_linear(x, w) for x, w in zip(xs, ws)],
+                                      reps=args.steps)
+    gbs = lin_bytes / (us_fused * 1e-6) / 1e9
+    return {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": 1, "ms_per_step": round(us_fused / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": ("draft-denoise-step-lm_head-M4-K2048-V151936" if M == 4 else
+                                "target-verify-lm_head-M32-K4096-V151936-probs16"),
+                   "M": M, "algorithmic_bytes_per_step": lin_bytes, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "lm_head thin_linear + softmax/argmax epilogue (3 launches)"},
+        "us_per_step": round(us_fused, 2),
+        "lm_head_alone_us": round(us_linear, 2),
+        "epilogue_us": round(us_fused - us_linear, 2),
+        "unfused_us_per_step": round(us_unfused, 2),
+        "unfused_epilogue_us": round(us_unfused - us_linear, 2),
+        "fused_speedup": round(us_unfused / us_fused, 3),
+    }, M
+
+
 # ────────────────────────────────────────────────────────────────── MoE ───
 def run_moe(args, torch, dev):
     from kernels.moe_dispatch_fused import moe_forward, moe_route
@@ -547,7 +636,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -565,8 +654,9 @@ def main():
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
         return
-    if args.workload.startswith("mlp") or args.workload.startswith("layer"):
-        result, _ = (run_mlp if args.workload.startswith("mlp") else run_layer)(args, torch, dev)
+    if args.workload.startswith(("mlp", "layer", "head")):
+        runner = {"mlp": run_mlp, "layer": run_layer, "head": run_head}[args.workload.rstrip("0123456789")]
+        result, _ = runner(args, torch, dev)
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)
         return

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 5
+#define SIMSD_ABI_VERSION 6
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -207,6 +207,37 @@ int simsd_moe_grouped_ffn(const void* x, int64_t stride_xt, int64_t stride_xh,
                           void* out, int64_t stride_ot, int64_t stride_oh,
                           int64_t T, int k, int64_t E, int64_t H, int64_t I, int dtype,
                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- logits epilogue: softmax statistics and the unmasking choice -------
+ * For logits rows l[m, 0:V] (bf16, fp16 or fp32; row stride slm elements,
+ * unit element stride):
+ *   ids[m]  = the first index of the row maximum (int64),
+ *   conf[m] = its softmax probability 1 / sum_v exp(l[m, v] - max) (fp32),
+ *   probs[m, v] = exp(l[m, v] - max) / sum (fp32, row stride spm; NULL to skip),
+ * i.e. probs = F.softmax(logits.float(), -1), ids = probs.argmax(-1),
+ * conf = probs.gather(1, ids): the epilogue of the draft denoise step,
+ * speculative_decoding/cache_aware.py:916-919, and the verify pass's
+ * target_probs, cache_aware.py:1197-1198.  All sums run in a fixed order
+ * (bit-reproducible).  Workspace: simsd_softmax_argmax_workspace_bytes(M, V),
+ * 16-byte aligned, no initialisation needed. */
+int64_t simsd_softmax_argmax_workspace_bytes(int64_t M, int64_t V);
+
+int simsd_softmax_argmax(const void* logits, int64_t slm, int64_t M, int64_t V, int dtype, int64_t* ids,
+                         float* conf, float* probs, int64_t spm, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/* One unmasking step of the draft's block denoise loop, in place,
+ * cache_aware.py:916-938: ids/conf as above for the M <= 64 rows of the
+ * block; among the rows with cur_ids[m] == mask_id, the n_unmask with the
+ * largest conf (ties: the lower row; rows not masked rank as -inf, as in the
+ * reference's masked_conf.topk) get cur_ids[m] = ids[m], step_map[m] = step
+ * (step_map may be NULL) and, when per_pos_probs is not NULL, their softmax
+ * row written to per_pos_probs[m, :] (row stride spp).  Workspace as for
+ * simsd_softmax_argmax. */
+int simsd_denoise_select(const void* logits, int64_t slm, int64_t M, int64_t V, int dtype, int64_t* cur_ids,
+                         int64_t mask_id, int n_unmask, int64_t* step_map, int64_t step, float* per_pos_probs,
+                         int64_t spp, int64_t* ids, float* conf, void* workspace, int64_t workspace_bytes,
+                         void* stream);
 
 #ifdef __cplusplus
 }

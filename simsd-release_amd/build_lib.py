@@ -10,10 +10,12 @@ disabled (the compiler would otherwise form v_pk_*_f32 from plain float code).
 from __future__ import annotations
 
 import argparse
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
@@ -21,7 +23,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "kernels", "libsimsd_kernels.so")
 
-SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip"]
+SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip", "logits.hip"]
 ARCH = os.environ.get("SIMSD_OFFLOAD_ARCH", "gfx950")
 
 
@@ -32,22 +34,22 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def command(out: str = OUT, extra=()) -> list[str]:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+def flags(extra=()) -> list[str]:
     return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
-        "-I", INCLUDE, "-I", CSRC, *extra, "-o", out, *srcs,
+        "-I", INCLUDE, "-I", CSRC, *extra,
     ]
 
 
-def build(verbose: bool = False, out: str = OUT) -> str:
-    cmd = command(out)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    tmp = out + ".tmp"
-    cmd[cmd.index("-o") + 1] = tmp
+def command(out: str = OUT, extra=()) -> list[str]:
+    """The equivalent single hipcc line (what --verbose prints)."""
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    return [hipcc(), *flags(extra), "-shared", "-o", out, *srcs]
+
+
+def _run(cmd: list[str]) -> str:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # The host pass does not know the packed-fp32 feature and says so; that
     # line is expected.  Anything else on stderr is shown.
@@ -55,8 +57,25 @@ def build(verbose: bool = False, out: str = OUT) -> str:
     errs = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{errs}")
-    if errs.strip() and verbose:
-        print(errs, file=sys.stderr)
+    return errs
+
+
+def build(verbose: bool = False, out: str = OUT, extra=()) -> str:
+    """Compile every source to an object in parallel, then link the library
+    (same result as the single line from command())."""
+    if verbose:
+        print(" ".join(command(out, extra)), flush=True)
+    with tempfile.TemporaryDirectory(prefix="simsd_build_") as tmpdir:
+        objs = [os.path.join(tmpdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+        jobs = [[hipcc(), *flags(extra), "-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+        workers = max(1, min(len(jobs), os.cpu_count() or 1, 8))
+        with concurrent.futures.ThreadPoolExecutor(workers) as pool:
+            errs = list(pool.map(_run, jobs))
+        tmp = out + ".tmp"
+        errs.append(_run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]))
+    text = "\n".join(e for e in errs if e.strip())
+    if text and verbose:
+        print(text, file=sys.stderr)
     os.replace(tmp, out)
     return out
 
