@@ -27,6 +27,11 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           unmasking) and the target's verify pass over 32 rows (lm_head
           4096->151936, softmax probabilities of the 16 mask rows), fused
           against the reference's torch sequence.
+  attn4 / attn32
+          attention of the block over the static KV cache per layer: q/k norm +
+          RoPE + cache write, then attention over 1024 slots (28 draft layers,
+          4 rows, 16/8 heads; 36 target layers, 32 rows, 32/8 heads), against
+          the reference's sequence on its GQA-expanded cache.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
@@ -501,6 +506,104 @@ def run_head(args, torch, dev):
     }, M
 
 
+# ──────────────────────────────────────── attention over the static cache ───
+def run_attn(args, torch, dev):
+    """Per layer: q/k RMSNorm + RoPE + KV-cache write of the block's rows
+    (one launch), then attention over a 1024-slot context (two launches).
+    attn4: 28 draft layers, 4 rows, 16 query / 8 KV heads; attn32: 36 target
+    layers, 32 rows (4 verify blocks), 32 / 8 heads.  The unfused timing is the
+    reference's sequence (stock norms, apply_rotary_pos_emb, index_copy_ into
+    the GQA-expanded cache, SDPA with the bool mask; SDPA pinned to its
+    efficient kernel in bf16) on the same data."""
+    from kernels.attention_fused import (BlockKVCache, block_attention, default_inv_freq, qkv_rope_cache,
+                                         rope_tables)
+    F = torch.nn.functional
+    M, Hq, L_layers = (4, 16, 28) if args.workload == "attn4" else (32, 32, 36)
+    Hkv, D, ctx, eps = 8, 128, 1024 - M, 1e-6
+    n_rep = Hq // Hkv
+    cache = BlockKVCache(L_layers, Hkv, ctx, M, dev)
+    g = torch.Generator(device=dev).manual_seed(90)
+    for lay in range(L_layers):
+        cache.key_cache[lay].normal_(generator=g)
+        cache.value_cache_t[lay].normal_(generator=g)
+    cos, sin = rope_tables(default_inv_freq(device=dev), 4096, torch.bfloat16)
+    qkvs = [torch.randn(M, (Hq + 2 * Hkv) * D, device=dev, generator=g).bfloat16() for _ in range(L_layers)]
+    qn = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).bfloat16()
+    kn = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).bfloat16()
+    pos = torch.arange(ctx, ctx + M, device=dev)
+    slots = torch.arange(cache.max_cache_len, cache.max_cache_len + M, device=dev)
+    L = cache.max_cache_len + M
+    mask = torch.zeros(M, cache.full_len, dtype=torch.bool, device=dev)
+    mask[:, :ctx] = True
+    mask[:, ctx:ctx + M] = torch.tril(torch.ones(M, M, dtype=torch.bool, device=dev))
+    kv_bytes = Hkv * L * D * 2 * 2
+    step_bytes = L_layers * (kv_bytes + M * (Hq + 2 * Hkv) * D * 2 + 2 * M * Hq * D * 2)
+
+    def fused():
+        return [block_attention(qkv_rope_cache(x, Hq, qn, kn, eps, cos, sin, pos, slots, cache, lay),
+                                cache, lay, mask, valid_len=L) for lay, x in enumerate(qkvs)]
+
+    # the reference's expanded cache ([1, Hq, L, D]) holding the same context
+    kexp = [cache.key_cache[lay].repeat_interleave(n_rep, 0)[None].contiguous() for lay in range(L_layers)]
+    vexp = [cache.value_cache(lay).repeat_interleave(n_rep, 0)[None].contiguous() for lay in range(L_layers)]
+    c, s_ = cos[pos][:, None], sin[pos][:, None]
+
+    def norm(t, w):
+        t32 = t.float()
+        return w * (t32 * torch.rsqrt(t32.pow(2).mean(-1, keepdim=True) + eps)).to(t.dtype)
+
+    def rope(t):
+        return (t * c) + (torch.cat((-t[..., 64:], t[..., :64]), dim=-1) * s_)
+
+    def unfused():
+        outs = []
+        for lay, x in enumerate(qkvs):
+            h = x.view(M, Hq + 2 * Hkv, D)
+            q = rope(norm(h[:, :Hq], qn)).transpose(0, 1)[None]
+            k = rope(norm(h[:, Hq:Hq + Hkv], kn)).transpose(0, 1)[None]
+            v = h[:, Hq + Hkv:].transpose(0, 1)[None]
+            for i in range(n_rep):
+                kexp[lay][:, i::n_rep].index_copy_(2, slots, k)
+                vexp[lay][:, i::n_rep].index_copy_(2, slots, v)
+            o = F.scaled_dot_product_attention(q, kexp[lay], vexp[lay], attn_mask=mask[None, None],
+                                               scale=D ** -0.5)
+            outs.append(o.transpose(1, 2).reshape(M, Hq * D))
+        return outs
+
+    with torch.inference_mode():
+        fused()
+        torch.cuda.synchronize()
+        us_fused = graph_us_per_call(torch, [fused], reps=args.steps)
+        us_unfused, note = None, None
+        try:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            with sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION]):
+                unfused()
+                torch.cuda.synchronize()
+                us_unfused = graph_us_per_call(torch, [unfused], reps=max(5, args.steps // 5))
+        except RuntimeError as e:   # no efficient bf16 kernel with a bool mask on this build
+            note = f"reference sequence not timed: {str(e).splitlines()[0][:160]}"
+    ms = us_fused / 1e3
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    out = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": 1, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"block-attention-{L_layers}L-M{M}-Hq{Hq}-Hkv{Hkv}-ctx{L}", "M": M,
+                   "context_slots": L, "algorithmic_bytes_per_step": step_bytes, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "qkv_rope_cache + attn_partial + attn_combine per layer"},
+        "us_per_layer": round(us_fused / L_layers, 3),
+        "unfused_us_per_layer": None if us_unfused is None else round(us_unfused / L_layers, 3),
+        "fused_speedup": None if us_unfused is None else round(us_unfused / us_fused, 3),
+    }
+    if note:
+        out["note"] = note
+    return out, M
+
+
 # ────────────────────────────────────────────────────────────────── MoE ───
 def run_moe(args, torch, dev):
     from kernels.moe_dispatch_fused import moe_forward, moe_route
@@ -636,7 +739,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -654,8 +757,9 @@ def main():
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
         return
-    if args.workload.startswith(("mlp", "layer", "head")):
-        runner = {"mlp": run_mlp, "layer": run_layer, "head": run_head}[args.workload.rstrip("0123456789")]
+    if args.workload.startswith(("mlp", "layer", "head", "attn")):
+        runner = {"mlp": run_mlp, "layer": run_layer, "head": run_head,
+                  "attn": run_attn}[args.workload.rstrip("0123456789")]
         result, _ = runner(args, torch, dev)
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)

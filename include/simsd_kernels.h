@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 6
+#define SIMSD_ABI_VERSION 7
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -238,6 +238,48 @@ int simsd_denoise_select(const void* logits, int64_t slm, int64_t M, int64_t V, 
                          int64_t mask_id, int n_unmask, int64_t* step_map, int64_t step, float* per_pos_probs,
                          int64_t spp, int64_t* ids, float* conf, void* workspace, int64_t workspace_bytes,
                          void* stream);
+
+/* ---- attention over a static KV cache ----------------------------------
+ * Cache layout per layer (one sequence, head_dim D = 128): K [Hkv, L, D]
+ * (strides skh, skl) and V transposed, Vt [Hkv, D, L] (strides svh, svd).
+ * The KV heads are stored once per group, not replicated per query head.
+ *
+ * simsd_qkv_rope_cache: for each of the M tokens of qkv [M, (Hq + 2 Hkv) * D]
+ * (q heads, then k heads, then v heads; row stride sqkv), the SDAR attention
+ * prologue, sdar/modeling_sdar.py:250-262: q and k heads through their
+ * RMSNorm (stock rounding points; weights q_norm_w / k_norm_w [D], NULL to
+ * skip), then RoPE with the cos/sin rows of pos[m] (tables [n_pos, D], row
+ * stride scs, as the rotary embedding returns them, in the dtype):
+ *   out = dtype(dtype(x * cos) + dtype(rotate_half(x) * sin)),
+ * q to q_out [M, Hq, D] (strides sqo_m, sqo_h), k and v into the cache at
+ * slot slots[m] and, when slots2 is not NULL, also at slots2[m] -- the
+ * index_copy_ writes of adapters/base.py:184-236.  Positions outside
+ * [0, n_pos) give a zero q row and no k write; slots outside [0, L) are
+ * skipped. */
+int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                         const void* cos, const void* sin, int64_t scs, int64_t n_pos, const int64_t* pos,
+                         const int64_t* slots, const int64_t* slots2, void* k_cache, int64_t skh, int64_t skl,
+                         void* vt_cache, int64_t svh, int64_t svd, int64_t L, void* q_out, int64_t sqo_m,
+                         int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t head_dim, int dtype,
+                         void* stream);
+
+/* simsd_block_attention: out[m, hq] = softmax(scale * q[m, hq] . K[h]^T over
+ * the visible slots) . V[h] with h = hq / (Hq / Hkv) -- the SDPA call of
+ * adapters/base.py:245-262 with its bool mask (mask [M, >= L_valid] uint8,
+ * row stride smask, nonzero = visible; NULL = all visible; 4-byte aligned
+ * rows of at least L_valid rounded up to 4 bytes).  Slots
+ * [0, L_valid) are considered, L_valid <= L_cap (the cache's slot count, a
+ * multiple of 4); fp32 softmax, output rounded to the dtype; rows with no
+ * visible slot give 0.  q [M, Hq, D] and out [M, Hq, D] with (row, head)
+ * strides.  Workspace: simsd_block_attention_workspace_bytes(M, Hq, Hkv,
+ * L_valid), 16-byte aligned.  Deterministic. */
+int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid);
+
+int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, int64_t skh, int64_t skl,
+                          const void* vt_cache, int64_t svh, int64_t svd, int64_t L_cap, const uint8_t* mask,
+                          int64_t smask, void* out, int64_t so_m, int64_t so_h, int64_t M, int64_t Hq, int64_t Hkv,
+                          int64_t L_valid, int64_t head_dim, float scale, int dtype, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,621 @@
+// Attention of a few query rows over a static KV cache, for the speculative
+// step's draft blocks and multi-block verify (gfx950).
+//
+// Replaces, per attention layer, the reference's static-cache forward
+// (speculative_decoding/adapters/base.py:161-265 with SDAR's qkv,
+// sdar/modeling_sdar.py:250-262):
+//   q = q_norm(q_proj(x)); k = k_norm(k_proj(x)); v = v_proj(x)
+//   q, k = apply_rotary_pos_emb(q, k, cos, sin)
+//   key_cache.index_copy_(2, slots, k) ... (per GQA replica)      -> qkv_rope_cache_kernel
+//   out = F.scaled_dot_product_attention(q, K, V, attn_mask=bool)  -> attn_partial + attn_combine
+//
+// Cache layout, per layer (one sequence): K [Hkv, L, D] and V stored
+// transposed, Vt [Hkv, D, L].  The KV heads are not replicated per query head
+// (the reference's "expand" mode copies each of them n_rep times); every query
+// head reads its group's KV head, so the cache and its traffic are n_rep times
+// smaller.  Vt puts the slot index innermost, which is the contraction index of
+// P.V, so both attention products take their MFMA operands with contiguous
+// loads:
+//   S^T = K . Q^T   A = K tile (16 keys x 32 dims), B = Q^T (32 dims x 16 rows)
+//   O^T = Vt . P^T  A = Vt tile (16 dims x 32 keys), B = P^T (32 keys x 16 rows)
+// and P^T never leaves registers: the S^T result lane (g, r) holds keys
+// 4g..4g+3 of each 16-key tile for row r, which, with the MFMA's k-slots
+// assigned as {tile 0: 4g..4g+3, tile 1: 4g..4g+3}, is exactly that lane's B
+// operand of the second product (A and B only need to agree on the k order).
+// Query rows are the (query head, token) pairs of one KV head's group,
+// row = i * M + m for query head h * n_rep + i, padded to 16-row blocks.
+//
+// The key range is split into chunks, one workgroup per (chunk, KV head); each
+// keeps an online softmax (running max and sum per row) and writes its
+// unnormalised partial output; attn_combine merges the chunks in chunk order
+// (fixed order: bit-reproducible).
+#include <type_traits>
+
+#include "simsd_common.hpp"
+#include "simsd_kernels.h"
+
+namespace simsd {
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kDSteps = kHeadDim / 32;      // MFMA k-steps over the head dim
+constexpr int kDTiles = kHeadDim / 16;      // 16-dim tiles of the output
+constexpr int kKeyStep = 32;                // keys per inner step (two 16-key tiles)
+
+// ---------------------------------------------------------- lane exchanges
+// Combine over the four 16-lane groups (lane bits 4 and 5): the gfx950 swaps
+// applied to (v, v) hand every lane the values of its row pair and then of
+// its half-wave pair, combined lower-first, so all lanes end equal.
+template <typename Combine>
+SIMSD_DEV float across_groups(float v, Combine combine) {
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = combine(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return combine(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
+template <int DT> SIMSD_DEV uint32_t pack2(float lo, float hi);
+template <> SIMSD_DEV uint32_t pack2<kBF16>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+template <> SIMSD_DEV uint32_t pack2<kF16>(float lo, float hi) {
+  return f32_to_h16<kF16>(lo) | (f32_to_h16<kF16>(hi) << 16);
+}
+
+// ------------------------------------------------ q/k norm, RoPE, cache write
+struct QkvArgs {
+  const char* qkv;            // [M, (Hq + 2 Hkv) * D]: q heads, then k heads, then v heads
+  int64_t sqkv;               // row stride (elements)
+  const char* qn;             // q_norm weight [D] or null
+  const char* kn;             // k_norm weight [D] or null
+  float eps;
+  const char* cos;            // [n_pos, D] rows (stride scs)
+  const char* sin;
+  int64_t scs, n_pos;
+  const int64_t* pos;         // [M]
+  const int64_t* slots;       // [M] cache slots written
+  const int64_t* slots2;      // [M] second slots (permanent copies) or null
+  char* kc;                   // K [Hkv, L, D]
+  int64_t skh, skl;
+  char* vt;                   // Vt [Hkv, D, L]
+  int64_t svh, svd;
+  int64_t L;
+  char* qo;                   // [M, Hq, D]
+  int64_t sqo_m, sqo_h;
+  int Hq, Hkv;
+};
+
+// grid (M, head groups of 8): one wave per (token, head); lane l owns dims l
+// and l + 64, the two halves rotate_half pairs.  All of a wave's loads are
+// issued before its arithmetic.  Rounding points of the bf16 reference: the
+// norm is the stock RMSNorm (weight * dtype(x * r), r in fp32), then
+// q_embed = dtype(dtype(q * cos) + dtype(rotate_half(q) * sin)).
+template <int DT>
+__global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const int lane = threadIdx.x & 63;
+  const int hh = (int)blockIdx.y * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
+  if (hh >= a.Hq + 2 * a.Hkv) return;
+  const int64_t m = blockIdx.x;
+  const int64_t p = a.pos[m];
+  const int64_t s1 = a.slots[m];
+  const int64_t s2 = a.slots2 != nullptr ? a.slots2[m] : -1;
+  const bool pos_ok = p >= 0 && p < a.n_pos;
+  const bool s1_ok = s1 >= 0 && s1 < a.L;
+  const bool s2_ok = s2 >= 0 && s2 < a.L;
+  const int d0 = lane, d1 = lane + 64;
+  const char* src = a.qkv + (m * a.sqkv + (int64_t)hh * kHeadDim) * ES;
+  const bool is_v = hh >= a.Hq + a.Hkv;
+  const bool is_q = hh < a.Hq;
+  const char* nwt = is_q ? a.qn : a.kn;
+  float x0 = load_elem<DT>(src, d0), x1 = load_elem<DT>(src, d1);
+  float w0 = 1.f, w1 = 1.f, c0 = 0.f, c1 = 0.f, n0 = 0.f, n1 = 0.f;
+  if (!is_v) {
+    if (nwt != nullptr) {
+      w0 = load_elem<DT>(nwt, d0);
+      w1 = load_elem<DT>(nwt, d1);
+    }
+    if (pos_ok) {
+      const char* cr = a.cos + p * a.scs * ES;
+      const char* sr = a.sin + p * a.scs * ES;
+      c0 = load_elem<DT>(cr, d0); c1 = load_elem<DT>(cr, d1);
+      n0 = load_elem<DT>(sr, d0); n1 = load_elem<DT>(sr, d1);
+    }
+  }
+  if (is_v) {   // v head: copy into the transposed cache
+    char* base = a.vt + (int64_t)(hh - a.Hq - a.Hkv) * a.svh * ES;
+    if (s1_ok) {
+      store_elem<DT>(base, d0 * a.svd + s1, x0);
+      store_elem<DT>(base, d1 * a.svd + s1, x1);
+    }
+    if (s2_ok) {
+      store_elem<DT>(base, d0 * a.svd + s2, x0);
+      store_elem<DT>(base, d1 * a.svd + s2, x1);
+    }
+    return;
+  }
+  if (nwt != nullptr) {
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float r = 1.f / sqrtf(ss / (float)kHeadDim + a.eps);
+    x0 = round_to<DT>(w0 * round_to<DT>(x0 * r));
+    x1 = round_to<DT>(w1 * round_to<DT>(x1 * r));
+  }
+  float y0 = 0.f, y1 = 0.f;
+  if (pos_ok) {
+    y0 = round_to<DT>(round_to<DT>(x0 * c0) + round_to<DT>(-x1 * n0));
+    y1 = round_to<DT>(round_to<DT>(x1 * c1) + round_to<DT>(x0 * n1));
+  }
+  if (is_q) {
+    char* dst = a.qo + (m * a.sqo_m + (int64_t)hh * a.sqo_h) * ES;
+    store_elem<DT>(dst, d0, y0);
+    store_elem<DT>(dst, d1, y1);
+  } else if (pos_ok) {
+    char* base = a.kc + (int64_t)(hh - a.Hq) * a.skh * ES;
+    if (s1_ok) {
+      store_elem<DT>(base, s1 * a.skl + d0, y0);
+      store_elem<DT>(base, s1 * a.skl + d1, y1);
+    }
+    if (s2_ok) {
+      store_elem<DT>(base, s2 * a.skl + d0, y0);
+      store_elem<DT>(base, s2 * a.skl + d1, y1);
+    }
+  }
+}
+
+// ------------------------------------------------------------ attention
+struct AttnArgs {
+  const char* q;              // [M, Hq, D]
+  int64_t sq_m, sq_h;
+  const char* kc;             // K [Hkv, L_cap, D]
+  int64_t skh, skl;
+  const char* vt;             // Vt [Hkv, D, L_cap]
+  int64_t svh, svd;
+  const uint8_t* mask;        // [M, >= L_valid] (nonzero = visible) or null
+  int64_t smask;
+  int64_t M;
+  int n_rep, Hkv;
+  int64_t L_valid, chunk, wave_chunk;
+  int n_chunks;
+  float scale;
+  int rows, rows_pad;         // n_rep * M, padded to 16
+  float* o_part;              // [Hkv][n_chunks][rows_pad][D]
+  float2* ml_part;            // [Hkv][n_chunks][rows_pad]
+};
+
+// Loads are unconditional -- the caller points an unused lane at a valid
+// address -- and unused values are replaced afterwards: a load under a branch
+// would make the compiler wait for it at the join, serialising the batch.
+SIMSD_DEV u32x4_t load16_sel(const char* p, bool ok) {
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+  return ok ? v : zero4();
+}
+
+// Four keys of one Vt row (8 bytes) from key (a multiple of 4); keys at or
+// past `end` read as zero.  last4 = (end - 1) & ~3, a valid group start.
+template <int DT>
+SIMSD_DEV u32x2_t load_vt4(const char* rowp, int64_t key, int64_t end, int64_t last4) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const int64_t kk = key < last4 ? key : last4;
+  u32x2_t v = *reinterpret_cast<const u32x2_t*>(rowp + kk * ES);
+  const int64_t n = end - key;   // valid keys in this group (may be <= 0)
+  v.x = n >= 2 ? v.x : (n >= 1 ? (v.x & 0xffffu) : 0u);
+  v.y = n >= 4 ? v.y : (n >= 3 ? (v.y & 0xffffu) : 0u);
+  return v;
+}
+
+// Operands of one 32-key step: K tiles (A of S^T = K.Q^T), Vt tiles (A of
+// O^T = Vt.P^T) and, per row block, the 2 x 4 mask bytes of the lane's keys.
+template <int RBW>
+struct StepBuf {
+  u32x4_t kf[2][kDSteps];
+  u32x4_t vf[kDTiles];
+  uint32_t mk[RBW][2];
+};
+
+// Issue every load of the 32-key step at c.  Keys at or past c_end read a
+// valid slot and are zeroed / masked afterwards; a mask row holds at least
+// L_valid rounded up to 4 bytes, so 4-byte groups below c_end stay inside it.
+template <int DT, int RBW>
+SIMSD_DEV void attn_load(const AttnArgs& a, const char* kbase, const char* vbase, const uint8_t* const (&mrow)[RBW],
+                         int64_t c, int64_t c_end, int g, int r, StepBuf<RBW>& b) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const int64_t last4 = (c_end - 1) & ~(int64_t)3;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int64_t key = c + 16 * t + r;
+    const char* kp = kbase + (key < c_end ? key : c_end - 1) * a.skl * ES;
+#pragma unroll
+    for (int ds = 0; ds < kDSteps; ++ds) b.kf[t][ds] = load16_sel(kp + (ds * 32 + 8 * g) * ES, key < c_end);
+  }
+  // dim dt*16 + r, keys c + 4g .. +4 (k-slots 0..3) and c + 16 + 4g .. +4 (4..7)
+#pragma unroll
+  for (int dt = 0; dt < kDTiles; ++dt) {
+    const char* vp = vbase + (int64_t)(dt * 16 + r) * a.svd * ES;
+    const u32x2_t lo = load_vt4<DT>(vp, c + 4 * g, c_end, last4);
+    const u32x2_t hi = load_vt4<DT>(vp, c + 16 + 4 * g, c_end, last4);
+    b.vf[dt] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+  }
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t k4 = c + 16 * t + 4 * g;
+      b.mk[rb][t] = a.mask != nullptr ? *reinterpret_cast<const uint32_t*>(mrow[rb] + (k4 < last4 ? k4 : last4))
+                                      : 0x01010101u;
+    }
+}
+
+// One 32-key step of the online softmax for RBW row blocks: S^T = K.Q^T,
+// mask and scale, running max / sum per row, O^T += Vt.P^T.
+template <int DT, int RBW>
+SIMSD_DEV void attn_step(const AttnArgs& a, const u32x4_t (&qf)[RBW][kDSteps], const bool (&row_ok)[RBW],
+                         const StepBuf<RBW>& b, int64_t c, int64_t c_end, int g, float (&m_run)[RBW],
+                         float (&l_run)[RBW], f32x4_t (&acc)[RBW][kDTiles]) {
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    f32x4_t s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < kDSteps; ++ds) s[t] = Mfma<DT>::step(b.kf[t][ds], qf[rb][ds], s[t]);
+    }
+    // lane (g, r): s[t][j] = S^T[key c + 16t + 4g + j][row rb*16 + r]
+    float sv[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t key = c + 16 * t + 4 * g + j;
+        const bool vis = row_ok[rb] && key < c_end && ((b.mk[rb][t] >> (8 * j)) & 0xffu) != 0;
+        sv[t][j] = vis ? s[t][j] * a.scale : -INFINITY;
+        mx = fmaxf(mx, sv[t][j]);
+      }
+    mx = across_groups(mx, [](float x, float y) { return fmaxf(x, y); });
+    const float m_new = fmaxf(m_run[rb], mx);
+    const float alpha = m_new == -INFINITY ? 1.f : expf(m_run[rb] - m_new);
+    float p[2][4];
+    float ps = 0.f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        p[t][j] = sv[t][j] == -INFINITY ? 0.f : expf(sv[t][j] - m_new);
+        ps += p[t][j];
+      }
+    ps = across_groups(ps, [](float x, float y) { return x + y; });
+    l_run[rb] = l_run[rb] * alpha + ps;
+    m_run[rb] = m_new;
+    const u32x4_t pf = u32x4_t{pack2<DT>(p[0][0], p[0][1]), pack2<DT>(p[0][2], p[0][3]),
+                               pack2<DT>(p[1][0], p[1][1]), pack2<DT>(p[1][2], p[1][3])};
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      acc[rb][dt] *= alpha;
+      acc[rb][dt] = Mfma<DT>::step(b.vf[dt], pf, acc[rb][dt]);
+    }
+  }
+}
+
+// grid (n_chunks, Hkv, row groups), 4 waves (KSPLIT) or W waves.
+//   KSPLIT: every wave holds all RBW row blocks and a quarter of the
+//     workgroup's key chunk; the four online-softmax states merge through LDS.
+//   otherwise: the waves share the key chunk and own row blocks
+//     [(z*W + w)*RBW, (z*W + w + 1)*RBW) of row group z.
+// Each wave runs its 32-key steps with the next step's K/Vt loads in flight.
+template <int DT, int RBW, bool KSPLIT>
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int chunk_id = blockIdx.x;
+  const int h = blockIdx.y;
+  const int rb0 = KSPLIT ? 0 : ((int)blockIdx.z * nw + wv) * RBW;
+  if (!KSPLIT && rb0 * 16 >= a.rows) return;   // no rows for this wave (whole wave exits)
+
+  // Q^T fragments (B operand): row = rb*16 + r, dims ds*32 + 8g .. +8
+  u32x4_t qf[RBW][kDSteps];
+  int tok[RBW];
+  bool row_ok[RBW];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    const int row = (rb0 + rb) * 16 + r;
+    row_ok[rb] = row < a.rows;
+    const int i = row_ok[rb] ? row / (int)a.M : 0;
+    tok[rb] = row_ok[rb] ? row % (int)a.M : 0;
+    const int hq = h * a.n_rep + i;
+    const char* qp = a.q + ((int64_t)tok[rb] * a.sq_m + (int64_t)hq * a.sq_h) * ES;
+#pragma unroll
+    for (int ds = 0; ds < kDSteps; ++ds) qf[rb][ds] = load16_sel(qp + (ds * 32 + 8 * g) * ES, row_ok[rb]);
+  }
+
+  float m_run[RBW], l_run[RBW];
+  f32x4_t acc[RBW][kDTiles];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int64_t chunk_lo = (int64_t)chunk_id * a.chunk;
+  const int64_t chunk_hi = min(a.L_valid, chunk_lo + a.chunk);
+  const int64_t c_begin = KSPLIT ? min(chunk_hi, chunk_lo + (int64_t)wv * a.wave_chunk) : chunk_lo;
+  const int64_t c_end = KSPLIT ? min(chunk_hi, c_begin + a.wave_chunk) : chunk_hi;
+  const char* kbase = a.kc + (int64_t)h * a.skh * ES;
+  const char* vbase = a.vt + (int64_t)h * a.svh * ES;
+
+  const uint8_t* mrow[RBW];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) mrow[rb] = a.mask != nullptr ? a.mask + (int64_t)tok[rb] * a.smask : nullptr;
+  // the next step's loads are issued unconditionally (past c_end they read a
+  // valid slot and are zeroed), so no load sits under a branch
+  StepBuf<RBW> bA, bB;
+  if (c_begin < c_end) {
+    attn_load<DT, RBW>(a, kbase, vbase, mrow, c_begin, c_end, g, r, bA);
+    for (int64_t c = c_begin;; c += 2 * kKeyStep) {
+      attn_load<DT, RBW>(a, kbase, vbase, mrow, c + kKeyStep, c_end, g, r, bB);
+      attn_step<DT, RBW>(a, qf, row_ok, bA, c, c_end, g, m_run, l_run, acc);
+      if (c + kKeyStep >= c_end) break;
+      attn_load<DT, RBW>(a, kbase, vbase, mrow, c + 2 * kKeyStep, c_end, g, r, bA);
+      attn_step<DT, RBW>(a, qf, row_ok, bB, c + kKeyStep, c_end, g, m_run, l_run, acc);
+      if (c + 2 * kKeyStep >= c_end) break;
+    }
+  }
+
+  const int64_t base_row = ((int64_t)h * a.n_chunks + chunk_id) * a.rows_pad;
+  if constexpr (KSPLIT) {
+    // merge the four waves' states in wave order: LDS o[w][row][d], ml[w][row]
+    __shared__ __attribute__((aligned(16))) float o_sh[4][RBW * 16][kHeadDim];
+    __shared__ float2 ml_sh[4][RBW * 16];
+#pragma unroll
+    for (int rb = 0; rb < RBW; ++rb) {
+      const int row = rb * 16 + r;
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt)
+        *reinterpret_cast<f32x4_t*>(&o_sh[wv][row][dt * 16 + 4 * g]) = acc[rb][dt];
+      if (g == 0) ml_sh[wv][row] = make_float2(m_run[rb], l_run[rb]);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < RBW * 16 * kHeadDim; e += blockDim.x) {
+      const int row = e / kHeadDim, d = e % kHeadDim;
+      if (row >= a.rows) continue;
+      float mx = -INFINITY;
+      for (int w = 0; w < nw; ++w) mx = fmaxf(mx, ml_sh[w][row].x);
+      float o = 0.f, l = 0.f;
+      for (int w = 0; w < nw; ++w) {
+        const float2 ml = ml_sh[w][row];
+        const float wt = ml.x == -INFINITY ? 0.f : expf(ml.x - mx);
+        o += o_sh[w][row][d] * wt;
+        l += ml.y * wt;
+      }
+      a.o_part[(base_row + row) * kHeadDim + d] = o;
+      if (d == 0) a.ml_part[base_row + row] = make_float2(mx, l);
+    }
+  } else {
+    // lane (g, r): acc[rb][dt][j] = O^T[dim dt*16 + 4g + j][row rb*16 + r]
+#pragma unroll
+    for (int rb = 0; rb < RBW; ++rb) {
+      const int row = (rb0 + rb) * 16 + r;
+      if (!row_ok[rb]) continue;
+      float* op = a.o_part + (base_row + row) * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt)
+        *reinterpret_cast<f32x4_t*>(op + dt * 16 + 4 * g) = acc[rb][dt];
+      if (g == 0) a.ml_part[base_row + row] = make_float2(m_run[rb], l_run[rb]);
+    }
+  }
+}
+
+constexpr int kMaxChunks = 1024;
+
+// One workgroup per (token, query head), one thread per dim: merge the chunk
+// partials in chunk order, normalise, round.  Rows with no visible key give 0.
+// The chunk weights are formed once in LDS; the partial rows are read kBatch
+// chunks at a time.
+template <int DT>
+__global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __restrict__ o_part,
+                                                               const float2* __restrict__ ml_part, int n_chunks,
+                                                               int rows_pad, int64_t M, int Hq, int n_rep,
+                                                               char* __restrict__ out, int64_t so_m, int64_t so_h) {
+  constexpr int kBatch = 8;
+  __shared__ float w_sh[kMaxChunks];
+  __shared__ float red[kHeadDim / 64][2];
+  const int64_t m = blockIdx.x / Hq;
+  const int hq = blockIdx.x % Hq;
+  const int h = hq / n_rep, i = hq % n_rep;
+  const int64_t row = (int64_t)i * M + m;
+  const int d = threadIdx.x;
+  const int lane = d & 63, wv = d >> 6;
+  const int64_t base = (int64_t)h * n_chunks * rows_pad;
+  // running maxima of the chunks: per thread over its chunks, then the block
+  float mx = -INFINITY;
+  for (int c = d; c < n_chunks; c += kHeadDim) {
+    const float2 ml = ml_part[base + (int64_t)c * rows_pad + row];
+    w_sh[c] = ml.x;
+    mx = fmaxf(mx, ml.x);
+  }
+  mx = wave_max(mx);
+  if (lane == 0) red[wv][0] = mx;
+  __syncthreads();
+  mx = fmaxf(red[0][0], red[1][0]);
+  // weights exp(m_c - max) and the denominator (each thread its chunks, then
+  // the block in thread order)
+  float l = 0.f;
+  for (int c = d; c < n_chunks; c += kHeadDim) {
+    const float mc = w_sh[c];
+    const float wt = (mx == -INFINITY || mc == -INFINITY) ? 0.f : expf(mc - mx);
+    w_sh[c] = wt;
+    l += ml_part[base + (int64_t)c * rows_pad + row].y * wt;
+  }
+  l = wave_sum(l);
+  if (lane == 0) red[wv][1] = l;
+  __syncthreads();
+  l = red[0][1] + red[1][1];
+  float o = 0.f;
+  for (int c0 = 0; c0 < n_chunks; c0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      v[u] = o_part[(base + (int64_t)min(c0 + u, n_chunks - 1) * rows_pad + row) * kHeadDim + d];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (c0 + u < n_chunks) o += v[u] * w_sh[c0 + u];
+  }
+  store_elem<DT>(out, m * so_m + (int64_t)hq * so_h + d, l > 0.f ? o / l : 0.f);
+}
+
+struct AttnPlan {
+  int rows, rows_pad, rb, rbw, waves, groups, n_chunks;
+  bool ksplit;
+  int64_t chunk, wave_chunk;
+  int64_t o_bytes, ml_bytes, bytes;
+};
+
+inline int64_t up256(int64_t n) { return (n + 255) / 256 * 256; }
+inline int64_t up32(int64_t n) { return (n + 31) / 32 * 32; }
+
+// Up to 32 query rows per KV head (two row blocks): four waves split each
+// workgroup's key chunk, about 256 waves in all, at least one 32-key step per
+// wave.  More rows: the row blocks spread over up to 4 waves (2 blocks per wave
+// above 4 blocks) and row groups of 8 blocks, sharing 64-key or longer chunks.
+AttnPlan attn_plan(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
+  AttnPlan p{};
+  const int n_rep = (int)(Hq / Hkv);
+  p.rows = (int)(n_rep * M);
+  p.rb = (p.rows + 15) / 16;
+  p.rows_pad = p.rb * 16;
+  const int64_t L = L_valid > 0 ? L_valid : 1;
+  p.ksplit = p.rb <= 2;
+  if (p.ksplit) {
+    p.rbw = p.rb;
+    p.waves = 4;
+    p.groups = 1;
+    int64_t wc = up32((Hkv * L + 255) / 256);            // keys per wave for ~256 waves
+    if (wc < 32) wc = 32;
+    while ((L + 4 * wc - 1) / (4 * wc) > kMaxChunks) wc *= 2;
+    p.wave_chunk = wc;
+    p.chunk = 4 * wc;
+  } else {
+    p.rbw = p.rb > 4 ? 2 : 1;
+    p.waves = (p.rb + p.rbw - 1) / p.rbw;
+    if (p.waves > 4) p.waves = 4;
+    p.groups = (p.rb + p.waves * p.rbw - 1) / (p.waves * p.rbw);
+    int64_t want = (256 + Hkv - 1) / Hkv;                  // chunks per head
+    int64_t chunk = (L + want - 1) / want;
+    chunk = (chunk + 63) / 64 * 64;
+    if (chunk < 64) chunk = 64;
+    while ((L + chunk - 1) / chunk > kMaxChunks) chunk *= 2;
+    p.chunk = chunk;
+    p.wave_chunk = chunk;
+  }
+  p.n_chunks = (int)((L + p.chunk - 1) / p.chunk);
+  p.o_bytes = up256(Hkv * (int64_t)p.n_chunks * p.rows_pad * kHeadDim * 4);
+  p.ml_bytes = up256(Hkv * (int64_t)p.n_chunks * p.rows_pad * 8);
+  p.bytes = p.o_bytes + p.ml_bytes;
+  return p;
+}
+
+inline bool al(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+}  // namespace
+}  // namespace simsd
+
+using namespace simsd;
+
+extern "C" int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, const void* k_norm_w,
+                                    float eps, const void* cos, const void* sin, int64_t scs, int64_t n_pos,
+                                    const int64_t* pos, const int64_t* slots, const int64_t* slots2, void* k_cache,
+                                    int64_t skh, int64_t skl, void* vt_cache, int64_t svh, int64_t svd, int64_t L,
+                                    void* q_out, int64_t sqo_m, int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv,
+                                    int64_t head_dim, int dtype, void* stream) {
+  if (dtype != kBF16 && dtype != kF16) return set_error("qkv_rope_cache: dtype must be bf16 or fp16");
+  if (head_dim != kHeadDim) return set_error("qkv_rope_cache: head_dim must be %d (got %lld)", kHeadDim, (long long)head_dim);
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L <= 0 || n_pos <= 0)
+    return set_error("qkv_rope_cache: bad sizes");
+  if (skl < kHeadDim || svd < L || skh < L * skl || svh < kHeadDim * svd)
+    return set_error("qkv_rope_cache: cache strides do not hold [Hkv, L, D] / [Hkv, D, L]");
+  if (M == 0) return 0;
+  if (M > 0x7fffffff) return set_error("qkv_rope_cache: too many tokens");
+  if (!qkv || !cos || !sin || !pos || !slots || !k_cache || !vt_cache || !q_out)
+    return set_error("qkv_rope_cache: null pointer");
+  QkvArgs a{};
+  a.qkv = static_cast<const char*>(qkv); a.sqkv = sqkv;
+  a.qn = static_cast<const char*>(q_norm_w); a.kn = static_cast<const char*>(k_norm_w); a.eps = eps;
+  a.cos = static_cast<const char*>(cos); a.sin = static_cast<const char*>(sin); a.scs = scs; a.n_pos = n_pos;
+  a.pos = pos; a.slots = slots; a.slots2 = slots2;
+  a.kc = static_cast<char*>(k_cache); a.skh = skh; a.skl = skl;
+  a.vt = static_cast<char*>(vt_cache); a.svh = svh; a.svd = svd; a.L = L;
+  a.qo = static_cast<char*>(q_out); a.sqo_m = sqo_m; a.sqo_h = sqo_h;
+  a.Hq = (int)Hq; a.Hkv = (int)Hkv;
+  const int heads = (int)(Hq + 2 * Hkv);
+  const int waves = heads < 8 ? heads : 8;
+  const dim3 grid((unsigned)M, (unsigned)((heads + waves - 1) / waves));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == kBF16) hipLaunchKernelGGL(qkv_rope_cache_kernel<kBF16>, grid, dim3(64 * waves), 0, st, a);
+  else hipLaunchKernelGGL(qkv_rope_cache_kernel<kF16>, grid, dim3(64 * waves), 0, st, a);
+  return check_launch("qkv_rope_cache");
+}
+
+extern "C" int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L_valid < 0) return -1;
+  return attn_plan(M, Hq, Hkv, L_valid).bytes;
+}
+
+extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, int64_t skh,
+                                     int64_t skl, const void* vt_cache, int64_t svh, int64_t svd, int64_t L_cap,
+                                     const uint8_t* mask, int64_t smask, void* out, int64_t so_m, int64_t so_h,
+                                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid, int64_t head_dim,
+                                     float scale, int dtype, void* workspace, int64_t workspace_bytes,
+                                     void* stream) {
+  if (dtype != kBF16 && dtype != kF16) return set_error("block_attention: dtype must be bf16 or fp16");
+  if (head_dim != kHeadDim) return set_error("block_attention: head_dim must be %d (got %lld)", kHeadDim, (long long)head_dim);
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L_valid < 0 || L_valid > L_cap)
+    return set_error("block_attention: bad sizes (M=%lld Hq=%lld Hkv=%lld L_valid=%lld L_cap=%lld)", (long long)M,
+                     (long long)Hq, (long long)Hkv, (long long)L_valid, (long long)L_cap);
+  if (M == 0) return 0;
+  if (L_cap % 4 != 0) return set_error("block_attention: the cache slot count must be a multiple of 4");
+  if (!q || !k_cache || !vt_cache || !out) return set_error("block_attention: null pointer");
+  const AttnPlan pl = attn_plan(M, Hq, Hkv, L_valid);
+  if (pl.rows > 65536) return set_error("block_attention: %d query rows per KV head exceed 65536", pl.rows);
+  // 16-byte loads of q and K rows, 8-byte loads of Vt rows
+  if (!al(q, 16) || (sq_m % 8) || (sq_h % 8) || !al(k_cache, 16) || (skh % 8) || (skl % 8) || !al(vt_cache, 8) ||
+      (svh % 4) || (svd % 4) || svd < L_cap || skl < kHeadDim)
+    return set_error("block_attention: q/K need 16-byte aligned rows and Vt 8-byte aligned rows of >= L_cap slots");
+  if (mask != nullptr && (!al(mask, 4) || smask % 4 != 0 || smask < (L_valid + 3) / 4 * 4))
+    return set_error("block_attention: mask rows must be 4-byte aligned with at least L_valid rounded up to 4 bytes");
+  if (workspace == nullptr || workspace_bytes < pl.bytes || !al(workspace, 16))
+    return set_error("block_attention: needs a 16-byte aligned workspace of %lld bytes (got %lld)", (long long)pl.bytes,
+                     (long long)workspace_bytes);
+  AttnArgs a{};
+  a.q = static_cast<const char*>(q); a.sq_m = sq_m; a.sq_h = sq_h;
+  a.kc = static_cast<const char*>(k_cache); a.skh = skh; a.skl = skl;
+  a.vt = static_cast<const char*>(vt_cache); a.svh = svh; a.svd = svd;
+  a.mask = mask; a.smask = smask;
+  a.M = M; a.n_rep = (int)(Hq / Hkv); a.Hkv = (int)Hkv;
+  a.L_valid = L_valid; a.chunk = pl.chunk; a.wave_chunk = pl.wave_chunk; a.n_chunks = pl.n_chunks;
+  a.scale = scale;
+  a.rows = pl.rows; a.rows_pad = pl.rows_pad;
+  a.o_part = static_cast<float*>(workspace);
+  a.ml_part = reinterpret_cast<float2*>(static_cast<char*>(workspace) + pl.o_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)pl.n_chunks, (unsigned)Hkv, (unsigned)pl.groups), block(64 * pl.waves);
+  auto partial = [&](auto dt_tag) {
+    constexpr int DT = decltype(dt_tag)::value;
+    if (pl.ksplit) {
+      if (pl.rbw == 2) hipLaunchKernelGGL((attn_partial_kernel<DT, 2, true>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((attn_partial_kernel<DT, 1, true>), grid, block, 0, st, a);
+    } else {
+      if (pl.rbw == 2) hipLaunchKernelGGL((attn_partial_kernel<DT, 2, false>), grid, block, 0, st, a);
+      else hipLaunchKernelGGL((attn_partial_kernel<DT, 1, false>), grid, block, 0, st, a);
+    }
+    hipLaunchKernelGGL(attn_combine_kernel<DT>, dim3((unsigned)(M * Hq)), dim3(kHeadDim), 0, st, a.o_part,
+                       a.ml_part, pl.n_chunks, pl.rows_pad, M, (int)Hq, a.n_rep, static_cast<char*>(out), so_m, so_h);
+  };
+  if (dtype == kBF16) partial(std::integral_constant<int, kBF16>{});
+  else partial(std::integral_constant<int, kF16>{});
+  return check_launch("block_attention");
+}

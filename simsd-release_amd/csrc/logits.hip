@@ -31,6 +31,7 @@ constexpr int kRowThreads = 256;
 constexpr int64_t kNoIndex = INT64_MAX;
 constexpr int kFinalizeWaves = 16;
 constexpr int kMaxSelectRows = 64;    // the unmasking choice runs in one wave
+constexpr int kBatch = 8;             // logits a thread loads at once
 
 // Softmax state of a set of logits: the largest value, the sum of exp(l - mx)
 // over the set, and the lowest index holding the largest value.
@@ -97,7 +98,20 @@ __global__ __launch_bounds__(kRowThreads) void row_partial_kernel(const char* __
   const int64_t e1 = min(V, e0 + chunk);
   const char* row = logits + m * slm * DTypeInfo<DT>::kSize;
   RowStat s = stat_empty();
-  for (int64_t e = e0 + threadIdx.x; e < e1; e += kRowThreads) stat_push(s, load_elem<DT>(row, e), e);
+  // kBatch loads issued together, then folded in index order
+  for (int64_t b = e0 + threadIdx.x; b < e1; b += kBatch * kRowThreads) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t e = b + (int64_t)u * kRowThreads;
+      v[u] = load_elem<DT>(row, e < e1 ? e : e1 - 1);   // unconditional (no wait at a branch join)
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t e = b + (int64_t)u * kRowThreads;
+      if (e < e1) stat_push(s, v[u], e);
+    }
+  }
   s = stat_wave(s);
   if ((threadIdx.x & 63) == 0) wres[threadIdx.x >> 6] = s;
   __syncthreads();
@@ -174,7 +188,19 @@ __global__ __launch_bounds__(kRowThreads) void row_probs_kernel(const char* __re
   const int64_t e1 = min(V, e0 + chunk);
   const char* row = logits + m * slm * DTypeInfo<DT>::kSize;
   float* out = probs + m * spm;
-  for (int64_t e = e0 + threadIdx.x; e < e1; e += kRowThreads) out[e] = expf(load_elem<DT>(row, e) - st.x) / st.y;
+  for (int64_t b = e0 + threadIdx.x; b < e1; b += kBatch * kRowThreads) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t e = b + (int64_t)u * kRowThreads;
+      v[u] = load_elem<DT>(row, e < e1 ? e : e1 - 1);   // unconditional (no wait at a branch join)
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t e = b + (int64_t)u * kRowThreads;
+      if (e < e1) out[e] = expf(v[u] - st.x) / st.y;
+    }
+  }
 }
 
 // Slices per row: about 2048 logits per workgroup, at most 1024 slices.

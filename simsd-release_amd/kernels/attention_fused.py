@@ -1,0 +1,188 @@
+"""Attention of the speculative step on MI355X: q/k norm, RoPE and the KV
+cache write in one launch, then attention of the block's few query rows over
+the static cache (two launches: chunked partials, then their merge).
+
+Reference path, per attention layer (speculative_decoding/adapters/base.py:
+161-265 with SDAR's qkv, sdar/modeling_sdar.py:250-262, and the cache class
+StaticBlockCache, speculative_decoding/cache_aware.py:195-298)::
+
+    q = q_norm(q_proj(x)); k = k_norm(k_proj(x)); v = v_proj(x)
+    q, k = apply_rotary_pos_emb(q, k, cos, sin)
+    for i in range(n_rep):                       # GQA "expand" cache
+        key_cache[:, i::n_rep].index_copy_(2, cur_scratch_pos, k)   # (+ values,
+        ...                                                         #  + cache_position)
+    out = F.scaled_dot_product_attention(q, key_cache, value_cache, attn_mask=mask_bool)
+
+Here: ``qkv_rope_cache`` (one launch) and ``block_attention`` (two).  The
+cache (``BlockKVCache``) keeps one copy of each KV head (no per-query-head
+replicas) and stores V transposed, [Hkv, D, L], so the P.V product reads
+contiguous slots; the slot space is the reference's: [0, max_cache_len) the
+permanent cache, [max_cache_len, full_len) the scratch of the current forward.
+``rope_tables`` computes cos/sin exactly as the rotary embedding does
+(modeling_sdar.py:418-435).  Head dim 128; bf16 or fp16.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+HEAD_DIM = 128
+
+
+def rope_tables(inv_freq: torch.Tensor, n_pos: int, dtype: torch.dtype, attention_scaling: float = 1.0):
+    """(cos, sin) [n_pos, D] in ``dtype`` for positions 0..n_pos-1, computed as
+    SDARRotaryEmbedding.forward does (fp32 outer product, duplicated halves,
+    cos/sin, scaled, cast)."""
+    pos = torch.arange(n_pos, device=inv_freq.device, dtype=torch.float32)
+    freqs = (inv_freq.float()[None, :, None] @ pos[None, None, :]).transpose(1, 2)[0]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return ((emb.cos() * attention_scaling).to(dtype).contiguous(),
+            (emb.sin() * attention_scaling).to(dtype).contiguous())
+
+
+def default_inv_freq(head_dim: int = HEAD_DIM, theta: float = 1000000.0, device=None) -> torch.Tensor:
+    """The default RoPE frequencies, 1 / theta^(2i / D)."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64, device=device).float() / head_dim))
+
+
+class BlockKVCache:
+    """Static per-layer K [Hkv, L, D] and Vt [Hkv, D, L] buffers (zeroed),
+    L = max_cache_len + max_cur_len rounded up to a multiple of 32.  Slots
+    [0, max_cache_len) hold the committed context, [max_cache_len, L) the
+    scratch of the current forward, as in the reference's StaticBlockCache."""
+
+    def __init__(self, n_layers: int, n_kv_heads: int, max_cache_len: int, max_cur_len: int,
+                 device, dtype=torch.bfloat16, head_dim: int = HEAD_DIM):
+        if head_dim != HEAD_DIM:
+            raise ValueError(f"head_dim must be {HEAD_DIM}")
+        self.n_layers, self.n_kv_heads, self.head_dim = n_layers, n_kv_heads, head_dim
+        self.max_cache_len, self.max_cur_len = max_cache_len, max_cur_len
+        self.full_len = (max_cache_len + max_cur_len + 31) // 32 * 32
+        self.dtype = dtype
+        self.key_cache = [torch.zeros(n_kv_heads, self.full_len, head_dim, device=device, dtype=dtype)
+                          for _ in range(n_layers)]
+        self.value_cache_t = [torch.zeros(n_kv_heads, head_dim, self.full_len, device=device, dtype=dtype)
+                              for _ in range(n_layers)]
+
+    def __len__(self) -> int:
+        return self.n_layers
+
+    def reset(self) -> None:
+        for t in self.key_cache + self.value_cache_t:
+            t.zero_()
+
+    def value_cache(self, layer: int) -> torch.Tensor:
+        """V of a layer in the reference's [Hkv, L, D] orientation (a view)."""
+        return self.value_cache_t[layer].transpose(1, 2)
+
+
+def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weight, eps: float,
+                   cos: torch.Tensor, sin: torch.Tensor, position_ids: torch.Tensor,
+                   slots: torch.Tensor, cache: BlockKVCache, layer: int,
+                   slots2: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k norm + RoPE of the merged projection output and the K/V cache write.
+
+    qkv:          [M, (Hq + 2 Hkv) * 128] (q heads, k heads, v heads)
+    position_ids: int64 [M] rows of cos/sin
+    slots:        int64 [M] cache slots (the scratch positions); ``slots2``:
+                  int64 [M] permanent positions written too (store_kv)
+    -> q [M, Hq, 128] after norm and RoPE.
+    """
+    code = _native.DTYPE_CODES.get(qkv.dtype)
+    if code is None or qkv.dtype == torch.float32:
+        raise TypeError(f"qkv_rope_cache: dtype must be bf16 or fp16, got {qkv.dtype}")
+    if qkv.ndim != 2:
+        raise ValueError("qkv_rope_cache: qkv must be [M, (Hq + 2 Hkv) * D]")
+    M = qkv.shape[0]
+    Hkv, D = cache.n_kv_heads, cache.head_dim
+    if qkv.shape[1] != (n_q_heads + 2 * Hkv) * D or n_q_heads % Hkv != 0:
+        raise ValueError(f"qkv_rope_cache: width {qkv.shape[1]} != ({n_q_heads} + 2*{Hkv}) * {D}")
+    if qkv.stride(1) != 1:
+        qkv = qkv.contiguous()
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != qkv.dtype or t.ndim != 2 or t.shape[1] != D or t.stride(1) != 1:
+            raise ValueError(f"qkv_rope_cache: {name} must be [n_pos, {D}] in {qkv.dtype}")
+    if cos.shape != sin.shape or cos.stride(0) != sin.stride(0):
+        raise ValueError("qkv_rope_cache: cos and sin differ in shape or stride")
+    for name, t in (("position_ids", position_ids), ("slots", slots), ("slots2", slots2)):
+        if t is not None and (t.dtype != torch.int64 or t.shape != (M,) or (M > 1 and t.stride(0) != 1)):
+            raise ValueError(f"qkv_rope_cache: {name} must be int64 [M] with unit stride")
+    for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if t is not None and (t.dtype != qkv.dtype or t.shape != (D,) or t.stride(0) != 1):
+            raise ValueError(f"qkv_rope_cache: {name} must be [{D}] in {qkv.dtype}")
+    kc, vt = cache.key_cache[layer], cache.value_cache_t[layer]
+    if kc.dtype != qkv.dtype:
+        raise TypeError("qkv_rope_cache: cache dtype differs from qkv")
+    dev = _native.require_device(qkv, cos, sin, position_ids, slots, slots2, kc, q_norm_weight, k_norm_weight)
+    q = torch.empty((M, n_q_heads, D), device=dev, dtype=qkv.dtype)
+    if M == 0:
+        return q
+    with _native.device_guard(dev):
+        status = _native.lib().simsd_qkv_rope_cache(
+            qkv.data_ptr(), qkv.stride(0),
+            q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+            k_norm_weight.data_ptr() if k_norm_weight is not None else None, float(eps),
+            cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], position_ids.data_ptr(),
+            slots.data_ptr(), slots2.data_ptr() if slots2 is not None else None,
+            kc.data_ptr(), kc.stride(0), kc.stride(1), vt.data_ptr(), vt.stride(0), vt.stride(1), cache.full_len,
+            q.data_ptr(), q.stride(0), q.stride(1), M, n_q_heads, Hkv, D, code, _native.stream_of(dev))
+    _native.check(status, "qkv_rope_cache")
+    return q
+
+
+def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torch.Tensor | None = None,
+                    valid_len: int | None = None, scale: float | None = None) -> torch.Tensor:
+    """softmax(scale * q K^T, masked) V over the cache's slots [0, valid_len).
+
+    q:    [M, Hq, 128] (query head hq reads KV head hq // (Hq / Hkv))
+    mask: bool/uint8 [M, >= valid_len], True = visible (the reference's SDPA
+          mask rows), or None (all visible)
+    -> [M, Hq * 128] (the layout o_proj takes).
+    """
+    code = _native.DTYPE_CODES.get(q.dtype)
+    if code is None or q.dtype == torch.float32:
+        raise TypeError(f"block_attention: dtype must be bf16 or fp16, got {q.dtype}")
+    if q.ndim != 3 or q.shape[2] != cache.head_dim:
+        raise ValueError("block_attention: q must be [M, Hq, 128]")
+    M, Hq, D = q.shape
+    Hkv = cache.n_kv_heads
+    if Hq % Hkv != 0:
+        raise ValueError(f"block_attention: {Hq} query heads not a multiple of {Hkv} KV heads")
+    L = cache.full_len if valid_len is None else int(valid_len)
+    if not 0 <= L <= cache.full_len:
+        raise ValueError(f"block_attention: valid_len {L} outside [0, {cache.full_len}]")
+    if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    m8 = None
+    if mask is not None:
+        if mask.ndim != 2 or mask.shape[0] != M or mask.shape[1] < L:
+            raise ValueError(f"block_attention: mask must be [{M}, >= {L}]")
+        m8 = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
+        if m8.dtype != torch.uint8:
+            raise TypeError("block_attention: mask must be bool or uint8")
+        need = (L + 3) // 4 * 4      # the kernel reads 4 mask bytes at a time
+        if m8.stride(1) != 1 or m8.stride(0) % 4 or m8.data_ptr() % 4 or m8.shape[1] < need:
+            pad = torch.zeros((M, max(need, (m8.shape[1] + 3) // 4 * 4)), device=m8.device, dtype=torch.uint8)
+            pad[:, :m8.shape[1]].copy_(m8)
+            m8 = pad
+    kc, vt = cache.key_cache[layer], cache.value_cache_t[layer]
+    dev = _native.require_device(q, kc, m8)
+    out = torch.empty((M, Hq, D), device=dev, dtype=q.dtype)
+    if M == 0:
+        return out.view(M, Hq * D)
+    lib = _native.lib()
+    need = lib.simsd_block_attention_workspace_bytes(M, Hq, Hkv, L)
+    if need < 0:
+        _native.check(-1, "block_attention")
+    ws = torch.empty(max(need, 256), device=dev, dtype=torch.uint8)
+    with _native.device_guard(dev):
+        status = lib.simsd_block_attention(
+            q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), kc.stride(0), kc.stride(1),
+            vt.data_ptr(), vt.stride(0), vt.stride(1), cache.full_len,
+            m8.data_ptr() if m8 is not None else None, m8.stride(0) if m8 is not None else 0,
+            out.data_ptr(), out.stride(0), out.stride(1), M, Hq, Hkv, L, D,
+            float(D ** -0.5 if scale is None else scale), code, ws.data_ptr(), ws.numel(),
+            _native.stream_of(dev))
+    _native.check(status, "block_attention")
+    return out.view(M, Hq * D)

@@ -1,0 +1,275 @@
+"""GPU parity of the attention path (MI355X): q/k norm + RoPE + KV-cache write
+(one launch) and the block attention over the static cache, against the
+oracle on the same inputs and against the reference's own torch sequence.
+
+qkv_rope_cache: q rows and every cache slot written equal the oracle within
+one bf16 unit in the last place (the RMSNorm statistic may round either way;
+more than 99% of values are bit-equal), and slots not addressed stay
+untouched.  block_attention: within 2^-7 max|ref| + 1e-3 of the fp64 oracle
+(the reference's bf16 bound) at the draft shape (4 rows, 16/8 heads) and the
+verify shape (32 rows, 32/8 heads), ragged valid lengths, every GQA ratio, 256
+query rows per KV head, masks with empty rows, fp16; bitwise deterministic;
+graph replays equal eager calls.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as oatt
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+D = 128
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+
+
+def rnd(*shape, dtype=torch.bfloat16, scale=1.0, seed=0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(*shape, generator=g, device=DEV, dtype=torch.float32) * scale).to(dtype)
+
+
+def bound(ref):
+    return 2 ** -7 * float(np.abs(ref).max()) + 1e-3
+
+
+def fill_cache(cache, layer, L, seed, dtype=torch.bfloat16):
+    k = rnd(cache.n_kv_heads, L, D, dtype=dtype, seed=seed)
+    v = rnd(cache.n_kv_heads, L, D, dtype=dtype, seed=seed + 1)
+    cache.key_cache[layer][:, :L].copy_(k)
+    cache.value_cache_t[layer][:, :, :L].copy_(v.transpose(1, 2))
+    return k, v
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,L_valid,L_total", [(4, 16, 8, 1000, 1004), (32, 32, 8, 1024, 1056),
+                                                      (8, 8, 8, 37, 64), (3, 12, 3, 301, 320),
+                                                      (64, 32, 8, 530, 600), (1, 16, 8, 1, 32)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_block_attention_vs_oracle(M, Hq, Hkv, L_valid, L_total, masked):
+    from kernels.attention_fused import BlockKVCache, block_attention
+    print(f"block_attention M={M} Hq={Hq} Hkv={Hkv} L={L_valid} masked={masked}", flush=True)
+    cache = BlockKVCache(1, Hkv, L_total - 32, 32, DEV)
+    k, v = fill_cache(cache, 0, L_valid, seed=M + L_valid)
+    q = rnd(M, Hq, D, seed=7)
+    mask = None
+    if masked:
+        g = torch.Generator(device=DEV).manual_seed(11)
+        mask = torch.rand(M, cache.full_len, generator=g, device=DEV) < 0.6
+        mask[:, 0] = True
+        if M > 2:
+            mask[2] = False                       # a row with nothing visible -> zeros
+    with torch.inference_mode():
+        out = block_attention(q, cache, 0, mask=mask, valid_len=L_valid)
+    torch.cuda.synchronize()
+    ref = oatt.attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                         None if mask is None else mask[:, :L_valid].cpu().numpy(), D ** -0.5)
+    got = out.view(M, Hq, D).float().cpu().numpy()
+    err = float(np.abs(got - ref).max())
+    assert err <= bound(ref), f"max err {err:.3e} > {bound(ref):.3e}"
+    if masked and M > 2:
+        assert np.all(got[2] == 0)
+
+
+def test_block_attention_fp16_and_determinism():
+    from kernels.attention_fused import BlockKVCache, block_attention
+    cache = BlockKVCache(2, 8, 992, 32, DEV, dtype=torch.float16)
+    k, v = fill_cache(cache, 1, 900, seed=3, dtype=torch.float16)
+    q = rnd(16, 32, D, dtype=torch.float16, seed=4)
+    with torch.inference_mode():
+        a = block_attention(q, cache, 1, valid_len=900)
+        b = block_attention(q, cache, 1, valid_len=900)
+    assert torch.equal(a, b)
+    ref = oatt.attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), None, D ** -0.5)
+    got = a.view(16, 32, D).float().cpu().numpy()
+    assert float(np.abs(got - ref).max()) <= bound(ref)
+
+
+def test_block_attention_matches_torch_sdpa_on_expanded_cache():
+    """The reference's SDPA on its GQA-expanded [H_q, L, D] cache with the bool
+    mask (adapters/base.py:245-262), computed in fp32 on the device."""
+    from kernels.attention_fused import BlockKVCache, block_attention
+    M, Hq, Hkv, L = 32, 32, 8, 700
+    cache = BlockKVCache(1, Hkv, 736, 32, DEV)
+    k, v = fill_cache(cache, 0, L, seed=21)
+    q = rnd(M, Hq, D, seed=22)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    mask = torch.rand(M, L, generator=g, device=DEV) < 0.8
+    mask[:, :8] = True
+    kk = k.float().repeat_interleave(Hq // Hkv, dim=0)[None]
+    vv = v.float().repeat_interleave(Hq // Hkv, dim=0)[None]
+    ref = F.scaled_dot_product_attention(q.float().transpose(0, 1)[None], kk, vv, attn_mask=mask[None, None],
+                                         scale=D ** -0.5)[0].transpose(0, 1)
+    with torch.inference_mode():
+        out = block_attention(q, cache, 0, mask=mask, valid_len=L).view(M, Hq, D)
+    err = float((out.float() - ref).abs().max())
+    assert err <= 2 ** -7 * float(ref.abs().max()) + 1e-3
+
+
+def _qkv_case(M, Hq, Hkv, n_pos, seed, dtype=torch.bfloat16):
+    from kernels.attention_fused import default_inv_freq, rope_tables
+    qkv = rnd(M, (Hq + 2 * Hkv) * D, dtype=dtype, scale=2.0, seed=seed)
+    qn = (1 + 0.1 * rnd(D, dtype=torch.float32, seed=seed + 1)).to(dtype)
+    kn = (1 + 0.1 * rnd(D, dtype=torch.float32, seed=seed + 2)).to(dtype)
+    cos, sin = rope_tables(default_inv_freq(device=DEV), n_pos, dtype)
+    return qkv, qn, kn, cos, sin
+
+
+def _oracle_qkv(qkv, Hq, Hkv, qn, kn, cos, sin, pos, dtype="bf16"):
+    M = qkv.shape[0]
+    x = qkv.float().cpu().numpy().reshape(M, Hq + 2 * Hkv, D)
+    c = cos.float().cpu().numpy()[pos.cpu().numpy()]
+    s = sin.float().cpu().numpy()[pos.cpu().numpy()]
+    q = oatt.qk_norm_rope(x[:, :Hq], None if qn is None else qn.float().cpu().numpy(), 1e-6, c, s, dtype)
+    k = oatt.qk_norm_rope(x[:, Hq:Hq + Hkv], None if kn is None else kn.float().cpu().numpy(), 1e-6, c, s, dtype)
+    return q, k, x[:, Hq + Hkv:]
+
+
+def _close_ulp(got, ref, dtype="bf16"):
+    ulp = 2.0 ** (-7 if dtype == "bf16" else -10)
+    assert np.all(np.abs(got - ref) <= ulp * np.abs(ref) + 1e-30)
+    assert (got != ref).mean() < 0.01
+
+
+@pytest.mark.parametrize("M,Hq,Hkv", [(4, 16, 8), (32, 32, 8), (7, 8, 8), (8, 12, 4)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_qkv_rope_cache_vs_oracle(M, Hq, Hkv, norm):
+    from kernels.attention_fused import BlockKVCache, qkv_rope_cache
+    print(f"qkv_rope_cache M={M} Hq={Hq} Hkv={Hkv} norm={norm}", flush=True)
+    qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 4096, seed=M * 3 + Hq)
+    if not norm:
+        qn = kn = None
+    cache = BlockKVCache(2, Hkv, 512, 64, DEV)
+    before_k = cache.key_cache[1].clone()
+    pos = torch.randperm(4096, device=DEV)[:M]
+    perm = torch.randperm(cache.full_len, device=DEV)      # two disjoint slot sets
+    slots, slots2 = perm[:M], perm[M:2 * M]
+    with torch.inference_mode():
+        q = qkv_rope_cache(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, slots, cache, 1, slots2=slots2)
+    torch.cuda.synchronize()
+    rq, rk, rv = _oracle_qkv(qkv, Hq, Hkv, qn, kn, cos, sin, pos)
+    _close_ulp(q.float().cpu().numpy(), rq)
+    kc = cache.key_cache[1].float().cpu().numpy()
+    vt = cache.value_cache_t[1].float().cpu().numpy()
+    for sl in (slots, slots2):
+        s = sl.cpu().numpy()
+        _close_ulp(kc[:, s].transpose(1, 0, 2), rk)
+        assert np.array_equal(vt[:, :, s].transpose(2, 0, 1), rv)
+    touched = set(slots.cpu().tolist()) | set(slots2.cpu().tolist())
+    untouched = [i for i in range(cache.full_len) if i not in touched]
+    assert torch.equal(cache.key_cache[1][:, untouched], before_k[:, untouched])
+    assert torch.count_nonzero(cache.key_cache[0]) == 0      # other layers untouched
+
+
+def test_qkv_rope_cache_bad_positions_and_slots():
+    from kernels.attention_fused import BlockKVCache, qkv_rope_cache
+    qkv, qn, kn, cos, sin = _qkv_case(3, 8, 4, 100, seed=5)
+    cache = BlockKVCache(1, 4, 64, 32, DEV)
+    pos = torch.tensor([5, 100, -1], device=DEV)            # rows 1, 2 out of range
+    slots = torch.tensor([3, 4, cache.full_len], device=DEV)  # the last slot is out of range
+    with torch.inference_mode():
+        q = qkv_rope_cache(qkv, 8, qn, kn, 1e-6, cos, sin, pos, slots, cache, 0)
+    assert torch.count_nonzero(q[1:]) == 0
+    assert torch.count_nonzero(cache.key_cache[0][:, 4]) == 0   # no k write for a bad position
+    assert torch.count_nonzero(cache.value_cache_t[0][:, :, 4]) > 0   # v is still written
+    assert torch.count_nonzero(cache.key_cache[0][:, 3]) > 0
+
+
+def test_reference_sequence_end_to_end():
+    """qkv_rope_cache + block_attention against the reference's torch sequence
+    (stock norms, apply_rotary_pos_emb, GQA-expanded index_copy_ writes, SDPA
+    with the bool mask) for one verify-shaped forward: 32 scratch rows over a
+    600-slot context."""
+    from kernels.attention_fused import BlockKVCache, block_attention, qkv_rope_cache
+    M, Hq, Hkv, ctx = 32, 32, 8, 600
+    n_rep = Hq // Hkv
+    qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 4096, seed=31)
+    cache = BlockKVCache(1, Hkv, 640, M, DEV)
+    k_ctx, v_ctx = fill_cache(cache, 0, ctx, seed=40)
+    pos = torch.arange(ctx, ctx + M, device=DEV)
+    slots = torch.arange(cache.max_cache_len, cache.max_cache_len + M, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(9)
+    mask = torch.zeros(M, cache.full_len, dtype=torch.bool, device=DEV)
+    mask[:, :ctx] = True
+    mask[:, cache.max_cache_len:cache.max_cache_len + M] = torch.rand(M, M, generator=g, device=DEV) < 0.5
+    mask[torch.arange(M), cache.max_cache_len + torch.arange(M, device=DEV)] = True
+    with torch.inference_mode():
+        q = qkv_rope_cache(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, slots, cache, 0)
+        out = block_attention(q, cache, 0, mask=mask).view(M, Hq, D)
+    # the reference, in torch on the device (SDPA in fp32)
+    x = qkv.view(M, Hq + 2 * Hkv, D)
+    c, s = cos[pos], sin[pos]
+
+    def norm_rope(t, w):
+        t32 = t.float()
+        t = w * (t32 * torch.rsqrt(t32.pow(2).mean(-1, keepdim=True) + 1e-6)).to(t.dtype)
+        t1, t2 = t[..., :64], t[..., 64:]
+        return (t * c[:, None]) + (torch.cat((-t2, t1), dim=-1) * s[:, None])
+
+    qr = norm_rope(x[:, :Hq], qn)
+    kr = norm_rope(x[:, Hq:Hq + Hkv], kn)
+    vr = x[:, Hq + Hkv:]
+    kexp = torch.zeros(1, Hq, cache.full_len, D, device=DEV, dtype=torch.bfloat16)
+    vexp = torch.zeros_like(kexp)
+    for i in range(n_rep):
+        kexp[:, i::n_rep, :ctx] = k_ctx[None]
+        vexp[:, i::n_rep, :ctx] = v_ctx[None]
+        kexp[:, i::n_rep].index_copy_(2, slots, kr.transpose(0, 1)[None])
+        vexp[:, i::n_rep].index_copy_(2, slots, vr.transpose(0, 1)[None])
+    ref = F.scaled_dot_product_attention(qr.transpose(0, 1)[None].float(), kexp.float(), vexp.float(),
+                                         attn_mask=mask[None, None], scale=D ** -0.5)[0].transpose(0, 1)
+    err = float((out.float() - ref).abs().max())
+    assert err <= 2 ** -7 * float(ref.abs().max()) + 1e-3, err
+
+
+def test_graph_capture_replays():
+    from kernels.attention_fused import BlockKVCache, block_attention, qkv_rope_cache
+    M, Hq, Hkv = 4, 16, 8
+    qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 2048, seed=50)
+    cache = BlockKVCache(1, Hkv, 992, 32, DEV)
+    fill_cache(cache, 0, 900, seed=51)
+    pos = torch.arange(900, 904, device=DEV)
+    slots = torch.arange(992, 996, device=DEV)
+    mask = torch.zeros(M, cache.full_len, dtype=torch.bool, device=DEV)
+    mask[:, :900] = True
+    mask[:, 992:996] = True
+    with torch.inference_mode():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            block_attention(qkv_rope_cache(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, slots, cache, 0), cache, 0, mask)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = block_attention(qkv_rope_cache(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, slots, cache, 0),
+                                  cache, 0, mask)
+        for r in range(3):
+            qkv.copy_(rnd(M, (Hq + 2 * Hkv) * D, scale=2.0, seed=60 + r))
+            g.replay()
+            torch.cuda.synchronize()
+            ref = block_attention(qkv_rope_cache(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, slots, cache, 0),
+                                  cache, 0, mask)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+
+
+def test_errors():
+    from kernels.attention_fused import BlockKVCache, block_attention, qkv_rope_cache
+    cache = BlockKVCache(1, 8, 64, 32, DEV)
+    with pytest.raises(TypeError):
+        block_attention(rnd(4, 16, D, dtype=torch.float32), cache, 0)
+    with pytest.raises(ValueError):
+        block_attention(rnd(4, 12, D), cache, 0)             # 12 heads over 8 KV heads
+    with pytest.raises(ValueError):
+        block_attention(rnd(4, 16, D), cache, 0, valid_len=cache.full_len + 1)
+    qkv, qn, kn, cos, sin = _qkv_case(2, 16, 8, 64, seed=1)
+    with pytest.raises(ValueError):
+        qkv_rope_cache(qkv[:, :-128], 16, qn, kn, 1e-6, cos, sin, torch.zeros(2, dtype=torch.int64, device=DEV),
+                       torch.zeros(2, dtype=torch.int64, device=DEV), cache, 0)
