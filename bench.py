@@ -32,6 +32,10 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           RoPE + cache write, then attention over 1024 slots (28 draft layers,
           4 rows, 16/8 heads; 36 target layers, 32 rows, 32/8 heads), against
           the reference's sequence on its GQA-expanded cache.
+  c5      the end-to-end speculative step: random-init SDAR-1.7B draft and
+          SDAR-8B target on one GPU, 512-token prompt, 4-token blocks, 4
+          denoise steps, 4 blocks verified per target forward, greedy
+          acceptance; value in generated tokens / s.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
@@ -604,6 +608,83 @@ def run_attn(args, torch, dev):
     return out, M
 
 
+# ───────────────────────────────────────────── end-to-end speculative step ───
+def run_c5(args, torch, dev):
+    """C5: random-init SDAR-1.7B draft and SDAR-8B target resident on one GPU,
+    a 512-token prompt uniform over the vocabulary, 4-token blocks denoised in
+    4 steps, K = 4 blocks verified per target forward (32 rows), greedy
+    acceptance, committed blocks written to the target cache by an extend
+    forward.  value = generated tokens / second over the timed iterations."""
+    import time as _time
+
+    from speculative.model import DRAFT_1P7B, TARGET_8B, SynthModel
+    from speculative.step import SpecRunner
+
+    steps, warm = args.steps, max(2, args.warmup)
+    max_ctx = 512 + 16 * (steps + warm) + 64
+    t_init = _time.perf_counter()
+    draft = SynthModel(DRAFT_1P7B, dev, seed=11, max_ctx=max_ctx, max_rows=64)
+    target = SynthModel(TARGET_8B, dev, seed=12, max_ctx=max_ctx, max_rows=64)
+    runner = SpecRunner(draft, target)
+    prompt = torch.randint(0, DRAFT_1P7B.vocab - 1, (512,), generator=torch.Generator().manual_seed(5))
+    runner.prefill(prompt)
+    init_s = _time.perf_counter() - t_init
+    for _ in range(warm):                 # captures the graphs
+        runner.step()
+    torch.cuda.synchronize()
+    n_tok = n_acc = n_blocks = 0
+    phase = [0.0, 0.0, 0.0, 0.0]
+    t0 = _time.perf_counter()
+    for _ in range(steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        ctx0 = runner.ctx
+        gen, acc = runner.step(events=ev[:4])
+        ev[4].record()
+        n_tok += len(gen)
+        n_acc += acc
+        n_blocks += (runner.ctx - ctx0) // runner.bl
+        ev[4].synchronize()
+        for i in range(4):
+            phase[i] += ev[i].elapsed_time(ev[i + 1])
+    torch.cuda.synchronize()
+    secs = _time.perf_counter() - t0
+    it_ms = secs * 1e3 / steps
+
+    def layer_bytes(sh):
+        H, D, I = sh.hidden, sh.head_dim, sh.intermediate
+        return 2 * (H * (sh.n_q_heads + 2 * sh.n_kv_heads) * D + sh.n_q_heads * D * H + 2 * I * H + H * I)
+
+    d_fwd = DRAFT_1P7B.n_layers * layer_bytes(DRAFT_1P7B) + 2 * DRAFT_1P7B.vocab * DRAFT_1P7B.hidden
+    t_fwd = TARGET_8B.n_layers * layer_bytes(TARGET_8B)
+    t_head = 2 * TARGET_8B.vocab * TARGET_8B.hidden
+    d_fwds = runner.K * len(runner.schedule)
+    it_bytes = d_fwds * d_fwd + (t_fwd + t_head) + t_fwd * (n_blocks / steps)
+    gbs = it_bytes / (it_ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": round(n_tok / secs, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": steps, "warmup": warm, "ms_per_step": round(it_ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform random prompt)",
+        "config": {"workload": "spec-step-SDAR1.7B-draft-SDAR8B-target-bl4-ds4-K4-greedy",
+                   "prompt": 512, "block_length": 4, "denoise_steps": 4, "k_blocks": 4,
+                   "draft_forwards_per_iteration": d_fwds, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole iteration: weight bytes of every forward / iteration time",
+                     "bytes_per_iteration": int(it_bytes)},
+        "tokens_per_iteration": round(n_tok / steps, 3),
+        "accepted_draft_tokens_per_iteration": round(n_acc / steps, 3),
+        "committed_blocks_per_iteration": round(n_blocks / steps, 3),
+        "phase_ms_per_iteration": {"draft": round(phase[0] / steps, 3), "verify": round(phase[1] / steps, 3),
+                                   "accept_host": round(phase[2] / steps, 3), "extend": round(phase[3] / steps, 3)},
+        "hbm_bound_ms_per_iteration": round(it_bytes / 8e12 * 1e3, 3),
+        "init_s": round(init_s, 1),
+        "cpu_baseline": None,
+        "cpu_baseline_note": "not timed: one iteration is 16 draft + 2 target forwards of 1.7B/8B models "
+                             "(minutes per iteration on the host cores)",
+    }, 4
+
+
 # ────────────────────────────────────────────────────────────────── MoE ───
 def run_moe(args, torch, dev):
     from kernels.moe_dispatch_fused import moe_forward, moe_route
@@ -739,7 +820,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -756,6 +837,11 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
+    if args.workload == "c5":
+        result, _ = run_c5(args, torch, dev)
+        result["device"] = torch.cuda.get_device_name(dev)
+        print(json.dumps(result), flush=True)
         return
     if args.workload.startswith(("mlp", "layer", "head", "attn")):
         runner = {"mlp": run_mlp, "layer": run_layer, "head": run_head,

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 7
+#define SIMSD_ABI_VERSION 9
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -270,16 +270,33 @@ int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, co
  * rows of at least L_valid rounded up to 4 bytes).  Slots
  * [0, L_valid) are considered, L_valid <= L_cap (the cache's slot count, a
  * multiple of 4); fp32 softmax, output rounded to the dtype; rows with no
- * visible slot give 0.  q [M, Hq, D] and out [M, Hq, D] with (row, head)
- * strides.  Workspace: simsd_block_attention_workspace_bytes(M, Hq, Hkv,
+ * visible slot give 0.  valid_len_dev (nullable) points at a device int64
+ * that lowers L_valid at run time (clamped to [0, L_valid]), so a captured
+ * graph can follow a growing context.  q [M, Hq, D] and out [M, Hq, D] with
+ * (row, head) strides.  Workspace: simsd_block_attention_workspace_bytes(M, Hq, Hkv,
  * L_valid), 16-byte aligned.  Deterministic. */
 int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid);
 
 int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, int64_t skh, int64_t skl,
                           const void* vt_cache, int64_t svh, int64_t svd, int64_t L_cap, const uint8_t* mask,
                           int64_t smask, void* out, int64_t so_m, int64_t so_h, int64_t M, int64_t Hq, int64_t Hkv,
-                          int64_t L_valid, int64_t head_dim, float scale, int dtype, void* workspace,
-                          int64_t workspace_bytes, void* stream);
+                          int64_t L_valid, const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype,
+                          void* workspace, int64_t workspace_bytes, void* stream);
+
+/* simsd_block_mask: the attention mask rows (uint8, 1 = visible; row stride
+ * smask, n_cols slots) of a cached forward whose rows are n_prefix rows of a
+ * committed block folded in (speculative_decoding/cache_aware.py:1062-1070),
+ * n_free rows of the block being denoised, and K verify blocks of bl data
+ * then bl mask rows (speculative_decoding/verify.py:350-418).  Slots
+ * [0, ctx_len) are the committed context; the rows' own scratch slots start at
+ * s0 in row order.  Verify visibility follows the multi-block rule of
+ * sdar/new_attn_multi_block.py:22-183 with step_map [K, bl] (int64, device;
+ * -1 = never drafted) and bs denoising steps per block; every row sees the
+ * context and the prefix; the free block sees itself.  Replaces the torch
+ * mask construction of cache_aware.py:1149-1180 and the multi-block mask
+ * builder. */
+int simsd_block_mask(uint8_t* mask, int64_t smask, int64_t n_cols, int64_t ctx_len, int64_t s0, int n_prefix,
+                     int n_free, int K, int bl, int bs, const int64_t* step_map, void* stream);
 
 #ifdef __cplusplus
 }

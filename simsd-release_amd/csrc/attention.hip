@@ -178,6 +178,7 @@ struct AttnArgs {
   int n_chunks;
   float scale;
   int rows, rows_pad;         // n_rep * M, padded to 16
+  const int64_t* lv_dev;      // device-side valid slot count (<= L_valid) or null
   float* o_part;              // [Hkv][n_chunks][rows_pad][D]
   float2* ml_part;            // [Hkv][n_chunks][rows_pad]
 };
@@ -341,8 +342,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
+  int64_t lv = a.L_valid;
+  if (a.lv_dev != nullptr) {
+    const int64_t d = *a.lv_dev;
+    lv = d < 0 ? 0 : (d < lv ? d : lv);
+  }
   const int64_t chunk_lo = (int64_t)chunk_id * a.chunk;
-  const int64_t chunk_hi = min(a.L_valid, chunk_lo + a.chunk);
+  const int64_t chunk_hi = min(lv, chunk_lo + a.chunk);
   const int64_t c_begin = KSPLIT ? min(chunk_hi, chunk_lo + (int64_t)wv * a.wave_chunk) : chunk_lo;
   const int64_t c_end = KSPLIT ? min(chunk_hi, c_begin + a.wave_chunk) : chunk_hi;
   const char* kbase = a.kc + (int64_t)h * a.skh * ES;
@@ -468,6 +474,83 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __r
   store_elem<DT>(out, m * so_m + (int64_t)hq * so_h + d, l > 0.f ? o / l : 0.f);
 }
 
+// ------------------------------------------------------ block visibility
+// Attention mask rows of a cached forward over the slot space: [0, ctx_len)
+// committed context, then from slot s0 the rows' own scratch slots in row
+// order.  Rows: n_prefix rows of a committed block (folded in to store its
+// K/V), n_free rows of the block being denoised, then K verify blocks of bl
+// data rows and bl mask rows.  The verify rule is sdar/new_attn_multi_block.py:
+// 22-183 on the layout of speculative_decoding/verify.py:350-418: data at
+// position p carries step_map[k][p] + 1 (bs + 1, i.e. a mask, when never
+// drafted), a mask token takes the step of the data token of equal
+// within-block rank, and within a block
+//   data i sees data j iff t_j <= t_i, mask j iff t_j > t_i,
+//   mask i sees data j iff t_j <  t_i, mask j iff t_j >= t_i;
+// a later block sees an earlier block's data only.  Every row sees the
+// context and the prefix; the free block sees itself; nothing else is visible.
+constexpr int kMaxVerifyTokens = 1024;
+
+__global__ __launch_bounds__(256) void block_mask_kernel(uint8_t* __restrict__ mask, int64_t smask, int64_t n_cols,
+                                                         int64_t ctx_len, int64_t s0, int n_prefix, int n_free, int K,
+                                                         int bl, int bs, const int64_t* __restrict__ step_map) {
+  __shared__ int8_t typ[kMaxVerifyTokens];      // 1 data, 2 mask
+  __shared__ int16_t tim[kMaxVerifyTokens];
+  const int nv = 2 * K * bl;
+  auto label = [&](int v) {
+    const int k = v / (2 * bl), w = v % (2 * bl);
+    if (w >= bl) return bs + 1;
+    const int64_t st = step_map[(int64_t)k * bl + w];
+    return st >= 0 ? (int)st + 1 : bs + 1;
+  };
+  for (int v = threadIdx.x; v < nv; v += blockDim.x) {
+    const int k = v / (2 * bl), w = v % (2 * bl);
+    const int lab = label(v);
+    const bool is_data = lab <= bs;
+    int rank = 0;
+    for (int u = 0; u < w; ++u) rank += ((label(k * 2 * bl + u) <= bs) == is_data) ? 1 : 0;
+    int t = lab;
+    if (!is_data) {   // the data token of the same rank, if any
+      int seen = 0;
+      for (int u = 0; u < 2 * bl; ++u) {
+        const int lu = label(k * 2 * bl + u);
+        if (lu <= bs) {
+          if (seen == rank) { t = lu; break; }
+          ++seen;
+        }
+      }
+    }
+    typ[v] = is_data ? 1 : 2;
+    tim[v] = (int16_t)t;
+  }
+  __syncthreads();
+  const int row = blockIdx.y;
+  const int64_t col = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (col >= n_cols) return;
+  bool vis = false;
+  if (col < ctx_len) {
+    vis = true;
+  } else if (col >= s0) {
+    const int64_t u = col - s0;
+    if (u < n_prefix) {
+      vis = true;
+    } else if (u < n_prefix + n_free) {
+      vis = row >= n_prefix && row < n_prefix + n_free;
+    } else if (u < n_prefix + n_free + nv && row >= n_prefix + n_free) {
+      const int j = (int)(u - n_prefix - n_free);
+      const int i = row - n_prefix - n_free;
+      const int ki = i / (2 * bl), kj = j / (2 * bl);
+      if (ki == kj) {
+        const int ti = tim[i], tj = tim[j];
+        if (typ[i] == 1) vis = typ[j] == 1 ? tj <= ti : tj > ti;
+        else vis = typ[j] == 1 ? tj < ti : tj >= ti;
+      } else {
+        vis = ki > kj && typ[j] == 1;
+      }
+    }
+  }
+  mask[(int64_t)row * smask + col] = vis ? 1 : 0;
+}
+
 struct AttnPlan {
   int rows, rows_pad, rb, rbw, waves, groups, n_chunks;
   bool ksplit;
@@ -568,9 +651,9 @@ extern "C" int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, 
 extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, int64_t skh,
                                      int64_t skl, const void* vt_cache, int64_t svh, int64_t svd, int64_t L_cap,
                                      const uint8_t* mask, int64_t smask, void* out, int64_t so_m, int64_t so_h,
-                                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid, int64_t head_dim,
-                                     float scale, int dtype, void* workspace, int64_t workspace_bytes,
-                                     void* stream) {
+                                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid,
+                                     const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
   if (dtype != kBF16 && dtype != kF16) return set_error("block_attention: dtype must be bf16 or fp16");
   if (head_dim != kHeadDim) return set_error("block_attention: head_dim must be %d (got %lld)", kHeadDim, (long long)head_dim);
   if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L_valid < 0 || L_valid > L_cap)
@@ -595,6 +678,7 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
   a.kc = static_cast<const char*>(k_cache); a.skh = skh; a.skl = skl;
   a.vt = static_cast<const char*>(vt_cache); a.svh = svh; a.svd = svd;
   a.mask = mask; a.smask = smask;
+  a.lv_dev = valid_len_dev;
   a.M = M; a.n_rep = (int)(Hq / Hkv); a.Hkv = (int)Hkv;
   a.L_valid = L_valid; a.chunk = pl.chunk; a.wave_chunk = pl.wave_chunk; a.n_chunks = pl.n_chunks;
   a.scale = scale;
@@ -618,4 +702,22 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
   if (dtype == kBF16) partial(std::integral_constant<int, kBF16>{});
   else partial(std::integral_constant<int, kF16>{});
   return check_launch("block_attention");
+}
+
+extern "C" int simsd_block_mask(uint8_t* mask, int64_t smask, int64_t n_cols, int64_t ctx_len, int64_t s0,
+                                int n_prefix, int n_free, int K, int bl, int bs, const int64_t* step_map,
+                                void* stream) {
+  if (mask == nullptr || n_cols <= 0 || smask < n_cols || ctx_len < 0 || s0 < ctx_len || n_prefix < 0 ||
+      n_free < 0 || K < 0 || bl <= 0 || bs <= 0 || bs > 30000)
+    return set_error("block_mask: bad arguments");
+  if (2LL * K * bl > kMaxVerifyTokens) return set_error("block_mask: more than %d verify tokens", kMaxVerifyTokens);
+  if (K > 0 && step_map == nullptr) return set_error("block_mask: null step_map");
+  const int64_t rows = n_prefix + n_free + 2LL * K * bl;
+  if (rows == 0) return 0;
+  if (rows > 65535) return set_error("block_mask: too many rows");
+  if (s0 + n_prefix + n_free + 2LL * K * bl > n_cols) return set_error("block_mask: scratch slots past n_cols");
+  const dim3 grid((unsigned)((n_cols + 255) / 256), (unsigned)rows);
+  hipLaunchKernelGGL(block_mask_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), mask, smask, n_cols,
+                     ctx_len, s0, n_prefix, n_free, K, bl, bs, step_map);
+  return check_launch("block_mask");
 }

@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 9
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -57,8 +57,9 @@ SIGNATURES = {
                                     _i64, _i64, _i64, _i64, _i32, _vp]),
     "simsd_block_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "simsd_block_attention": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
-                                     _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
                                      _f32, _i32, _vp, _i64, _vp]),
+    "simsd_block_mask": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
     "simsd_moe_route_topk": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
     "simsd_moe_num_tiles": (_i32, [_i64, _i64]),
     "simsd_moe_align": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

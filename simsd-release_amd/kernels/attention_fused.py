@@ -132,12 +132,16 @@ def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weig
 
 
 def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torch.Tensor | None = None,
-                    valid_len: int | None = None, scale: float | None = None) -> torch.Tensor:
+                    valid_len: int | None = None, scale: float | None = None,
+                    valid_len_dev: torch.Tensor | None = None) -> torch.Tensor:
     """softmax(scale * q K^T, masked) V over the cache's slots [0, valid_len).
 
     q:    [M, Hq, 128] (query head hq reads KV head hq // (Hq / Hkv))
     mask: bool/uint8 [M, >= valid_len], True = visible (the reference's SDPA
           mask rows), or None (all visible)
+    valid_len_dev: optional int64 scalar tensor on the device that lowers
+          valid_len when the kernels run (for graphs replayed over a growing
+          context)
     -> [M, Hq * 128] (the layout o_proj takes).
     """
     code = _native.DTYPE_CODES.get(q.dtype)
@@ -167,7 +171,9 @@ def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torc
             pad[:, :m8.shape[1]].copy_(m8)
             m8 = pad
     kc, vt = cache.key_cache[layer], cache.value_cache_t[layer]
-    dev = _native.require_device(q, kc, m8)
+    if valid_len_dev is not None and (valid_len_dev.dtype != torch.int64 or valid_len_dev.numel() != 1):
+        raise ValueError("block_attention: valid_len_dev must be one int64 on the device")
+    dev = _native.require_device(q, kc, m8, valid_len_dev)
     out = torch.empty((M, Hq, D), device=dev, dtype=q.dtype)
     if M == 0:
         return out.view(M, Hq * D)
@@ -181,8 +187,40 @@ def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torc
             q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), kc.stride(0), kc.stride(1),
             vt.data_ptr(), vt.stride(0), vt.stride(1), cache.full_len,
             m8.data_ptr() if m8 is not None else None, m8.stride(0) if m8 is not None else 0,
-            out.data_ptr(), out.stride(0), out.stride(1), M, Hq, Hkv, L, D,
+            out.data_ptr(), out.stride(0), out.stride(1), M, Hq, Hkv, L,
+            valid_len_dev.data_ptr() if valid_len_dev is not None else None, D,
             float(D ** -0.5 if scale is None else scale), code, ws.data_ptr(), ws.numel(),
             _native.stream_of(dev))
     _native.check(status, "block_attention")
     return out.view(M, Hq * D)
+
+
+def block_mask(n_cols: int, ctx_len: int, s0: int, n_prefix: int = 0, n_free: int = 0,
+               step_maps: torch.Tensor | None = None, block_length: int = 4, block_size: int = 4,
+               out: torch.Tensor | None = None, device=None) -> torch.Tensor:
+    """Mask rows [n_prefix committed | n_free denoising | K verify blocks] of
+    a cached forward over ``n_cols`` slots (context [0, ctx_len), the rows'
+    scratch slots from ``s0``); ``step_maps`` int64 [K, block_length] on the
+    device (-1 = never drafted).  -> bool [rows, n_cols] (written into ``out``
+    when given: bool or uint8 with unit column stride and a row stride that is
+    a multiple of 4)."""
+    K = 0 if step_maps is None else int(step_maps.shape[0])
+    if step_maps is not None:
+        if step_maps.dtype != torch.int64 or step_maps.ndim != 2 or step_maps.shape[1] != block_length:
+            raise ValueError("block_mask: step_maps must be int64 [K, block_length]")
+        step_maps = step_maps.contiguous()
+        device = step_maps.device
+    rows = n_prefix + n_free + 2 * K * block_length
+    if out is None:
+        out = torch.empty((rows, (n_cols + 3) // 4 * 4), device=device, dtype=torch.bool)
+    if out.shape[0] != rows or out.shape[1] < n_cols or out.stride(1) != 1:
+        raise ValueError(f"block_mask: out must be [{rows}, >= {n_cols}] with unit column stride")
+    if rows == 0:
+        return out[:, :n_cols]
+    dev = _native.require_device(out, step_maps)
+    with _native.device_guard(dev):
+        status = _native.lib().simsd_block_mask(
+            out.data_ptr(), out.stride(0), n_cols, ctx_len, s0, n_prefix, n_free, K, block_length, block_size,
+            step_maps.data_ptr() if step_maps is not None else None, _native.stream_of(dev))
+    _native.check(status, "block_mask")
+    return out[:, :n_cols]

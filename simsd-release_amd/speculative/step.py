@@ -1,0 +1,228 @@
+"""The speculative step on one MI355X: K draft blocks denoised by the draft,
+verified by the target in one cached forward, greedy acceptance.
+
+Mirrors the reference's K-block loop (speculative_decoding/speculative_decode.py:
+840-953 with greedy_match_verify, the fused denoise graphs of
+cache_aware.py:840-1075 and the multi-block verify of verify.py:421-700),
+with the target's verify run against its KV cache: its rows are only the K
+draft blocks (data, mask), not the whole prompt.  Per iteration:
+
+  draft   K block graphs; each folds the previous block in as a committed
+          prefix (its K/V rewritten in place) and runs ds denoise forwards of
+          [prefix 4 | block 4] rows, each unmasking ceil(remaining / steps
+          left) positions by confidence (denoise_select)
+  verify  one target forward of the K x (4 data + 4 mask) rows; mask rows'
+          argmax (softmax_argmax)
+  accept  greedy match per block with first-reject truncation; a rejected
+          block is committed padded with the draft's own tokens
+          (partial_block_fill = "draft_argmax")
+  extend  one target forward of the committed block(s), storing their K/V.
+
+The committed context lives in permanent cache slots [0, ctx); a forward's
+rows write their K/V at slots ctx.. in row order (past the committed context,
+so a later forward overwrites them), and each row's mask comes from
+block_mask on the device.  Every forward is a captured HIP graph whose
+per-iteration inputs (ids, positions, slots, mask, valid length) are device
+buffers refreshed before the replay.  One host synchronisation per iteration
+reads the 2 x K x 4 ids the acceptance needs.
+"""
+from __future__ import annotations
+
+import torch
+
+from kernels.attention_fused import block_mask
+from kernels.logits_fused import denoise_select, softmax_argmax
+
+from .model import SynthModel
+from .verify import MASK_TOKEN_ID, accept_blocks
+
+
+def unmask_schedule(n_masks: int, steps: int):
+    """Positions unmasked per denoise step (cache_aware.py:869-877)."""
+    out, rem = [], n_masks
+    for s in range(steps):
+        n = -(-rem // (steps - s))
+        if n <= 0:
+            break
+        out.append(n)
+        rem -= n
+    return out
+
+
+class _Graphed:
+    """A forward captured once over static device buffers."""
+
+    def __init__(self, rows: int, n_cols: int, device):
+        self.ids = torch.zeros(rows, dtype=torch.int64, device=device)
+        self.pos = torch.zeros(rows, dtype=torch.int64, device=device)
+        self.slots = torch.zeros(rows, dtype=torch.int64, device=device)
+        self.mask = torch.zeros(rows, (n_cols + 3) // 4 * 4, dtype=torch.bool, device=device)
+        self.valid = torch.zeros(1, dtype=torch.int64, device=device)
+        self.graph = None
+
+    def set_span(self, start: int, ctx_len: int, rows: int):
+        """Rows at positions/slots start.. (row order); valid = start + rows."""
+        ar = torch.arange(start, start + rows, dtype=torch.int64, device=self.pos.device)
+        self.pos.copy_(ar)
+        self.slots.copy_(ar)
+        self.valid.fill_(start + rows)
+
+    def capture(self, body):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            body()                                   # warm: allocations, lazy init
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = body()
+
+    def replay(self):
+        self.graph.replay()
+        return self.out
+
+
+class SpecRunner:
+    """Greedy speculative decoding of one sequence with a draft and a target
+    resident on one GPU."""
+
+    def __init__(self, draft: SynthModel, target: SynthModel, block_length: int = 4, denoise_steps: int = 4,
+                 k_blocks: int = 4, mask_token_id: int = MASK_TOKEN_ID):
+        self.draft, self.target = draft, target
+        self.bl, self.ds, self.K = block_length, denoise_steps, k_blocks
+        self.mask_id = mask_token_id
+        self.dev = draft.device
+        self.schedule = unmask_schedule(block_length, denoise_steps)
+        bl, K = block_length, k_blocks
+        dcols, tcols = draft.cache.full_len, target.cache.full_len
+        self._dg = _Graphed(2 * bl, dcols, self.dev)                  # [prefix | block]
+        self._vg = _Graphed(2 * K * bl, tcols, self.dev)              # K x (data, mask)
+        self._eg = {}                                                 # committed blocks -> extend graph
+        self._step_map = torch.full((bl,), -1, dtype=torch.int64, device=self.dev)
+        self.draft_blocks = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
+        self.step_maps = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
+        self.ctx = 0
+        self.tokens = []          # generated tokens (accepted + bonus)
+        self.history = []         # the committed context: prompt + committed blocks
+
+    # ----------------------------------------------------------- prefill
+    @torch.inference_mode()
+    def prefill(self, prompt_ids: torch.Tensor):
+        """Both caches take the prompt (block-causal over blocks of
+        block_length, as the SDAR prompt rule; not part of the timed step)."""
+        n = int(prompt_ids.numel())
+        if n % self.bl:
+            raise ValueError("prompt length must be a multiple of the block length")
+        ids = prompt_ids.to(self.dev, torch.int64)
+        ar = torch.arange(n, device=self.dev)
+        blk = ar // self.bl
+        for m in (self.draft, self.target):
+            mask = torch.zeros(n, m.cache.full_len, dtype=torch.bool, device=self.dev)
+            mask[:, :n] = blk[None, :] <= blk[:, None]
+            m.forward(ids, ar, ar, mask, valid_len=n, head=False)
+        self.ctx = n
+        self.history = prompt_ids.tolist()
+        self.last_block = ids[n - self.bl:].clone()
+        torch.cuda.synchronize()
+
+    # ------------------------------------------------------------ graphs
+    def _draft_body(self):
+        g, bl = self._dg, self.bl
+        g.ids[bl:].fill_(self.mask_id)
+        self._step_map.fill_(-1)
+        for step, n_u in enumerate(self.schedule):
+            logits = self.draft.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.draft.cache.full_len,
+                                        valid_len_dev=g.valid, head_rows=slice(bl, 2 * bl))
+            denoise_select(logits, g.ids[bl:], self.mask_id, n_u, step, self._step_map)
+        return None
+
+    def _verify_body(self):
+        g = self._vg
+        logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.target.cache.full_len,
+                                     valid_len_dev=g.valid)
+        ids, _ = softmax_argmax(logits)
+        return ids
+
+    def _extend_body(self, g):
+        self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.target.cache.full_len,
+                            valid_len_dev=g.valid, head=False)
+        return None
+
+    def _extend_graph(self, n_blocks: int):
+        g = self._eg.get(n_blocks)
+        if g is None:
+            g = _Graphed(n_blocks * self.bl, self.target.cache.full_len, self.dev)
+            g.set_span(self.ctx, self.ctx, n_blocks * self.bl)
+            g.capture(lambda: self._extend_body(g))
+            self._eg[n_blocks] = g
+        return g
+
+    def history_ids(self):
+        return list(self.history)
+
+    # ---------------------------------------------------------- one step
+    @torch.inference_mode()
+    def draft_blocks_(self):
+        """K blocks; block k folds block k - 1 (the last committed block for
+        k = 0) in as its prefix."""
+        g, bl, dcols = self._dg, self.bl, self.draft.cache.full_len
+        for k in range(self.K):
+            start = self.ctx - bl + k * bl            # prefix position
+            g.ids[:bl].copy_(self.last_block if k == 0 else self.draft_blocks[k - 1])
+            g.set_span(start, start, 2 * bl)
+            block_mask(dcols, start, start, n_prefix=bl, n_free=bl, out=g.mask)
+            if g.graph is None:
+                g.capture(self._draft_body)
+            g.replay()
+            self.draft_blocks[k].copy_(g.ids[bl:])
+            self.step_maps[k].copy_(self._step_map)
+
+    @torch.inference_mode()
+    def verify_(self):
+        g, bl, K = self._vg, self.bl, self.K
+        ids = g.ids.view(K, 2, bl)
+        ids[:, 0].copy_(self.draft_blocks)
+        ids[:, 1].fill_(self.mask_id)
+        pos = torch.arange(self.ctx, self.ctx + K * bl, dtype=torch.int64, device=self.dev).view(K, 1, bl)
+        g.pos.view(K, 2, bl).copy_(pos.expand(K, 2, bl))       # masks share the data positions
+        g.slots.copy_(torch.arange(self.ctx, self.ctx + 2 * K * bl, dtype=torch.int64, device=self.dev))
+        g.valid.fill_(self.ctx + 2 * K * bl)
+        block_mask(self.target.cache.full_len, self.ctx, self.ctx, step_maps=self.step_maps,
+                   block_length=bl, block_size=self.ds, out=g.mask)
+        if g.graph is None:
+            g.capture(self._verify_body)
+        return g.replay().view(K, 2, bl)[:, 1]
+
+    @torch.inference_mode()
+    def extend_(self, blocks):
+        n = len(blocks)
+        g = self._extend_graph(n)
+        g.ids.copy_(torch.tensor([t for b in blocks for t in b], dtype=torch.int64).to(self.dev, non_blocking=True))
+        g.set_span(self.ctx, self.ctx, n * self.bl)
+        block_mask(self.target.cache.full_len, self.ctx, self.ctx, n_prefix=n * self.bl, out=g.mask)
+        g.replay()
+
+    @torch.inference_mode()
+    def step(self, events=None):
+        """One iteration -> (generated tokens, accepted draft tokens).  With
+        ``events`` (four torch.cuda.Event), their records bracket the draft,
+        verify, acceptance and extend phases on the current stream."""
+        if events:
+            events[0].record()
+        self.draft_blocks_()
+        if events:
+            events[1].record()
+        target_ids = self.verify_()
+        if events:
+            events[2].record()
+        both = torch.stack([self.draft_blocks, target_ids]).cpu()     # the one host sync
+        committed, generated, n_acc = accept_blocks(both[0].tolist(), both[1].tolist(), self.bl)
+        if events:
+            events[3].record()
+        self.extend_(committed)
+        self.ctx += self.bl * len(committed)
+        self.history.extend(t for b in committed for t in b)
+        self.last_block = torch.tensor(committed[-1], dtype=torch.int64, device=self.dev)
+        self.tokens.extend(generated)
+        return generated, n_acc
