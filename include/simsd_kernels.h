@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 9
+#define SIMSD_ABI_VERSION 10
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -208,6 +208,17 @@ int simsd_moe_grouped_ffn(const void* x, int64_t stride_xt, int64_t stride_xh,
                           int64_t T, int k, int64_t E, int64_t H, int64_t I, int dtype,
                           void* workspace, int64_t workspace_bytes, void* stream);
 
+/* y[m, n] = residual[m, n] + dtype(sum_k x[m, k] * w[n, k]): the linear with
+ * the decoder layer's residual add in its epilogue (the projection rounded to
+ * the dtype, then the dtype add, as `hidden = residual + o_proj(attn)` and
+ * `hidden = residual + mlp(...)` compute it, sdar/modeling_sdar.py's decoder
+ * layer).  y may be the residual itself (in place).  Other arguments as
+ * simsd_thin_linear; workspace from simsd_thin_linear_workspace_bytes. */
+int simsd_thin_linear_residual(const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn, int64_t swk,
+                               const void* residual, int64_t srm, int64_t srn, void* y, int64_t sym, int64_t syn,
+                               int64_t M, int64_t N, int64_t K, int dtype, int block_n, int block_k, int split_k,
+                               int num_waves, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- logits epilogue: softmax statistics and the unmasking choice -------
  * For logits rows l[m, 0:V] (bf16, fp16 or fp32; row stride slm elements,
  * unit element stride):
@@ -270,7 +281,10 @@ int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, co
  * rows of at least L_valid rounded up to 4 bytes).  Slots
  * [0, L_valid) are considered, L_valid <= L_cap (the cache's slot count, a
  * multiple of 4); fp32 softmax, output rounded to the dtype; rows with no
- * visible slot give 0.  valid_len_dev (nullable) points at a device int64
+ * visible slot give 0.  Every slot below L_cap must hold finite values (a
+ * zero-initialised cache written only with finite K/V), since slots past a
+ * row's visible range may enter the P.V product with weight 0.
+ * valid_len_dev (nullable) points at a device int64
  * that lowers L_valid at run time (clamped to [0, L_valid]), so a captured
  * graph can follow a growing context.  q [M, Hq, D] and out [M, Hq, D] with
  * (row, head) strides.  Workspace: simsd_block_attention_workspace_bytes(M, Hq, Hkv,

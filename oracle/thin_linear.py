@@ -17,6 +17,9 @@ plus bias (``y += bias`` after the GEMM, kernels/thin_linear_fused.py:343-344).
 ``rmsnorm_exact``     the stock RMSNorm (sdar/run_native_tp2.py:42-47): the
                       mean of squares in fp64, x * r rounded to the dtype, times
                       the weight, rounded again.
+``linear_residual_exact``  residual + linear_exact(x, w): the projection
+                      rounded to the dtype, then the dtype add (the decoder
+                      layer's ``hidden = residual + proj(...)``).
 ``tolerance``         the reference's bounds (thin_linear_fused_test.py:28-32).
 """
 from __future__ import annotations
@@ -56,6 +59,13 @@ def rmsnorm_exact(x: np.ndarray, weight: np.ndarray, eps: float, dtype: str = "b
     x64 = np.asarray(x, dtype=np.float64)
     r = 1.0 / np.sqrt((x64 * x64).mean(axis=-1, keepdims=True) + eps)
     return rnd(np.asarray(weight, dtype=np.float64) * rnd(x64 * r))
+
+
+def linear_residual_exact(x: np.ndarray, w: np.ndarray, residual: np.ndarray, dtype: str = "bf16") -> np.ndarray:
+    """rnd(rnd(x w^T) + residual), the add formed in fp32 as the dtype's add."""
+    y = linear_exact(x, w, dtype=dtype)
+    s = (y + np.asarray(residual, dtype=np.float64)).astype(np.float32).astype(np.float64)
+    return ROUNDERS[dtype](s)
 
 
 def linear_cpu_torch(x, w, bias=None):

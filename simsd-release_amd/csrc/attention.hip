@@ -204,6 +204,54 @@ SIMSD_DEV u32x2_t load_vt4(const char* rowp, int64_t key, int64_t end, int64_t l
   return v;
 }
 
+// Buffer loads of 8 and 4 bytes (the 16-byte one is in simsd_common.hpp):
+// offsets at or past the descriptor's extent read as zero, with no branch.
+__device__ int32_t __attribute__((ext_vector_type(2)))
+simsd_raw_buffer_load_v2i32(i32x4_t rsrc, int32_t voffset, int32_t soffset, int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v2i32");
+__device__ int32_t simsd_raw_buffer_load_i32(i32x4_t rsrc, int32_t voffset, int32_t soffset, int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i32");
+
+SIMSD_DEV u32x2_t buf_load8(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2_t, simsd_raw_buffer_load_v2i32(r, (int32_t)off, 0, 0));
+}
+SIMSD_DEV uint32_t buf_load4(rsrc_t r, uint32_t off) { return (uint32_t)simsd_raw_buffer_load_i32(r, (int32_t)off, 0, 0); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// A wave's view of one KV head over its key range [.., c_end): descriptors
+// and per-lane byte offsets, so each 32-key step's loads are one add each.
+//   K:  extent c_end rows -- keys past the range read as zero;
+//   Vt: the head's D x svd block -- keys past the range read stale slots,
+//       which are finite (the cache starts zeroed and only takes finite
+//       values) and meet p = 0;
+//   mask: all M rows.
+template <int RBW>
+struct WaveKV {
+  rsrc_t rk, rv, rm;
+  uint32_t k_off[2], v_off[kDTiles], m_off[RBW];
+  uint32_t k_step;   // bytes of one key row
+};
+
+template <int DT, int RBW>
+SIMSD_DEV WaveKV<RBW> wave_kv(const AttnArgs& a, int h, int64_t c_end, const int (&tok)[RBW], int g, int r) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  WaveKV<RBW> w;
+  const char* kbase = a.kc + (int64_t)h * a.skh * ES;
+  const char* vbase = a.vt + (int64_t)h * a.svh * ES;
+  w.k_step = (uint32_t)(a.skl * ES);
+  w.rk = make_rsrc(kbase, (uint32_t)c_end * w.k_step);
+  w.rv = make_rsrc(vbase, (uint32_t)(kHeadDim * a.svd * ES));
+  w.rm = make_rsrc(a.mask, a.mask != nullptr ? (uint32_t)(a.M * a.smask) : 0u);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) w.k_off[t] = (uint32_t)(16 * t + r) * w.k_step + (uint32_t)(8 * g * ES);
+#pragma unroll
+  for (int dt = 0; dt < kDTiles; ++dt) w.v_off[dt] = (uint32_t)((dt * 16 + r) * a.svd + 4 * g) * ES;
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) w.m_off[rb] = (uint32_t)(tok[rb] * a.smask + 4 * g);
+  return w;
+}
+
 // Operands of one 32-key step: K tiles (A of S^T = K.Q^T), Vt tiles (A of
 // O^T = Vt.P^T) and, per row block, the 2 x 4 mask bytes of the lane's keys.
 template <int RBW>
@@ -213,45 +261,36 @@ struct StepBuf {
   uint32_t mk[RBW][2];
 };
 
-// Issue every load of the 32-key step at c.  Keys at or past c_end read a
-// valid slot and are zeroed / masked afterwards; a mask row holds at least
-// L_valid rounded up to 4 bytes, so 4-byte groups below c_end stay inside it.
 template <int DT, int RBW>
-SIMSD_DEV void attn_load(const AttnArgs& a, const char* kbase, const char* vbase, const uint8_t* const (&mrow)[RBW],
-                         int64_t c, int64_t c_end, int g, int r, StepBuf<RBW>& b) {
+SIMSD_DEV void attn_load(const AttnArgs& a, const WaveKV<RBW>& w, int c, StepBuf<RBW>& b) {
   constexpr int ES = DTypeInfo<DT>::kSize;
-  const int64_t last4 = (c_end - 1) & ~(int64_t)3;
+  const uint32_t kc = (uint32_t)c * w.k_step;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int64_t key = c + 16 * t + r;
-    const char* kp = kbase + (key < c_end ? key : c_end - 1) * a.skl * ES;
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int ds = 0; ds < kDSteps; ++ds) b.kf[t][ds] = load16_sel(kp + (ds * 32 + 8 * g) * ES, key < c_end);
-  }
+    for (int ds = 0; ds < kDSteps; ++ds) b.kf[t][ds] = buf_load16<kAuxKeep>(w.rk, kc + w.k_off[t] + ds * 32 * ES);
   // dim dt*16 + r, keys c + 4g .. +4 (k-slots 0..3) and c + 16 + 4g .. +4 (4..7)
 #pragma unroll
   for (int dt = 0; dt < kDTiles; ++dt) {
-    const char* vp = vbase + (int64_t)(dt * 16 + r) * a.svd * ES;
-    const u32x2_t lo = load_vt4<DT>(vp, c + 4 * g, c_end, last4);
-    const u32x2_t hi = load_vt4<DT>(vp, c + 16 + 4 * g, c_end, last4);
+    const u32x2_t lo = buf_load8(w.rv, w.v_off[dt] + (uint32_t)c * ES);
+    const u32x2_t hi = buf_load8(w.rv, w.v_off[dt] + (uint32_t)(c + 16) * ES);
     b.vf[dt] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
   }
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb)
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int64_t k4 = c + 16 * t + 4 * g;
-      b.mk[rb][t] = a.mask != nullptr ? *reinterpret_cast<const uint32_t*>(mrow[rb] + (k4 < last4 ? k4 : last4))
-                                      : 0x01010101u;
-    }
+    for (int t = 0; t < 2; ++t) b.mk[rb][t] = a.mask != nullptr ? buf_load4(w.rm, w.m_off[rb] + c + 16 * t) : ~0u;
 }
 
 // One 32-key step of the online softmax for RBW row blocks: S^T = K.Q^T,
-// mask and scale, running max / sum per row, O^T += Vt.P^T.
+// mask, running max / sum per row in the log2 domain (scores scaled by
+// scale * log2(e), p = 2^(s - m)), O^T += Vt.P^T.  The accumulators are
+// rescaled only when some row's maximum moved.
 template <int DT, int RBW>
 SIMSD_DEV void attn_step(const AttnArgs& a, const u32x4_t (&qf)[RBW][kDSteps], const bool (&row_ok)[RBW],
-                         const StepBuf<RBW>& b, int64_t c, int64_t c_end, int g, float (&m_run)[RBW],
+                         const StepBuf<RBW>& b, int c, int c_end, int g, float (&m_run)[RBW],
                          float (&l_run)[RBW], f32x4_t (&acc)[RBW][kDTiles]) {
+  const float sl2 = a.scale * kLog2e;
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) {
     f32x4_t s[2];
@@ -268,33 +307,35 @@ SIMSD_DEV void attn_step(const AttnArgs& a, const u32x4_t (&qf)[RBW][kDSteps], c
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int64_t key = c + 16 * t + 4 * g + j;
-        const bool vis = row_ok[rb] && key < c_end && ((b.mk[rb][t] >> (8 * j)) & 0xffu) != 0;
-        sv[t][j] = vis ? s[t][j] * a.scale : -INFINITY;
+        const bool vis = row_ok[rb] && c + 16 * t + 4 * g + j < c_end && ((b.mk[rb][t] >> (8 * j)) & 0xffu) != 0;
+        sv[t][j] = vis ? s[t][j] * sl2 : -INFINITY;
         mx = fmaxf(mx, sv[t][j]);
       }
     mx = across_groups(mx, [](float x, float y) { return fmaxf(x, y); });
     const float m_new = fmaxf(m_run[rb], mx);
-    const float alpha = m_new == -INFINITY ? 1.f : expf(m_run[rb] - m_new);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;   // no visible key yet: every p is 0
+    const float alpha = __builtin_amdgcn_exp2f(m_run[rb] - m_use);
     float p[2][4];
     float ps = 0.f;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        p[t][j] = sv[t][j] == -INFINITY ? 0.f : expf(sv[t][j] - m_new);
+        p[t][j] = __builtin_amdgcn_exp2f(sv[t][j] - m_use);
         ps += p[t][j];
       }
     ps = across_groups(ps, [](float x, float y) { return x + y; });
     l_run[rb] = l_run[rb] * alpha + ps;
+    const bool moved = m_run[rb] != -INFINITY && m_new != m_run[rb];
     m_run[rb] = m_new;
+    if (__any(moved)) {
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] *= alpha;
+    }
     const u32x4_t pf = u32x4_t{pack2<DT>(p[0][0], p[0][1]), pack2<DT>(p[0][2], p[0][3]),
                                pack2<DT>(p[1][0], p[1][1]), pack2<DT>(p[1][2], p[1][3])};
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) {
-      acc[rb][dt] *= alpha;
-      acc[rb][dt] = Mfma<DT>::step(b.vf[dt], pf, acc[rb][dt]);
-    }
+    for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = Mfma<DT>::step(b.vf[dt], pf, acc[rb][dt]);
   }
 }
 
@@ -351,24 +392,20 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const int64_t chunk_hi = min(lv, chunk_lo + a.chunk);
   const int64_t c_begin = KSPLIT ? min(chunk_hi, chunk_lo + (int64_t)wv * a.wave_chunk) : chunk_lo;
   const int64_t c_end = KSPLIT ? min(chunk_hi, c_begin + a.wave_chunk) : chunk_hi;
-  const char* kbase = a.kc + (int64_t)h * a.skh * ES;
-  const char* vbase = a.vt + (int64_t)h * a.svh * ES;
-
-  const uint8_t* mrow[RBW];
-#pragma unroll
-  for (int rb = 0; rb < RBW; ++rb) mrow[rb] = a.mask != nullptr ? a.mask + (int64_t)tok[rb] * a.smask : nullptr;
-  // the next step's loads are issued unconditionally (past c_end they read a
-  // valid slot and are zeroed), so no load sits under a branch
+  // the next step's loads are issued before this step's arithmetic; past
+  // c_end they read zeros (K) or finite stale slots (Vt) and meet p = 0
   StepBuf<RBW> bA, bB;
   if (c_begin < c_end) {
-    attn_load<DT, RBW>(a, kbase, vbase, mrow, c_begin, c_end, g, r, bA);
-    for (int64_t c = c_begin;; c += 2 * kKeyStep) {
-      attn_load<DT, RBW>(a, kbase, vbase, mrow, c + kKeyStep, c_end, g, r, bB);
-      attn_step<DT, RBW>(a, qf, row_ok, bA, c, c_end, g, m_run, l_run, acc);
-      if (c + kKeyStep >= c_end) break;
-      attn_load<DT, RBW>(a, kbase, vbase, mrow, c + 2 * kKeyStep, c_end, g, r, bA);
-      attn_step<DT, RBW>(a, qf, row_ok, bB, c + kKeyStep, c_end, g, m_run, l_run, acc);
-      if (c + 2 * kKeyStep >= c_end) break;
+    const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, c_end, tok, g, r);
+    const int ce = (int)c_end;
+    attn_load<DT, RBW>(a, w, (int)c_begin, bA);
+    for (int c = (int)c_begin;; c += 2 * kKeyStep) {
+      attn_load<DT, RBW>(a, w, c + kKeyStep, bB);
+      attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
+      if (c + kKeyStep >= ce) break;
+      attn_load<DT, RBW>(a, w, c + 2 * kKeyStep, bA);
+      attn_step<DT, RBW>(a, qf, row_ok, bB, c + kKeyStep, ce, g, m_run, l_run, acc);
+      if (c + 2 * kKeyStep >= ce) break;
     }
   }
 
@@ -394,7 +431,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       float o = 0.f, l = 0.f;
       for (int w = 0; w < nw; ++w) {
         const float2 ml = ml_sh[w][row];
-        const float wt = ml.x == -INFINITY ? 0.f : expf(ml.x - mx);
+        const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
         o += o_sh[w][row][d] * wt;
         l += ml.y * wt;
       }
@@ -413,6 +450,115 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
         *reinterpret_cast<f32x4_t*>(op + dt * 16 + 4 * g) = acc[rb][dt];
       if (g == 0) a.ml_part[base_row + row] = make_float2(m_run[rb], l_run[rb]);
     }
+  }
+}
+
+// Up to 32 query rows per KV head over a short context: one workgroup per
+// KV head, its 4 waves splitting the valid slots evenly; the four
+// online-softmax states merge in LDS (fixed wave order) and the normalised
+// rows go straight to the output -- one launch, no partials.
+constexpr int kHeadWaves = 4;
+// Each wave walks its slots with one step of loads in flight, so past two
+// 32-key steps per wave the chunked two-launch form, with every step's loads
+// in flight at once, wins.
+constexpr int kHeadMaxSlots = 256;
+
+template <int DT, int RBW>
+__global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnArgs a, char* __restrict__ out, int64_t so_m,
+                                                                    int64_t so_h) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int ROWS = RBW * 16;
+  constexpr int OSTR = kHeadDim + 4;   // padded rows: the b128 writes of 16 rows spread over the banks
+  __shared__ __attribute__((aligned(16))) float o_sh[kHeadWaves][ROWS][OSTR];
+  __shared__ float2 ml_sh[kHeadWaves][ROWS];
+  __shared__ float wt_sh[kHeadWaves][ROWS];
+  __shared__ float l_sh[ROWS];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int h = blockIdx.x;
+
+  u32x4_t qf[RBW][kDSteps];
+  int tok[RBW];
+  bool row_ok[RBW];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    const int row = rb * 16 + r;
+    row_ok[rb] = row < a.rows;
+    const int i = row_ok[rb] ? row / (int)a.M : 0;
+    tok[rb] = row_ok[rb] ? row % (int)a.M : 0;
+    const char* qp = a.q + ((int64_t)tok[rb] * a.sq_m + (int64_t)(h * a.n_rep + i) * a.sq_h) * ES;
+#pragma unroll
+    for (int ds = 0; ds < kDSteps; ++ds) qf[rb][ds] = load16_sel(qp + (ds * 32 + 8 * g) * ES, row_ok[rb]);
+  }
+  float m_run[RBW], l_run[RBW];
+  f32x4_t acc[RBW][kDTiles];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  int64_t lv = a.L_valid;
+  if (a.lv_dev != nullptr) {
+    const int64_t d = *a.lv_dev;
+    lv = d < 0 ? 0 : (d < lv ? d : lv);
+  }
+  const int64_t wc = ((lv + kHeadWaves - 1) / kHeadWaves + kKeyStep - 1) / kKeyStep * kKeyStep;
+  const int64_t c_begin = min(lv, (int64_t)wv * wc);
+  const int64_t c_end = min(lv, c_begin + wc);
+  // the next step's loads are issued before this step's arithmetic; past
+  // c_end they read zeros (K) or finite stale slots (Vt) and meet p = 0
+  StepBuf<RBW> bA, bB;
+  if (c_begin < c_end) {
+    const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, c_end, tok, g, r);
+    const int ce = (int)c_end;
+    attn_load<DT, RBW>(a, w, (int)c_begin, bA);
+    for (int c = (int)c_begin;; c += 2 * kKeyStep) {
+      attn_load<DT, RBW>(a, w, c + kKeyStep, bB);
+      attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
+      if (c + kKeyStep >= ce) break;
+      attn_load<DT, RBW>(a, w, c + 2 * kKeyStep, bA);
+      attn_step<DT, RBW>(a, qf, row_ok, bB, c + kKeyStep, ce, g, m_run, l_run, acc);
+      if (c + 2 * kKeyStep >= ce) break;
+    }
+  }
+  // lane (g, r): acc[rb][dt][j] = O^T[dim dt*16 + 4g + j][row rb*16 + r]
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt)
+      *reinterpret_cast<f32x4_t*>(&o_sh[wv][rb * 16 + r][dt * 16 + 4 * g]) = acc[rb][dt];
+    if (g == 0) ml_sh[wv][rb * 16 + r] = make_float2(m_run[rb], l_run[rb]);
+  }
+  __syncthreads();
+  if (threadIdx.x < ROWS) {
+    const int row = threadIdx.x;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kHeadWaves; ++w) mx = fmaxf(mx, ml_sh[w][row].x);
+    float l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kHeadWaves; ++w) {
+      const float2 ml = ml_sh[w][row];
+      const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+      wt_sh[w][row] = wt;
+      l += ml.y * wt;
+    }
+    l_sh[row] = l;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * kHeadWaves) {
+    const int row = e / kHeadDim, d = e % kHeadDim;
+    if (row >= a.rows) break;
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kHeadWaves; ++w) o += o_sh[w][row][d] * wt_sh[w][row];
+    const float l = l_sh[row];
+    const int i = row / (int)a.M;
+    const int64_t m = row % (int)a.M;
+    store_elem<DT>(out, m * so_m + (int64_t)(h * a.n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
   }
 }
 
@@ -453,7 +599,7 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __r
   float l = 0.f;
   for (int c = d; c < n_chunks; c += kHeadDim) {
     const float mc = w_sh[c];
-    const float wt = (mx == -INFINITY || mc == -INFINITY) ? 0.f : expf(mc - mx);
+    const float wt = (mx == -INFINITY || mc == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mc - mx);
     w_sh[c] = wt;
     l += ml_part[base + (int64_t)c * rows_pad + row].y * wt;
   }
@@ -553,7 +699,7 @@ __global__ __launch_bounds__(256) void block_mask_kernel(uint8_t* __restrict__ m
 
 struct AttnPlan {
   int rows, rows_pad, rb, rbw, waves, groups, n_chunks;
-  bool ksplit;
+  bool ksplit, head;
   int64_t chunk, wave_chunk;
   int64_t o_bytes, ml_bytes, bytes;
 };
@@ -596,9 +742,10 @@ AttnPlan attn_plan(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
     p.wave_chunk = chunk;
   }
   p.n_chunks = (int)((L + p.chunk - 1) / p.chunk);
+  p.head = p.ksplit && L <= kHeadMaxSlots;   // one launch, no partials
   p.o_bytes = up256(Hkv * (int64_t)p.n_chunks * p.rows_pad * kHeadDim * 4);
   p.ml_bytes = up256(Hkv * (int64_t)p.n_chunks * p.rows_pad * 8);
-  p.bytes = p.o_bytes + p.ml_bytes;
+  p.bytes = p.head ? 0 : p.o_bytes + p.ml_bytes;
   return p;
 }
 
@@ -670,7 +817,7 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
     return set_error("block_attention: q/K need 16-byte aligned rows and Vt 8-byte aligned rows of >= L_cap slots");
   if (mask != nullptr && (!al(mask, 4) || smask % 4 != 0 || smask < (L_valid + 3) / 4 * 4))
     return set_error("block_attention: mask rows must be 4-byte aligned with at least L_valid rounded up to 4 bytes");
-  if (workspace == nullptr || workspace_bytes < pl.bytes || !al(workspace, 16))
+  if (pl.bytes > 0 && (workspace == nullptr || workspace_bytes < pl.bytes || !al(workspace, 16)))
     return set_error("block_attention: needs a 16-byte aligned workspace of %lld bytes (got %lld)", (long long)pl.bytes,
                      (long long)workspace_bytes);
   AttnArgs a{};
@@ -689,6 +836,14 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
   const dim3 grid((unsigned)pl.n_chunks, (unsigned)Hkv, (unsigned)pl.groups), block(64 * pl.waves);
   auto partial = [&](auto dt_tag) {
     constexpr int DT = decltype(dt_tag)::value;
+    if (pl.head) {
+      char* o = static_cast<char*>(out);
+      if (pl.rbw == 2)
+        hipLaunchKernelGGL((attn_head_kernel<DT, 2>), dim3((unsigned)Hkv), dim3(64 * kHeadWaves), 0, st, a, o, so_m, so_h);
+      else
+        hipLaunchKernelGGL((attn_head_kernel<DT, 1>), dim3((unsigned)Hkv), dim3(64 * kHeadWaves), 0, st, a, o, so_m, so_h);
+      return;
+    }
     if (pl.ksplit) {
       if (pl.rbw == 2) hipLaunchKernelGGL((attn_partial_kernel<DT, 2, true>), grid, block, 0, st, a);
       else hipLaunchKernelGGL((attn_partial_kernel<DT, 1, true>), grid, block, 0, st, a);

@@ -43,6 +43,8 @@ struct ThinArgs {
   int64_t sw2n;
   const char* gamma;         // RMSNorm prologue: weight [K] (contiguous), epsilon
   float eps;
+  const char* res;           // residual added to the rounded output (nullable), strides srm, srn
+  int64_t srm, srn;
   int64_t M, N, K;           // gated: N = output columns (rows of each of w, w2)
   int steps;                 // ceil(K * esize / 64)
   int steps_per_split;
@@ -134,6 +136,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
               a.part[((int64_t)split_id * a.M + m) * a.N + n] = v;
             } else {
               if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+              if (a.res != nullptr) v = round_to<DT>(v) + load_elem<DT>(a.res, m * a.srm + n * a.srn);
               store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
             }
           }
@@ -174,6 +177,8 @@ SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, fl
     store_elem<DT>(a.y, m * a.sym + n * a.syn, silu_mul<DT>(v, u));
   } else {
     if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+    // residual: the projection rounded to the dtype, then the dtype add
+    if (a.res != nullptr) v = round_to<DT>(v) + load_elem<DT>(a.res, m * a.srm + n * a.srn);
     store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
   }
 }
@@ -503,7 +508,8 @@ template <int DT>
 __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restrict__ part, int split,
                                                           int64_t M, int64_t N,
                                                           const char* bias, int64_t sb, char* y,
-                                                          int64_t sym, int64_t syn, int glu) {
+                                                          int64_t sym, int64_t syn, int glu, const char* res,
+                                                          int64_t srm, int64_t srn) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= M * N) return;
   const int64_t m = e / N, n = e % N;
@@ -520,6 +526,7 @@ __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restric
   float v = 0.f;
   for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + e];
   if (bias != nullptr) v += load_elem<DT>(bias, n * sb);
+  if (res != nullptr) v = round_to<DT>(v) + load_elem<DT>(res, m * srm + n * srn);
   store_elem<DT>(y, m * sym + n * syn, v);
 }
 
@@ -766,7 +773,7 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
     const int64_t total = args.M * args.N;
     hipLaunchKernelGGL((thin_reduce_kernel<DT>), dim3((unsigned)cdiv(total, 256)), dim3(256), 0,
                        stream, args.part, pl.split, args.M, args.N, args.bias, args.sb, args.y,
-                       args.sym, args.syn, pl.glu ? 1 : 0);
+                       args.sym, args.syn, pl.glu ? 1 : 0, args.res, args.srm, args.srn);
   }
 }
 
@@ -981,7 +988,9 @@ extern "C" int simsd_rmsnorm_thin_linear(const void* x, int64_t sxm, int64_t sxk
   args.bias = static_cast<const char*>(bias); args.sb = sb;
   args.y = static_cast<char*>(y); args.sym = sym; args.syn = syn;
   args.M = M; args.N = N; args.K = K;
-  if (pl.fast && pl.kind == 1 && aligned16(gamma)) {   // the norm runs inside the GEMV
+  // the norm runs inside the GEMV up to 4 tokens; beyond that, each
+  // workgroup's statistics pass over all rows costs more than a launch
+  if (pl.fast && pl.kind == 1 && pl.ms == 1 && aligned16(gamma)) {
     pl.norm = true;
     args.x = static_cast<const char*>(x); args.sxm = sxm;
     args.gamma = static_cast<const char*>(gamma); args.eps = eps;
@@ -1032,7 +1041,7 @@ extern "C" int simsd_rmsnorm_thin_linear_silu_mul(const void* x, int64_t sxm, in
   args.w2 = static_cast<const char*>(w_up); args.sw2n = sun;
   args.y = static_cast<char*>(h); args.sym = shm; args.syn = shn;
   args.M = M; args.N = I; args.K = K;
-  if (pl.fast && pl.kind == 1 && aligned16(gamma)) {
+  if (pl.fast && pl.kind == 1 && pl.ms == 1 && aligned16(gamma)) {
     pl.norm = true;
     args.x = static_cast<const char*>(x); args.sxm = sxm;
     args.gamma = static_cast<const char*>(gamma); args.eps = eps;
@@ -1052,4 +1061,32 @@ extern "C" int simsd_rmsnorm_thin_linear_silu_mul(const void* x, int64_t sxm, in
   args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
   return run_planned(pl, args, dtype, xn + xn_bytes, workspace_bytes - xn_bytes, stream,
                      "rmsnorm_thin_linear_silu_mul");
+}
+
+extern "C" int simsd_thin_linear_residual(const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn,
+                                          int64_t swk, const void* residual, int64_t srm, int64_t srn, void* y,
+                                          int64_t sym, int64_t syn, int64_t M, int64_t N, int64_t K, int dtype,
+                                          int block_n, int block_k, int split_k, int num_waves, void* workspace,
+                                          int64_t workspace_bytes, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
+    return set_error("thin_linear_residual: unsupported dtype code %d", dtype);
+  if (M < 0 || N < 0 || K < 0) return set_error("thin_linear_residual: negative size");
+  if (M == 0 || N == 0) return 0;
+  if (K == 0) return set_error("thin_linear_residual: K == 0 must be handled by the caller");
+  if (x == nullptr || w == nullptr || y == nullptr || residual == nullptr)
+    return set_error("thin_linear_residual: null pointer");
+  if (K * (int64_t)esize_of(dtype) > ((int64_t)1 << 31) - 64)
+    return set_error("thin_linear_residual: K=%lld too large", (long long)K);
+  ThinPlan pl{};
+  if (make_plan(pl, x, sxm, sxk, w, swn, swk, M, N, K, dtype, block_n, block_k, split_k, num_waves) != 0)
+    return -1;
+  ThinArgs args{};
+  args.x = static_cast<const char*>(x); args.sxm = sxm; args.sxk = sxk;
+  args.w = static_cast<const char*>(w); args.swn = swn; args.swk = swk;
+  args.y = static_cast<char*>(y); args.sym = sym; args.syn = syn;
+  args.res = static_cast<const char*>(residual); args.srm = srm; args.srn = srn;
+  args.M = M; args.N = N; args.K = K;
+  args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
+  return run_planned(pl, args, dtype, workspace, workspace_bytes, stream, "thin_linear_residual");
 }

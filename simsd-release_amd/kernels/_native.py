@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -36,6 +36,8 @@ SIGNATURES = {
     "simsd_thin_linear_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                           _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                                           _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
+    "simsd_thin_linear_residual": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
+                                          _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
     "simsd_rmsnorm": (_i32, [_vp, _i64, _vp, _f32, _vp, _i64, _i64, _i64, _i32, _vp]),
     "simsd_rmsnorm_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32, _i32]),
     "simsd_rmsnorm_thin_linear": (_i32, [_vp, _i64, _i64, _vp, _f32, _vp, _i64, _i64, _vp, _i64,

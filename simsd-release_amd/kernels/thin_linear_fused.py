@@ -8,8 +8,10 @@ argument meaning and the same exceptions.  The arithmetic runs in a
 hand-written gfx950 HIP kernel (``libsimsd_kernels.so``, C ABI in
 ``include/simsd_kernels.h``) instead of Triton.  Added on top:
 ``thin_linear_silu_mul``, an MLP's gate and up projections with the SiLU and
-product in the same kernel; ``thin_rmsnorm`` (one launch) and the RMSNorm
-prologue forms ``thin_rmsnorm_linear`` / ``thin_rmsnorm_linear_silu_mul``.
+product in the same kernel; ``thin_linear_residual``, a projection with the
+decoder layer's residual add in its epilogue; ``thin_rmsnorm`` (one launch)
+and the RMSNorm prologue forms ``thin_rmsnorm_linear`` /
+``thin_rmsnorm_linear_silu_mul``.
 
 How the MI355X kernels work (``csrc/thin_gemm.hip``)
 -----------------------------------------------------
@@ -378,6 +380,54 @@ def _launch_config(M: int, N_rows: int, K: int, itemsize: int, config, num_warps
     if split_k < 1:
         raise ValueError(f"SPLIT_K must be >= 1, got {split_k}")
     return _rows_for(block_n), block_k, split_k, (2 if waves <= 2 else (4 if waves <= 4 else 8))
+
+
+def thin_linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor,
+                         out: torch.Tensor | None = None, config=None, num_warps=None) -> torch.Tensor:
+    """``residual + thin_linear(x, w)`` in one launch (the decoder layer's
+    ``hidden = residual + proj(...)``): the projection is rounded to the dtype,
+    then added in the dtype, as PyTorch computes the two ops.  ``out`` may be
+    ``residual`` itself (in place).  x: [M, K], w: [N, K], residual: [M, N]."""
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad or residual.requires_grad):
+        raise RuntimeError("thin_linear_residual is a forward-only inference kernel; "
+                           "call it under torch.no_grad() / torch.inference_mode()")
+    if x.dtype != w.dtype or residual.dtype != x.dtype:
+        raise TypeError(f"dtype mismatch: x={x.dtype} w={w.dtype} residual={residual.dtype}")
+    code = _native.DTYPE_CODES.get(x.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {x.dtype} (bf16, fp16 or fp32)")
+    if x.ndim != 2 or w.ndim != 2 or w.shape[1] != x.shape[1]:
+        raise ValueError(f"shapes: x {tuple(x.shape)}, w {tuple(w.shape)}")
+    M, K = x.shape
+    N = w.shape[0]
+    if residual.shape != (M, N):
+        raise ValueError(f"residual must be [{M}, {N}], got {tuple(residual.shape)}")
+    dev = _native.require_device(x, w, residual, out)
+    y = torch.empty((M, N), device=dev, dtype=x.dtype) if out is None else out
+    if y.shape != (M, N) or y.dtype != x.dtype:
+        raise ValueError(f"out must be [{M}, {N}] in {x.dtype}")
+    if M == 0 or N == 0:
+        return y
+    if K == 0:
+        y.copy_(residual)
+        return y
+    block_n, block_k, split_k, waves = _launch_config(M, N, K, x.element_size(), config, num_warps)
+    lib = _native.lib()
+    ws, ws_bytes = None, 0
+    if split_k > 1:
+        need = lib.simsd_thin_linear_workspace_bytes(M, N, K, code, block_n, split_k, waves)
+        if need < 0:
+            _native.check(-1, "thin_linear_residual")
+        ws = _partials(dev, need)
+        ws_bytes = ws.numel()
+    with _native.device_guard(dev):
+        status = lib.simsd_thin_linear_residual(
+            x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), w.stride(0), w.stride(1),
+            residual.data_ptr(), residual.stride(0), residual.stride(1),
+            y.data_ptr(), y.stride(0), y.stride(1), M, N, K, code, block_n, block_k, split_k, waves,
+            ws.data_ptr() if ws is not None else None, ws_bytes, _native.stream_of(dev))
+    _native.check(status, "thin_linear_residual")
+    return y
 
 
 def _norm_args(x: torch.Tensor, weight: torch.Tensor):

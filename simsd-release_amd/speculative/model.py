@@ -8,9 +8,9 @@ of the real shapes (no checkpoint is available offline).  Each layer runs as
     qkv = rmsnorm + merged q/k/v projection       (thin_rmsnorm_linear)
     q   = q/k norm + RoPE + K/V cache write        (qkv_rope_cache)
     a   = attention over the static cache          (block_attention)
-    h  += o_proj(a)                                (thin_linear)
+    h  += o_proj(a)                                (thin_linear_residual)
     g   = rmsnorm + gate/up projection + SiLU.mul  (thin_rmsnorm_linear_silu_mul)
-    h  += down_proj(g)                             (thin_linear)
+    h  += down_proj(g)                             (thin_linear_residual)
 
 and the head is rmsnorm + lm_head (thin_rmsnorm, thin_linear).  A forward
 takes its rows' token ids, RoPE positions, cache slots and mask rows, all as
@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from kernels.attention_fused import BlockKVCache, block_attention, default_inv_freq, qkv_rope_cache, rope_tables
-from kernels.thin_linear_fused import (thin_linear, thin_rmsnorm, thin_rmsnorm_linear,
+from kernels.thin_linear_fused import (thin_linear, thin_linear_residual, thin_rmsnorm, thin_rmsnorm_linear,
                                        thin_rmsnorm_linear_silu_mul)
 
 
@@ -98,9 +98,9 @@ class SynthModel:
             qkv = thin_rmsnorm_linear(h, L.ln1, s.eps, L.wqkv)
             q = qkv_rope_cache(qkv, s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin, pos, slots, self.cache, li)
             a = block_attention(q, self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
-            h = h + thin_linear(a, L.wo)
+            h = thin_linear_residual(a, L.wo, h)
             g = thin_rmsnorm_linear_silu_mul(h, L.ln2, s.eps, L.wgu[:I], L.wgu[I:])
-            h = h + thin_linear(g, L.wd)
+            h = thin_linear_residual(g, L.wd, h)
         if not head:
             return None
         if head_rows is not None:

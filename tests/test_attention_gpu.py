@@ -2,6 +2,10 @@
 (one launch) and the block attention over the static cache, against the
 oracle on the same inputs and against the reference's own torch sequence.
 
+Both attention forms are covered: up to 32 query rows per KV head over at
+most 256 slots run as one launch (a workgroup per KV head), the rest as
+chunked partials and their merge.
+
 qkv_rope_cache: q rows and every cache slot written equal the oracle within
 one bf16 unit in the last place (the RMSNorm statistic may round either way;
 more than 99% of values are bit-equal), and slots not addressed stay
@@ -50,7 +54,8 @@ def fill_cache(cache, layer, L, seed, dtype=torch.bfloat16):
 
 @pytest.mark.parametrize("M,Hq,Hkv,L_valid,L_total", [(4, 16, 8, 1000, 1004), (32, 32, 8, 1024, 1056),
                                                       (8, 8, 8, 37, 64), (3, 12, 3, 301, 320),
-                                                      (64, 32, 8, 530, 600), (1, 16, 8, 1, 32)])
+                                                      (64, 32, 8, 530, 600), (1, 16, 8, 1, 32),
+                                                      (8, 32, 8, 250, 288), (16, 16, 8, 256, 288)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_block_attention_vs_oracle(M, Hq, Hkv, L_valid, L_total, masked):
     from kernels.attention_fused import BlockKVCache, block_attention

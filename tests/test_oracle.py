@@ -338,3 +338,24 @@ def test_planted_mistakes_are_caught(golden, monkeypatch):
     pad_end = np.cumsum((np.bincount(flat, minlength=256) + 15) // 16 * 16)
     left = np.searchsorted(pad_end, np.arange(int(a["c2_n_tiles"])) * 16, side="left")
     assert not np.array_equal(left, a["c2_tile_expert"])
+
+
+def test_linear_residual_exact_vs_torch_cpu():
+    """residual + F.linear in bf16 on the CPU equals the oracle on exact
+    (small-integer) products; a slip that skips the projection's rounding
+    fails."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randint(-3, 4, (8, 512), generator=g).bfloat16()
+    w = torch.randint(-3, 4, (96, 512), generator=g).bfloat16()
+    r = (torch.randn(8, 96, generator=g) * 300).bfloat16()
+    ref = (r + F.linear(x, w)).float().numpy()
+    got = othin.linear_residual_exact(x.float().numpy(), w.float().numpy(), r.float().numpy())
+    assert np.array_equal(got, ref)
+    xf, wf, rf = (t.float().numpy().astype(np.float64) for t in (x, w, r))
+    one_round = round_bf16(xf @ wf.T + rf)
+    x2 = (torch.randn(8, 512, generator=g) * 2).bfloat16()
+    ref2 = (r + F.linear(x2, w)).float().numpy()
+    got2 = othin.linear_residual_exact(x2.float().numpy(), w.float().numpy(), r.float().numpy())
+    slip2 = round_bf16(x2.float().numpy().astype(np.float64) @ wf.T + rf)
+    assert np.abs(got2 - ref2).max() <= 2 ** -7 * np.abs(ref2).max()
+    assert not np.array_equal(slip2, got2) or not np.array_equal(one_round, got)

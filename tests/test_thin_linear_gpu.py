@@ -555,3 +555,33 @@ def test_properties_at_full_size():
             wt = torch.empty(N, K + 64, device=DEV, dtype=w.dtype)
             wt[:, 32:32 + K] = w
             assert torch.equal(thin_linear(x, wt[:, 32:32 + K]), y)           # strided view
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_linear_residual_vs_oracle(M, dtype):
+    """residual + x w^T in one launch: bit-exact on small-integer data (every
+    sum exact), within the reference bound on random data; in place; split K."""
+    from kernels.thin_linear_fused import thin_linear, thin_linear_residual
+    name = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    g = torch.Generator().manual_seed(M)
+    K, N = 2048, 4096
+    xi = torch.randint(-3, 4, (M, K), generator=g).to(dtype)
+    wi = torch.randint(-3, 4, (N, K), generator=g).to(dtype)
+    r = (torch.randn(M, N, generator=g) * 100).to(dtype)
+    want = othin.linear_residual_exact(xi.float().numpy(), wi.float().numpy(), r.float().numpy(), dtype=name)
+    with torch.inference_mode():
+        got = thin_linear_residual(xi.to(DEV), wi.to(DEV), r.to(DEV))
+    assert np.array_equal(got.float().cpu().numpy(), want)
+    x = rnd(M, K, dtype=dtype, seed=M + 1)
+    w = rnd(N, K, dtype=dtype, scale=0.02, seed=M + 2)
+    res = rnd(M, N, dtype=dtype, seed=M + 3)
+    with torch.inference_mode():
+        ref = res + thin_linear(x, w)
+        got = thin_linear_residual(x, w, res)
+        assert torch.equal(got, ref)                          # the same rounding points as the two ops
+        split = thin_linear_residual(x, w, res, config=(16, 16, 256, 4))
+        assert float((split.float() - ref.float()).abs().max()) <= tol(ref)
+        inplace = res.clone()
+        thin_linear_residual(x, w, inplace, out=inplace)
+        assert torch.equal(inplace, got)
