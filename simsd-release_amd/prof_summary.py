@@ -30,7 +30,7 @@ from collections import defaultdict
 
 def short_name(name: str) -> str:
     """Kernel name without 'void ', the namespace and the argument list."""
-    name = name.strip().strip('"')
+    name = name.strip().strip('"').replace("(anonymous namespace)::", "")
     if name.startswith("void "):
         name = name[5:]
     depth, cut = 0, len(name)
