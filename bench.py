@@ -614,7 +614,8 @@ def run_c5(args, torch, dev):
     a 512-token prompt uniform over the vocabulary, 4-token blocks denoised in
     4 steps, K = 4 blocks verified per target forward (32 rows), greedy
     acceptance, committed blocks written to the target cache by an extend
-    forward.  value = generated tokens / second over the timed iterations."""
+    forward on a second stream (overlapping the next iteration's draft).
+    value = generated tokens / second over the timed iterations."""
     import time as _time
 
     from speculative.model import DRAFT_1P7B, TARGET_8B, SynthModel
@@ -646,9 +647,18 @@ def run_c5(args, torch, dev):
         ev[4].synchronize()
         for i in range(4):
             phase[i] += ev[i].elapsed_time(ev[i + 1])
+    runner.finish()
     torch.cuda.synchronize()
     secs = _time.perf_counter() - t0
     it_ms = secs * 1e3 / steps
+    # the same iterations with the extend in line (no second stream), for comparison
+    runner.overlap = False
+    n_serial = max(4, steps // 2)
+    t1 = _time.perf_counter()
+    for _ in range(n_serial):
+        runner.step()
+    torch.cuda.synchronize()
+    serial_ms = (_time.perf_counter() - t1) * 1e3 / n_serial
 
     def layer_bytes(sh):
         H, D, I = sh.hidden, sh.head_dim, sh.intermediate
@@ -665,7 +675,7 @@ def run_c5(args, torch, dev):
         "steps": steps, "warmup": warm, "ms_per_step": round(it_ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (random-init weights, uniform random prompt)",
-        "config": {"workload": "spec-step-SDAR1.7B-draft-SDAR8B-target-bl4-ds4-K4-greedy",
+        "config": {"workload": "spec-step-SDAR1.7B-draft-SDAR8B-target-bl4-ds4-K4-greedy-2stream",
                    "prompt": 512, "block_length": 4, "denoise_steps": 4, "k_blocks": 4,
                    "draft_forwards_per_iteration": d_fwds, "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -676,7 +686,10 @@ def run_c5(args, torch, dev):
         "accepted_draft_tokens_per_iteration": round(n_acc / steps, 3),
         "committed_blocks_per_iteration": round(n_blocks / steps, 3),
         "phase_ms_per_iteration": {"draft": round(phase[0] / steps, 3), "verify": round(phase[1] / steps, 3),
-                                   "accept_host": round(phase[2] / steps, 3), "extend": round(phase[3] / steps, 3)},
+                                   "accept_host": round(phase[2] / steps, 3),
+                                   "extend_issue": round(phase[3] / steps, 3)},
+        "extend_on_second_stream": True,
+        "ms_per_iteration_extend_in_line": round(serial_ms, 3),
         "hbm_bound_ms_per_iteration": round(it_bytes / 8e12 * 1e3, 3),
         "init_s": round(init_s, 1),
         "cpu_baseline": None,

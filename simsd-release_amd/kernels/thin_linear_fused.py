@@ -103,6 +103,14 @@ def _partials(dev: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+def _scratch(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """A call's own scratch (the normalised rows of the RMSNorm + linear forms,
+    plus their split-K partials), from the caching allocator: nothing is shared
+    between calls, so graphs captured at different sizes and calls on two
+    streams stay independent."""
+    return torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
+
+
 def reset_workspace() -> None:
     """Drop the staging buffers (call before re-capturing graphs in a new pool)."""
     _PARTIALS.clear()
@@ -484,7 +492,7 @@ def thin_rmsnorm_linear(x: torch.Tensor, weight: torch.Tensor, eps: float, w: to
     need = lib.simsd_rmsnorm_linear_workspace_bytes(M, N, K, code, block_n, split_k, waves)
     if need < 0:
         _native.check(-1, "rmsnorm_thin_linear")
-    ws = _partials(dev, need)
+    ws = _scratch(dev, need)
     y = torch.empty((M, N), device=dev, dtype=x.dtype)
     with _native.device_guard(dev):
         st = lib.simsd_rmsnorm_thin_linear(
@@ -525,7 +533,7 @@ def thin_rmsnorm_linear_silu_mul(x: torch.Tensor, weight: torch.Tensor, eps: flo
     need = lib.simsd_rmsnorm_linear_workspace_bytes(M, 2 * I, K, code, block_n, split_k, waves)
     if need < 0:
         _native.check(-1, "rmsnorm_thin_linear_silu_mul")
-    ws = _partials(dev, need)
+    ws = _scratch(dev, need)
     h = torch.empty((M, I), device=dev, dtype=x.dtype)
     with _native.device_guard(dev):
         st = lib.simsd_rmsnorm_thin_linear_silu_mul(

@@ -8,15 +8,19 @@ with the target's verify run against its KV cache: its rows are only the K
 draft blocks (data, mask), not the whole prompt.  Per iteration:
 
   draft   K block graphs; each folds the previous block in as a committed
-          prefix (its K/V rewritten in place) and runs ds denoise forwards of
-          [prefix 4 | block 4] rows, each unmasking ceil(remaining / steps
-          left) positions by confidence (denoise_select)
+          prefix (its K/V rewritten in place by the first of ds denoise
+          forwards, [prefix 4 | block 4] rows; the rest run the block's 4
+          rows), each unmasking ceil(remaining / steps left) positions by
+          confidence (denoise_select)
   verify  one target forward of the K x (4 data + 4 mask) rows; mask rows'
           argmax (softmax_argmax)
   accept  greedy match per block with first-reject truncation; a rejected
           block is committed padded with the draft's own tokens
           (partial_block_fill = "draft_argmax")
-  extend  one target forward of the committed block(s), storing their K/V.
+  extend  one target forward of the committed block(s), storing their K/V,
+          on a second HIP stream: it overlaps the next iteration's draft
+          blocks, which only need the committed ids; the next verify waits
+          for it (an event).  ``overlap=False`` runs it in line.
 
 The committed context lives in permanent cache slots [0, ctx); a forward's
 rows write their K/V at slots ctx.. in row order (past the committed context,
@@ -88,7 +92,7 @@ class SpecRunner:
     resident on one GPU."""
 
     def __init__(self, draft: SynthModel, target: SynthModel, block_length: int = 4, denoise_steps: int = 4,
-                 k_blocks: int = 4, mask_token_id: int = MASK_TOKEN_ID):
+                 k_blocks: int = 4, mask_token_id: int = MASK_TOKEN_ID, overlap: bool = True):
         self.draft, self.target = draft, target
         self.bl, self.ds, self.K = block_length, denoise_steps, k_blocks
         self.mask_id = mask_token_id
@@ -102,6 +106,9 @@ class SpecRunner:
         self._step_map = torch.full((bl,), -1, dtype=torch.int64, device=self.dev)
         self.draft_blocks = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
         self.step_maps = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
+        self.overlap = overlap
+        self.side = torch.cuda.Stream(device=self.dev)      # default priority
+        self._extend_done = None
         self.ctx = 0
         self.tokens = []          # generated tokens (accepted + bonus)
         self.history = []         # the committed context: prompt + committed blocks
@@ -128,12 +135,20 @@ class SpecRunner:
 
     # ------------------------------------------------------------ graphs
     def _draft_body(self):
+        """ds denoise forwards of one block.  The first carries the prefix
+        rows, which writes their K/V; the later ones run the block's rows
+        alone, reading the prefix from the cache (the reference re-encodes the
+        prefix in every step, cache_aware.py:851-861, which is idempotent)."""
         g, bl = self._dg, self.bl
         g.ids[bl:].fill_(self.mask_id)
         self._step_map.fill_(-1)
         for step, n_u in enumerate(self.schedule):
-            logits = self.draft.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.draft.cache.full_len,
-                                        valid_len_dev=g.valid, head_rows=slice(bl, 2 * bl))
+            if step == 0:
+                logits = self.draft.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.draft.cache.full_len,
+                                            valid_len_dev=g.valid, head_rows=slice(bl, 2 * bl))
+            else:
+                logits = self.draft.forward(g.ids[bl:], g.pos[bl:], g.slots[bl:], g.mask[bl:],
+                                            valid_len=self.draft.cache.full_len, valid_len_dev=g.valid)
             denoise_select(logits, g.ids[bl:], self.mask_id, n_u, step, self._step_map)
         return None
 
@@ -180,6 +195,9 @@ class SpecRunner:
 
     @torch.inference_mode()
     def verify_(self):
+        if self._extend_done is not None:            # the target cache must hold the last commit
+            torch.cuda.current_stream().wait_event(self._extend_done)
+            self._extend_done = None
         g, bl, K = self._vg, self.bl, self.K
         ids = g.ids.view(K, 2, bl)
         ids[:, 0].copy_(self.draft_blocks)
@@ -198,10 +216,25 @@ class SpecRunner:
     def extend_(self, blocks):
         n = len(blocks)
         g = self._extend_graph(n)
-        g.ids.copy_(torch.tensor([t for b in blocks for t in b], dtype=torch.int64).to(self.dev, non_blocking=True))
-        g.set_span(self.ctx, self.ctx, n * self.bl)
-        block_mask(self.target.cache.full_len, self.ctx, self.ctx, n_prefix=n * self.bl, out=g.mask)
-        g.replay()
+        ids = torch.tensor([t for b in blocks for t in b], dtype=torch.int64)
+        main = torch.cuda.current_stream()
+        stream = self.side if self.overlap else main
+        if self.overlap:
+            stream.wait_stream(main)                  # after the verify that wrote its rows
+        with torch.cuda.stream(stream):
+            g.ids.copy_(ids.to(self.dev, non_blocking=True))
+            g.set_span(self.ctx, self.ctx, n * self.bl)
+            block_mask(self.target.cache.full_len, self.ctx, self.ctx, n_prefix=n * self.bl, out=g.mask)
+            g.replay()
+            if self.overlap:
+                self._extend_done = torch.cuda.Event()
+                self._extend_done.record(stream)
+
+    def finish(self):
+        """Wait for an extend still running on the side stream."""
+        if self._extend_done is not None:
+            torch.cuda.current_stream().wait_event(self._extend_done)
+            self._extend_done = None
 
     @torch.inference_mode()
     def step(self, events=None):
