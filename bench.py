@@ -622,7 +622,7 @@ def run_c5(args, torch, dev):
     from speculative.step import SpecRunner
 
     steps, warm = args.steps, max(2, args.warmup)
-    max_ctx = 512 + 16 * (steps + warm) + 64
+    max_ctx = 512 + 16 * (steps + warm + 2 * max(4, steps // 2)) + 64
     t_init = _time.perf_counter()
     draft = SynthModel(DRAFT_1P7B, dev, seed=11, max_ctx=max_ctx, max_rows=64)
     target = SynthModel(TARGET_8B, dev, seed=12, max_ctx=max_ctx, max_rows=64)
@@ -659,6 +659,14 @@ def run_c5(args, torch, dev):
         runner.step()
     torch.cuda.synchronize()
     serial_ms = (_time.perf_counter() - t1) * 1e3 / n_serial
+    # and with the optimistic pipelined mode (next drafts beside the verify)
+    runner.overlap, runner.pipelined = True, True
+    t2 = _time.perf_counter()
+    for _ in range(n_serial):
+        runner.step()
+    runner.finish()
+    torch.cuda.synchronize()
+    pipe_ms = (_time.perf_counter() - t2) * 1e3 / n_serial
 
     def layer_bytes(sh):
         H, D, I = sh.hidden, sh.head_dim, sh.intermediate
@@ -690,6 +698,8 @@ def run_c5(args, torch, dev):
                                    "extend_issue": round(phase[3] / steps, 3)},
         "extend_on_second_stream": True,
         "ms_per_iteration_extend_in_line": round(serial_ms, 3),
+        "ms_per_iteration_pipelined": round(pipe_ms, 3),
+        "pipelined_optimistic_drafts": dict(runner.stats),
         "hbm_bound_ms_per_iteration": round(it_bytes / 8e12 * 1e3, 3),
         "init_s": round(init_s, 1),
         "cpu_baseline": None,

@@ -22,6 +22,16 @@ draft blocks (data, mask), not the whole prompt.  Per iteration:
           blocks, which only need the committed ids; the next verify waits
           for it (an event).  ``overlap=False`` runs it in line.
 
+``pipelined=True`` adds the reference's optimistic execution
+(cache_aware.py:2169-2668, speculative_generate_with_kv_cache_pipelined, there
+across two GPUs with K = 1; here on two streams of one GPU, any K): while the
+target verifies iteration N on the main stream, the draft already denoises
+iteration N + 1's blocks on a side stream as if every block of N were
+accepted.  On full acceptance those drafts are used as they are; otherwise
+they are dropped (rollback: the context is what acceptance committed, and the
+slots the optimistic drafts wrote past it are rewritten or masked out) and the
+blocks are drafted again.  Both modes commit exactly the same tokens.
+
 The committed context lives in permanent cache slots [0, ctx); a forward's
 rows write their K/V at slots ctx.. in row order (past the committed context,
 so a later forward overwrites them), and each row's mask comes from
@@ -92,7 +102,8 @@ class SpecRunner:
     resident on one GPU."""
 
     def __init__(self, draft: SynthModel, target: SynthModel, block_length: int = 4, denoise_steps: int = 4,
-                 k_blocks: int = 4, mask_token_id: int = MASK_TOKEN_ID, overlap: bool = True):
+                 k_blocks: int = 4, mask_token_id: int = MASK_TOKEN_ID, overlap: bool = True,
+                 pipelined: bool = False):
         self.draft, self.target = draft, target
         self.bl, self.ds, self.K = block_length, denoise_steps, k_blocks
         self.mask_id = mask_token_id
@@ -107,8 +118,14 @@ class SpecRunner:
         self.draft_blocks = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
         self.step_maps = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
         self.overlap = overlap
+        self.pipelined = pipelined
         self.side = torch.cuda.Stream(device=self.dev)      # default priority
+        self.draft_stream = torch.cuda.Stream(device=self.dev)
         self._extend_done = None
+        self._verify_ready = None
+        self._draft_done = None       # optimistic drafts still running on draft_stream
+        self._have_next = False       # draft_blocks hold valid drafts for the next iteration
+        self.stats = {"optimistic_used": 0, "optimistic_dropped": 0}
         self.ctx = 0
         self.tokens = []          # generated tokens (accepted + bonus)
         self.history = []         # the committed context: prompt + committed blocks
@@ -178,13 +195,16 @@ class SpecRunner:
 
     # ---------------------------------------------------------- one step
     @torch.inference_mode()
-    def draft_blocks_(self):
+    def draft_blocks_(self, ctx: int | None = None, last_block: torch.Tensor | None = None):
         """K blocks; block k folds block k - 1 (the last committed block for
-        k = 0) in as its prefix."""
+        k = 0) in as its prefix.  ``ctx`` / ``last_block`` default to the
+        committed state (the optimistic drafts pass the assumed one)."""
         g, bl, dcols = self._dg, self.bl, self.draft.cache.full_len
+        ctx = self.ctx if ctx is None else ctx
+        last_block = self.last_block if last_block is None else last_block
         for k in range(self.K):
-            start = self.ctx - bl + k * bl            # prefix position
-            g.ids[:bl].copy_(self.last_block if k == 0 else self.draft_blocks[k - 1])
+            start = ctx - bl + k * bl                 # prefix position
+            g.ids[:bl].copy_(last_block if k == 0 else self.draft_blocks[k - 1])
             g.set_span(start, start, 2 * bl)
             block_mask(dcols, start, start, n_prefix=bl, n_free=bl, out=g.mask)
             if g.graph is None:
@@ -210,6 +230,9 @@ class SpecRunner:
                    block_length=bl, block_size=self.ds, out=g.mask)
         if g.graph is None:
             g.capture(self._verify_body)
+        # the verify's inputs are set: later work may overwrite draft_blocks / step_maps
+        self._verify_ready = torch.cuda.Event()
+        self._verify_ready.record()
         return g.replay().view(K, 2, bl)[:, 1]
 
     @torch.inference_mode()
@@ -231,26 +254,49 @@ class SpecRunner:
                 self._extend_done.record(stream)
 
     def finish(self):
-        """Wait for an extend still running on the side stream."""
+        """Wait for work still running on the side streams (an extend, an
+        optimistic draft)."""
         if self._extend_done is not None:
             torch.cuda.current_stream().wait_event(self._extend_done)
             self._extend_done = None
+        if self._draft_done is not None:
+            torch.cuda.current_stream().wait_event(self._draft_done)
+            self._draft_done = None
 
     @torch.inference_mode()
     def step(self, events=None):
         """One iteration -> (generated tokens, accepted draft tokens).  With
         ``events`` (four torch.cuda.Event), their records bracket the draft,
         verify, acceptance and extend phases on the current stream."""
+        main = torch.cuda.current_stream()
         if events:
             events[0].record()
-        self.draft_blocks_()
+        if self._draft_done is not None:              # optimistic drafts finish before use or redo
+            main.wait_event(self._draft_done)
+            self._draft_done = None
+        if not self._have_next:
+            self.draft_blocks_()
+        self._have_next = False
         if events:
             events[1].record()
         target_ids = self.verify_()
+        if self.pipelined:
+            # iteration N + 1's drafts, assuming every block of N is accepted,
+            # on their own stream while the verify runs
+            K, bl = self.K, self.bl
+            with torch.cuda.stream(self.draft_stream):
+                self.draft_stream.wait_event(self._verify_ready)
+                self.draft_blocks_(ctx=self.ctx + K * bl, last_block=self._vg.ids.view(K, 2, bl)[K - 1, 0])
+                self._draft_done = torch.cuda.Event()
+                self._draft_done.record(self.draft_stream)
         if events:
             events[2].record()
-        both = torch.stack([self.draft_blocks, target_ids]).cpu()     # the one host sync
+        drafted = self._vg.ids.view(self.K, 2, self.bl)[:, 0]          # the drafts this verify checked
+        both = torch.stack([drafted, target_ids]).cpu()                # the one host sync
         committed, generated, n_acc = accept_blocks(both[0].tolist(), both[1].tolist(), self.bl)
+        if self.pipelined:
+            self._have_next = n_acc == self.K * self.bl
+            self.stats["optimistic_used" if self._have_next else "optimistic_dropped"] += 1
         if events:
             events[3].record()
         self.extend_(committed)

@@ -107,3 +107,38 @@ def test_runner_iterations():
     # the step maps are permutations of the schedule's steps
     for row in runner.step_maps.cpu().tolist():
         assert sorted(row) == [0, 1, 2, 3]
+
+
+def _run(pipelined, draft_seed, target_seed, iters=6, prompt_seed=2):
+    from speculative.model import ModelShape, SynthModel
+    from speculative.step import SpecRunner
+    shape = ModelShape(**TINY)
+    draft = SynthModel(shape, DEV, draft_seed, 256, 64)
+    target = SynthModel(shape, DEV, target_seed, 256, 64)
+    runner = SpecRunner(draft, target, mask_token_id=shape.vocab - 1, pipelined=pipelined)
+    prompt = torch.randint(0, shape.vocab - 1, (32,), generator=torch.Generator().manual_seed(prompt_seed))
+    runner.prefill(prompt)
+    out = [runner.step() for _ in range(iters)]
+    runner.finish()
+    torch.cuda.synchronize()
+    return out, runner
+
+
+@pytest.mark.parametrize("same_weights", [True, False])
+def test_pipelined_equals_sequential(same_weights):
+    """The optimistic two-stream mode (the next iteration's drafts run beside
+    the verify) commits exactly the tokens of the sequential runner, both when
+    its drafts are used (draft = target weights: every block accepted) and
+    when they are dropped (independent weights: rollback and redraft)."""
+    ts = 5 if same_weights else 6
+    seq, r_seq = _run(False, 5, ts)
+    pip, r_pip = _run(True, 5, ts)
+    assert pip == seq
+    assert r_pip.history_ids() == r_seq.history_ids()
+    assert r_pip.ctx == r_seq.ctx
+    used, dropped = r_pip.stats["optimistic_used"], r_pip.stats["optimistic_dropped"]
+    assert used + dropped == len(seq)
+    if same_weights:
+        assert used >= 1, r_pip.stats
+    else:
+        assert dropped >= 1, r_pip.stats
