@@ -489,6 +489,162 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
   store_elem<DT>(a.out, t * a.sot + h * a.soh, o);
 }
 
+// down + combine for a few tokens (T <= kSmallT).  One workgroup owns R = 4*G
+// output features for every token; its W waves take the tiles round-robin
+// (the shared expert last), at most UM per wave.  A tile's weight rows stream
+// in the GEMV layout of thin_gemv4_kernel (4 rows x 256 contiguous bytes per
+// load, tokens as the 4 columns of v_mfma_f32_4x4x4) and are reused for each
+// set of 4 valid slots of the tile (one set unless a token picks an expert
+// twice).  A wave first reads the descriptors of all its tiles (one round
+// trip), then keeps two tiles' loads in flight.  The expert outputs, rounded
+// to the dtype as moe_down_kernel stores them, meet in LDS; the combine of
+// moe_combine_kernel then runs on them: one launch instead of two, and no
+// [T*k, H] round trip through memory.
+constexpr int kSmallT = 4;
+constexpr int kSmallSlots = 64;   // T * k limit of the LDS table
+
+template <int DT, int G, int S>
+struct SmallUnit {
+  u32x4_t A[G][S];
+  u32x4_t B[S];
+};
+
+template <int DT, int G, int S, int W, int UM>
+__global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  constexpr int R = 4 * G;
+  __shared__ float y_sh[kSmallSlots + kSmallT][R];   // [slot t*k + j | T*k + token][feature]
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int i4 = lane & 3, b4 = lane >> 2;
+  const int64_t n0 = (int64_t)blockIdx.x * R;
+  const int rows = (int)min((int64_t)R, a.H - n0);
+  const int n_units = a.num_tiles + (a.shared_tiles > 0 ? 1 : 0);
+  const int M = (int)(a.T * a.k);
+  const uint32_t lane_k = (uint32_t)b4 * kLaneBytes;
+
+  // descriptors of this wave's units: expert (-1 shared, -2 none) and the
+  // lane's first-set column (a slot, or a token for the shared expert)
+  int ue[UM], ucol[UM];
+#pragma unroll
+  for (int i = 0; i < UM; ++i) {
+    const int u = wv + i * W;
+    if (u < a.num_tiles) {
+      const int e = a.tile_expert[u];
+      ue[i] = (e >= 0 && e < a.E) ? e : -2;
+      ucol[i] = a.slots[(int64_t)u * kTile + i4];
+    } else if (u < n_units) {
+      ue[i] = -1;
+      ucol[i] = i4 < a.T ? i4 : -1;
+    } else {
+      ue[i] = -2;
+      ucol[i] = -1;
+    }
+  }
+  auto w_rsrc = [&](int e, uint32_t& sn_b, uint32_t& Kb) {
+    const bool shared = e < 0;
+    Kb = (uint32_t)((shared ? a.Is : a.I) * ES);
+    const int64_t sn = shared ? a.shd_h : a.sdh;
+    sn_b = (uint32_t)(sn * ES);
+    const char* wb = (shared ? a.shd : a.wd + (int64_t)e * a.sde * ES) + n0 * sn * ES;
+    return make_rsrc(wb, (uint32_t)(rows - 1) * sn_b + Kb);
+  };
+  auto h_rsrc = [&](int e, uint32_t Kb) {
+    return make_rsrc(e < 0 ? a.hs : a.h, (uint32_t)(e < 0 ? a.T : M) * Kb);
+  };
+  auto load_b = [&](const rsrc_t& rH, uint32_t Kb, int col, u32x4_t (&B)[S]) {
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const uint32_t k = (uint32_t)st * kStep4Bytes + lane_k;
+      B[st] = buf_load16<kAuxKeep>(rH, (col >= 0 && k < Kb) ? (uint32_t)col * Kb + k : kOob);
+    }
+  };
+  auto issue = [&](int i, SmallUnit<DT, G, S>& U) {
+    if (ue[i] == -2) return;
+    uint32_t sn_b, Kb;
+    const rsrc_t rW = w_rsrc(ue[i], sn_b, Kb);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        const uint32_t k = (uint32_t)st * kStep4Bytes + lane_k;
+        U.A[g][st] = buf_load16<kAuxStream>(rW, k < Kb ? (uint32_t)(4 * g + i4) * sn_b + k : kOob);
+      }
+    load_b(h_rsrc(ue[i], Kb), Kb, ucol[i], U.B);
+  };
+  // one column set: MFMAs, the 16 k blocks summed (lane bits 2..5), lanes
+  // with bits 2..3 clear hold feature q0 + p of column i4
+  auto finish = [&](const SmallUnit<DT, G, S>& U, const u32x4_t (&B)[S], int col, bool shared) {
+    f32x4_t acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      acc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        acc[g] = Mfma4<DT>::step(lo2(U.A[g][st]), lo2(B[st]), acc[g]);
+        acc[g] = Mfma4<DT>::step(hi2(U.A[g][st]), hi2(B[st]), acc[g]);
+      }
+    }
+    constexpr int NV = G * 4;
+    float val[NV];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) val[g * 4 + v] = acc[g][v];
+    reduce_lanes<NV, 4>(val);
+    if (((lane >> 2) & 3) == 0 && col >= 0) {
+      const int q0 = ((lane >> 5) & 1) * (NV / 2) + ((lane >> 4) & 1) * (NV / 4);
+      const int row = shared ? M + col : col;
+#pragma unroll
+      for (int p = 0; p < NV / 4; ++p) y_sh[row][q0 + p] = round_to<DT>(val[p]);
+    }
+  };
+  auto compute = [&](int i, const SmallUnit<DT, G, S>& U) {
+    if (ue[i] == -2) return;
+    const bool shared = ue[i] == -1;
+    finish(U, U.B, ucol[i], shared);
+    if (shared) return;
+    // further sets of 4 slots: only when a token picked this expert twice
+    const int u = wv + i * W;
+    uint32_t Kb = (uint32_t)(a.I * ES);
+    const rsrc_t rH = h_rsrc(ue[i], Kb);
+    for (int cs = 1; cs < kTile / 4; ++cs) {
+      const int col = a.slots[(int64_t)u * kTile + 4 * cs + i4];
+      if (!__any(col >= 0)) break;       // slots fill a tile from the front
+      u32x4_t B[S];
+      load_b(rH, Kb, col, B);
+      finish(U, B, col, false);
+    }
+  };
+
+  SmallUnit<DT, G, S> U0, U1;
+  issue(0, U0);
+  if (UM > 1) issue(1, U1);
+#pragma unroll
+  for (int i = 0; i < UM; i += 2) {
+    compute(i, U0);
+    if (i + 2 < UM) issue(i + 2, U0);
+    if (i + 1 < UM) {
+      compute(i + 1, U1);
+      if (i + 3 < UM) issue(i + 3, U1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < (int)a.T * R; e += 64 * W) {
+    const int64_t t = e / R;
+    const int f = e % R;
+    if (f >= rows) continue;
+    float acc = 0.f;
+    for (int j = 0; j < a.k; ++j) {
+      const int64_t id = a.ids[t * a.sidt + j * a.sidk];
+      const float w = a.topk_w[t * a.swt + j * a.swk];
+      if (id >= 0 && id < a.E) acc = __fadd_rn(acc, __fmul_rn(y_sh[t * a.k + j][f], w));
+    }
+    float o = round_to<DT>(acc);
+    if (a.shared_tiles > 0) o = o + y_sh[M + t][f];
+    store_elem<DT>(a.out, t * a.sot + (n0 + f) * a.soh, o);
+  }
+}
+
 // ------------------------------------------------------------------ host side
 namespace {
 
@@ -515,14 +671,41 @@ MoeLayout moe_layout(int64_t T, int k, int64_t H, int64_t I, int64_t Is, int es)
   return L;
 }
 
+// the fused down + combine: small-T steps whose h rows fit S 256-byte steps;
+// W waves of at most UM tiles each
+#ifndef SIMSD_MOE_SMALL_G
+#define SIMSD_MOE_SMALL_G 2
+#endif
+#ifndef SIMSD_MOE_SMALL_W
+#define SIMSD_MOE_SMALL_W 8
+#endif
+#ifndef SIMSD_MOE_SMALL_UM
+#define SIMSD_MOE_SMALL_UM 5
+#endif
+constexpr int kSmallG = SIMSD_MOE_SMALL_G, kSmallW = SIMSD_MOE_SMALL_W, kSmallUM = SIMSD_MOE_SMALL_UM;
+constexpr int kSmallUM8 = 10;   // the 8-step variant: 4 features per workgroup
+
 template <int DT>
-void launch_ffn(const MoeArgs& a, bool fast_gu, bool fast_dn, void* stream_) {
+void launch_ffn(const MoeArgs& a, bool fast_gu, bool fast_dn, bool small, void* stream_) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   const int tiles = a.num_tiles + a.shared_tiles;
   const int64_t imax = a.I > a.Is ? a.I : a.Is;
   dim3 g1((unsigned)tiles, (unsigned)((imax + 15) / 16));
   if (fast_gu) hipLaunchKernelGGL((moe_gate_up_kernel<DT, true>), g1, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL((moe_gate_up_kernel<DT, false>), g1, dim3(256), 0, stream, a);
+  if constexpr (DT != kF32) {
+    if (small) {
+      constexpr int R = 4 * kSmallG;
+      const dim3 gs((unsigned)((a.H + R - 1) / R));
+      if (imax * DTypeInfo<DT>::kSize <= 4 * kStep4Bytes)
+        hipLaunchKernelGGL((moe_down_combine_kernel<DT, kSmallG, 4, kSmallW, kSmallUM>), gs, dim3(64 * kSmallW), 0,
+                           stream, a);
+      else   // twice the k steps: 4 features per workgroup
+        hipLaunchKernelGGL((moe_down_combine_kernel<DT, 1, 8, kSmallW, kSmallUM8>),
+                           dim3((unsigned)((a.H + 3) / 4)), dim3(64 * kSmallW), 0, stream, a);
+      return;
+    }
+  }
   dim3 g2((unsigned)tiles, (unsigned)((a.H + 63) / 64));
   if (fast_dn) hipLaunchKernelGGL((moe_down_kernel<DT, true>), g2, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL((moe_down_kernel<DT, false>), g2, dim3(256), 0, stream, a);
@@ -681,10 +864,17 @@ extern "C" int simsd_moe_grouped_ffn(
     fast_dn = fast_dn && row_ok(sh_down, shd_h, shd_i, Is, es) && shd_h > 0 &&
               (H + 16) * shd_h * es < lim;
   }
+  // a few tokens: down and combine in one launch (every operand row 16-byte
+  // aligned, h rows within 8 load steps, the T*k slot outputs within LDS)
+  const int64_t units = num_tiles + (has_shared ? 1 : 0);
+  const bool small = fast_dn && dtype != kF32 && T <= kSmallT && T * k <= kSmallSlots &&
+                     Imax * es <= 8 * kStep4Bytes && (sde * es) % 16 == 0 && (sdh * es) % 16 == 0 &&
+                     (!has_shared || (shd_h * es) % 16 == 0) &&
+                     units <= kSmallW * (Imax * es <= 4 * kStep4Bytes ? kSmallUM : kSmallUM8);
   switch (dtype) {
-    case kBF16: launch_ffn<kBF16>(a, fast_gu, fast_dn, stream); break;
-    case kF16: launch_ffn<kF16>(a, fast_gu, fast_dn, stream); break;
-    default: launch_ffn<kF32>(a, fast_gu, fast_dn, stream); break;
+    case kBF16: launch_ffn<kBF16>(a, fast_gu, fast_dn, small, stream); break;
+    case kF16: launch_ffn<kF16>(a, fast_gu, fast_dn, small, stream); break;
+    default: launch_ffn<kF32>(a, fast_gu, fast_dn, false, stream); break;
   }
   return check_launch("moe_grouped_ffn");
 }

@@ -183,43 +183,6 @@ SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, fl
   }
 }
 
-// Sum NV per-lane values over lane bits 5, 4 and the row bits from log2(LO)
-// up to 3.  Bits 5 and 4 by reduce-scatter on the gfx950 lane swaps:
-// v_permlane32_swap(a, b) leaves [a.lo, b.lo] / [a.hi, b.hi], so one swap and
-// one add sum a pair of values over the two half-waves and keep one of them
-// per half (likewise rows 0/1 and 2/3 with v_permlane16_swap).  The row bits
-// by adding row rotations by 8, 4, ..., LO (after which every lane of the
-// rotation class holds the full sum).  Afterwards lane l holds, in val[p] for
-// p < NV/4, the sum of original value p + bit5(l) * NV/2 + bit4(l) * NV/4.
-// A fixed instruction sequence: bit-reproducible.
-template <int NV, int LO>
-__device__ __forceinline__ void reduce_lanes(float (&val)[NV]) {
-  static_assert(NV >= 4 && (NV & (NV - 1)) == 0, "power of two >= 4");
-  static_assert(LO == 1 || LO == 2 || LO == 4 || LO == 8, "rotation");
-#pragma unroll
-  for (int p = 0; p < NV / 2; ++p) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(val[p]),
-                                                    __float_as_uint(val[p + NV / 2]), false, false);
-    val[p] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-#pragma unroll
-  for (int p = 0; p < NV / 4; ++p) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(val[p]),
-                                                    __float_as_uint(val[p + NV / 4]), false, false);
-    val[p] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-#pragma unroll
-  for (int p = 0; p < NV / 4; ++p) {
-    val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x128, 0xF, 0xF, false));
-    if (LO <= 4)
-      val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x124, 0xF, 0xF, false));
-    if (LO <= 2)
-      val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x122, 0xF, 0xF, false));
-    if (LO <= 1)
-      val[p] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(val[p]), 0x121, 0xF, 0xF, false));
-  }
-}
-
 template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU, bool NORM>
 __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;

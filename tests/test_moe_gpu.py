@@ -404,3 +404,43 @@ def test_moe_forward_c4(T):
     err = float(np.abs(_np(out) - ref).max())
     assert err <= omoe.tolerance(amax, "bf16"), err
     assert err / amax <= 1e-2
+
+
+# ───────────────────────── a few tokens: down and combine in one launch ───
+SMALL = [
+    # name, T, k, E, H, I, shared, ids pattern
+    ("T4_k8_E256", 4, 8, 256, 2048, 512, True, None),
+    ("T1_k8_noshared", 1, 8, 256, 2048, 512, False, None),
+    ("T3_k4_I1024", 3, 4, 32, 256, 1024, True, None),        # 8 load steps per h row
+    ("T4_all_one_expert", 4, 8, 64, 512, 256, True, "same"),  # 32 slots of one expert: 2 tiles x 4 column sets
+    ("T2_dup_invalid", 2, 6, 16, 136, 128, False, "dup"),     # repeated and out-of-range ids, H % 8 != 0
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+@pytest.mark.parametrize("case", SMALL, ids=[c[0] for c in SMALL])
+def test_small_token_down_combine(case, dtype):
+    """T <= 4 runs down and combine as one kernel; it must agree with the
+    oracle like the three-launch path, including experts holding more than
+    four slots of the tile and ids that add nothing."""
+    from kernels.moe_dispatch_fused import _align, _grouped_ffn, _num_tiles
+    name, T, k, E, H, I, with_shared, pattern = case
+    x, ids, w, wg, wu, wd = _case(T, k, E, H, I, dtype, seed=zlib.crc32(name.encode()) & 0xFFFF)
+    ids = ids.clone()
+    if pattern == "same":
+        ids.fill_(5)
+    elif pattern == "dup":
+        ids[0, 1] = ids[0, 0]
+        ids[1, 0] = ids[0, 0]
+        ids[1, 2] = -1
+        ids[0, 3] = E
+    g = torch.Generator(device=DEV).manual_seed(9)
+    mk = lambda *s: (torch.randn(*s, device=DEV, generator=g) / (s[-1] ** 0.5)).to(_dt(dtype))
+    shared = (mk(I, H), mk(I, H), mk(H, I)) if with_shared else None
+    slots, te = _align(ids, E, _num_tiles(ids.numel(), E))
+    with torch.inference_mode():
+        got = _grouped_ffn(x, ids, w, wg, wu, wd, slots, te, shared=shared)
+    sh = tuple(_np(s) for s in shared) if shared is not None else None
+    ref = omoe.dispatch_direct(_np(x), ids.cpu().numpy(), _np(w), _np(wg), _np(wu), _np(wd), dtype=dtype, shared=sh)
+    err = float(np.abs(_np(got) - ref).max())
+    assert err <= omoe.tolerance(float(np.abs(ref).max()), dtype), (name, err)
