@@ -528,8 +528,8 @@ def run_attn(args, torch, dev):
     cache = BlockKVCache(L_layers, Hkv, ctx, M, dev)
     g = torch.Generator(device=dev).manual_seed(90)
     for lay in range(L_layers):
-        cache.key_cache[lay].normal_(generator=g)
-        cache.value_cache_t[lay].normal_(generator=g)
+        cache.k_tiles[lay].normal_(generator=g)
+        cache.v_tiles[lay].normal_(generator=g)
     cos, sin = rope_tables(default_inv_freq(device=dev), 4096, torch.bfloat16)
     qkvs = [torch.randn(M, (Hq + 2 * Hkv) * D, device=dev, generator=g).bfloat16() for _ in range(L_layers)]
     qn = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).bfloat16()
@@ -548,8 +548,8 @@ def run_attn(args, torch, dev):
                                 cache, lay, mask, valid_len=L) for lay, x in enumerate(qkvs)]
 
     # the reference's expanded cache ([1, Hq, L, D]) holding the same context
-    kexp = [cache.key_cache[lay].repeat_interleave(n_rep, 0)[None].contiguous() for lay in range(L_layers)]
-    vexp = [cache.value_cache(lay).repeat_interleave(n_rep, 0)[None].contiguous() for lay in range(L_layers)]
+    kexp = [cache.keys(lay).repeat_interleave(n_rep, 0)[None].contiguous() for lay in range(L_layers)]
+    vexp = [cache.values(lay).repeat_interleave(n_rep, 0)[None].contiguous() for lay in range(L_layers)]
     c, s_ = cos[pos][:, None], sin[pos][:, None]
 
     def norm(t, w):

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 10
+#define SIMSD_ABI_VERSION 11
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -251,8 +251,13 @@ int simsd_denoise_select(const void* logits, int64_t slm, int64_t M, int64_t V, 
                          void* stream);
 
 /* ---- attention over a static KV cache ----------------------------------
- * Cache layout per layer (one sequence, head_dim D = 128): K [Hkv, L, D]
- * (strides skh, skl) and V transposed, Vt [Hkv, D, L] (strides svh, svd).
+ * Cache layout per layer (one sequence, head_dim D = 128, L slots, L a
+ * multiple of 32): one block of L * D elements per KV head (head stride
+ * kv_head_stride >= L * D elements) in each of two tile arrays, laid out in
+ * the order the attention's MFMA operands read them:
+ *   K: (slot s, dim d) at ((s/16 * 16 + d/8) * 16 + s%16) * 8 + d%8
+ *   V: (slot s, dim d) at ((((s/32 * 8 + d/16) * 16 + d%16) * 4 + s/4%4) * 2
+ *                          + s/16%2) * 4 + s%4
  * The KV heads are stored once per group, not replicated per query head.
  *
  * simsd_qkv_rope_cache: for each of the M tokens of qkv [M, (Hq + 2 Hkv) * D]
@@ -269,10 +274,9 @@ int simsd_denoise_select(const void* logits, int64_t slm, int64_t M, int64_t V, 
  * skipped. */
 int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, const void* k_norm_w, float eps,
                          const void* cos, const void* sin, int64_t scs, int64_t n_pos, const int64_t* pos,
-                         const int64_t* slots, const int64_t* slots2, void* k_cache, int64_t skh, int64_t skl,
-                         void* vt_cache, int64_t svh, int64_t svd, int64_t L, void* q_out, int64_t sqo_m,
-                         int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t head_dim, int dtype,
-                         void* stream);
+                         const int64_t* slots, const int64_t* slots2, void* k_cache, void* v_cache,
+                         int64_t kv_head_stride, int64_t L, void* q_out, int64_t sqo_m, int64_t sqo_h, int64_t M,
+                         int64_t Hq, int64_t Hkv, int64_t head_dim, int dtype, void* stream);
 
 /* simsd_block_attention: out[m, hq] = softmax(scale * q[m, hq] . K[h]^T over
  * the visible slots) . V[h] with h = hq / (Hq / Hkv) -- the SDPA call of
@@ -280,7 +284,7 @@ int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, co
  * row stride smask, nonzero = visible; NULL = all visible; 4-byte aligned
  * rows of at least L_valid rounded up to 4 bytes).  Slots
  * [0, L_valid) are considered, L_valid <= L_cap (the cache's slot count, a
- * multiple of 4); fp32 softmax, output rounded to the dtype; rows with no
+ * multiple of 32); fp32 softmax, output rounded to the dtype; rows with no
  * visible slot give 0.  Every slot below L_cap must hold finite values (a
  * zero-initialised cache written only with finite K/V), since slots past a
  * row's visible range may enter the P.V product with weight 0.
@@ -291,11 +295,11 @@ int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, co
  * L_valid), 16-byte aligned.  Deterministic. */
 int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid);
 
-int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, int64_t skh, int64_t skl,
-                          const void* vt_cache, int64_t svh, int64_t svd, int64_t L_cap, const uint8_t* mask,
-                          int64_t smask, void* out, int64_t so_m, int64_t so_h, int64_t M, int64_t Hq, int64_t Hkv,
-                          int64_t L_valid, const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype,
-                          void* workspace, int64_t workspace_bytes, void* stream);
+int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, const void* v_cache,
+                          int64_t kv_head_stride, int64_t L_cap, const uint8_t* mask, int64_t smask, void* out,
+                          int64_t so_m, int64_t so_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid,
+                          const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype, void* workspace,
+                          int64_t workspace_bytes, void* stream);
 
 /* simsd_block_mask: the attention mask rows (uint8, 1 = visible; row stride
  * smask, n_cols slots) of a cached forward whose rows are n_prefix rows of a

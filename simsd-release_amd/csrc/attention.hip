@@ -9,13 +9,17 @@
 //   key_cache.index_copy_(2, slots, k) ... (per GQA replica)      -> qkv_rope_cache_kernel
 //   out = F.scaled_dot_product_attention(q, K, V, attn_mask=bool)  -> attn_partial + attn_combine
 //
-// Cache layout, per layer (one sequence): K [Hkv, L, D] and V stored
-// transposed, Vt [Hkv, D, L].  The KV heads are not replicated per query head
-// (the reference's "expand" mode copies each of them n_rep times); every query
-// head reads its group's KV head, so the cache and its traffic are n_rep times
-// smaller.  Vt puts the slot index innermost, which is the contraction index of
-// P.V, so both attention products take their MFMA operands with contiguous
-// loads:
+// Cache layout, per layer (one sequence) and KV head, L a multiple of 32: K and
+// V in tiles laid out in the order the MFMA operands are read, so that every
+// wave-wide 16-byte load covers 1 KB of contiguous memory (8 whole cache
+// lines, where a row-major [L, D] or [D, L] layout touches 16 lines per load):
+//   K: [L/16][16 dim chunks of 8][16 keys][8 dims]
+//      (slot s, dim d) -> ((s/16 * 16 + d/8) * 16 + s%16) * 8 + d%8
+//   V: [L/32][8 dim tiles of 16][16 dims][4 key quads][2 halves][4 keys]
+//      (slot s, dim d) -> ((((s/32 * 8 + d/16) * 16 + d%16) * 4 + s/4%4) * 2 + s/16%2) * 4 + s%4
+// The KV heads are not replicated per query head (the reference's "expand"
+// mode copies each of them n_rep times); every query head reads its group's
+// KV head, so the cache and its traffic are n_rep times smaller.  The products:
 //   S^T = K . Q^T   A = K tile (16 keys x 32 dims), B = Q^T (32 dims x 16 rows)
 //   O^T = Vt . P^T  A = Vt tile (16 dims x 32 keys), B = P^T (32 keys x 16 rows)
 // and P^T never leaves registers: the S^T result lane (g, r) holds keys
@@ -25,10 +29,12 @@
 // Query rows are the (query head, token) pairs of one KV head's group,
 // row = i * M + m for query head h * n_rep + i, padded to 16-row blocks.
 //
-// The key range is split into chunks, one workgroup per (chunk, KV head); each
-// keeps an online softmax (running max and sum per row) and writes its
-// unnormalised partial output; attn_combine merges the chunks in chunk order
-// (fixed order: bit-reproducible).
+// Short contexts: one workgroup per KV head, its waves taking the 32-key steps
+// in turn and merging their online-softmax states in LDS (one launch).  Long
+// contexts: the key range is split into chunks, one workgroup per (chunk, KV
+// head); each keeps an online softmax (running max and sum per row) and writes
+// its unnormalised partial output; attn_combine merges the chunks in chunk
+// order.  Both orders are fixed: bit-reproducible.
 #include <type_traits>
 
 #include "simsd_common.hpp"
@@ -63,6 +69,14 @@ template <> SIMSD_DEV uint32_t pack2<kF16>(float lo, float hi) {
 }
 
 // ------------------------------------------------ q/k norm, RoPE, cache write
+// Element index of (slot s, dim d) in one KV head's K and V tiles.
+SIMSD_DEV int64_t k_tile_index(int64_t s, int d) {
+  return (((s >> 4) * 16 + (d >> 3)) * 16 + (s & 15)) * 8 + (d & 7);
+}
+SIMSD_DEV int64_t v_tile_index(int64_t s, int d) {
+  return (((((s >> 5) * 8 + (d >> 4)) * 16 + (d & 15)) * 4 + ((s >> 2) & 3)) * 2 + ((s >> 4) & 1)) * 4 + (s & 3);
+}
+
 struct QkvArgs {
   const char* qkv;            // [M, (Hq + 2 Hkv) * D]: q heads, then k heads, then v heads
   int64_t sqkv;               // row stride (elements)
@@ -75,10 +89,9 @@ struct QkvArgs {
   const int64_t* pos;         // [M]
   const int64_t* slots;       // [M] cache slots written
   const int64_t* slots2;      // [M] second slots (permanent copies) or null
-  char* kc;                   // K [Hkv, L, D]
-  int64_t skh, skl;
-  char* vt;                   // Vt [Hkv, D, L]
-  int64_t svh, svd;
+  char* kc;                   // K tiles, head stride sh (elements)
+  char* vc;                   // V tiles, head stride sh
+  int64_t sh;
   int64_t L;
   char* qo;                   // [M, Hq, D]
   int64_t sqo_m, sqo_h;
@@ -122,15 +135,15 @@ __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
       n0 = load_elem<DT>(sr, d0); n1 = load_elem<DT>(sr, d1);
     }
   }
-  if (is_v) {   // v head: copy into the transposed cache
-    char* base = a.vt + (int64_t)(hh - a.Hq - a.Hkv) * a.svh * ES;
+  if (is_v) {   // v head: copy into the V tiles
+    char* base = a.vc + (int64_t)(hh - a.Hq - a.Hkv) * a.sh * ES;
     if (s1_ok) {
-      store_elem<DT>(base, d0 * a.svd + s1, x0);
-      store_elem<DT>(base, d1 * a.svd + s1, x1);
+      store_elem<DT>(base, v_tile_index(s1, d0), x0);
+      store_elem<DT>(base, v_tile_index(s1, d1), x1);
     }
     if (s2_ok) {
-      store_elem<DT>(base, d0 * a.svd + s2, x0);
-      store_elem<DT>(base, d1 * a.svd + s2, x1);
+      store_elem<DT>(base, v_tile_index(s2, d0), x0);
+      store_elem<DT>(base, v_tile_index(s2, d1), x1);
     }
     return;
   }
@@ -150,14 +163,14 @@ __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
     store_elem<DT>(dst, d0, y0);
     store_elem<DT>(dst, d1, y1);
   } else if (pos_ok) {
-    char* base = a.kc + (int64_t)(hh - a.Hq) * a.skh * ES;
+    char* base = a.kc + (int64_t)(hh - a.Hq) * a.sh * ES;
     if (s1_ok) {
-      store_elem<DT>(base, s1 * a.skl + d0, y0);
-      store_elem<DT>(base, s1 * a.skl + d1, y1);
+      store_elem<DT>(base, k_tile_index(s1, d0), y0);
+      store_elem<DT>(base, k_tile_index(s1, d1), y1);
     }
     if (s2_ok) {
-      store_elem<DT>(base, s2 * a.skl + d0, y0);
-      store_elem<DT>(base, s2 * a.skl + d1, y1);
+      store_elem<DT>(base, k_tile_index(s2, d0), y0);
+      store_elem<DT>(base, k_tile_index(s2, d1), y1);
     }
   }
 }
@@ -166,10 +179,9 @@ __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
 struct AttnArgs {
   const char* q;              // [M, Hq, D]
   int64_t sq_m, sq_h;
-  const char* kc;             // K [Hkv, L_cap, D]
-  int64_t skh, skl;
-  const char* vt;             // Vt [Hkv, D, L_cap]
-  int64_t svh, svd;
+  const char* kc;             // K tiles, head stride sh (elements)
+  const char* vc;             // V tiles, head stride sh
+  int64_t sh, L_cap;
   const uint8_t* mask;        // [M, >= L_valid] (nonzero = visible) or null
   int64_t smask;
   int64_t M;
@@ -191,68 +203,44 @@ SIMSD_DEV u32x4_t load16_sel(const char* p, bool ok) {
   return ok ? v : zero4();
 }
 
-// Four keys of one Vt row (8 bytes) from key (a multiple of 4); keys at or
-// past `end` read as zero.  last4 = (end - 1) & ~3, a valid group start.
-template <int DT>
-SIMSD_DEV u32x2_t load_vt4(const char* rowp, int64_t key, int64_t end, int64_t last4) {
-  constexpr int ES = DTypeInfo<DT>::kSize;
-  const int64_t kk = key < last4 ? key : last4;
-  u32x2_t v = *reinterpret_cast<const u32x2_t*>(rowp + kk * ES);
-  const int64_t n = end - key;   // valid keys in this group (may be <= 0)
-  v.x = n >= 2 ? v.x : (n >= 1 ? (v.x & 0xffffu) : 0u);
-  v.y = n >= 4 ? v.y : (n >= 3 ? (v.y & 0xffffu) : 0u);
-  return v;
-}
-
-// Buffer loads of 8 and 4 bytes (the 16-byte one is in simsd_common.hpp):
-// offsets at or past the descriptor's extent read as zero, with no branch.
-__device__ int32_t __attribute__((ext_vector_type(2)))
-simsd_raw_buffer_load_v2i32(i32x4_t rsrc, int32_t voffset, int32_t soffset, int32_t aux)
-    __asm("llvm.amdgcn.raw.buffer.load.v2i32");
-__device__ int32_t simsd_raw_buffer_load_i32(i32x4_t rsrc, int32_t voffset, int32_t soffset, int32_t aux)
-    __asm("llvm.amdgcn.raw.buffer.load.i32");
-
-SIMSD_DEV u32x2_t buf_load8(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x2_t, simsd_raw_buffer_load_v2i32(r, (int32_t)off, 0, 0));
-}
-SIMSD_DEV uint32_t buf_load4(rsrc_t r, uint32_t off) { return (uint32_t)simsd_raw_buffer_load_i32(r, (int32_t)off, 0, 0); }
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// A wave's view of one KV head over its key range [.., c_end): descriptors
-// and per-lane byte offsets, so each 32-key step's loads are one add each.
-//   K:  extent c_end rows -- keys past the range read as zero;
-//   Vt: the head's D x svd block -- keys past the range read stale slots,
-//       which are finite (the cache starts zeroed and only takes finite
-//       values) and meet p = 0;
-//   mask: all M rows.
+// A wave's view of one KV head: descriptors over the head's K and V tiles and
+// per-lane byte offsets, so each 32-key step's loads are one add each.  A
+// step at slot c (a multiple of 32) starts at byte c * 256 of both tile
+// arrays; within it, lane (g, r) reads
+//   K tile t, dim step ds: 16 bytes at t*4096 + (4*ds + g)*256 + r*16
+//     (keys c + 16t + r, dims 32*ds + 8g .. +8: the A operand of S^T)
+//   V dim tile dt:         16 bytes at dt*1024 + r*64 + g*16
+//     (dim 16*dt + r, keys c + 4g .. +4 then c + 16 + 4g .. +4: the A operand
+//      of O^T with the k-slots of P^T)
+// so every load instruction covers 1 KB of contiguous memory.  Slots past the
+// valid range read stale cache values, which are finite (the cache starts
+// zeroed and only takes finite values) and meet p = 0; past L_cap they read
+// as zero.  mask: all M rows.
 template <int RBW>
 struct WaveKV {
   rsrc_t rk, rv, rm;
-  uint32_t k_off[2], v_off[kDTiles], m_off[RBW];
-  uint32_t k_step;   // bytes of one key row
+  uint32_t k_off, v_off, m_off[RBW];
 };
 
 template <int DT, int RBW>
-SIMSD_DEV WaveKV<RBW> wave_kv(const AttnArgs& a, int h, int64_t c_end, const int (&tok)[RBW], int g, int r) {
+SIMSD_DEV WaveKV<RBW> wave_kv(const AttnArgs& a, int h, const int (&tok)[RBW], int g, int r) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   WaveKV<RBW> w;
-  const char* kbase = a.kc + (int64_t)h * a.skh * ES;
-  const char* vbase = a.vt + (int64_t)h * a.svh * ES;
-  w.k_step = (uint32_t)(a.skl * ES);
-  w.rk = make_rsrc(kbase, (uint32_t)c_end * w.k_step);
-  w.rv = make_rsrc(vbase, (uint32_t)(kHeadDim * a.svd * ES));
+  const uint32_t head_bytes = (uint32_t)(a.L_cap * kHeadDim * ES);
+  w.rk = make_rsrc(a.kc + (int64_t)h * a.sh * ES, head_bytes);
+  w.rv = make_rsrc(a.vc + (int64_t)h * a.sh * ES, head_bytes);
   w.rm = make_rsrc(a.mask, a.mask != nullptr ? (uint32_t)(a.M * a.smask) : 0u);
-#pragma unroll
-  for (int t = 0; t < 2; ++t) w.k_off[t] = (uint32_t)(16 * t + r) * w.k_step + (uint32_t)(8 * g * ES);
-#pragma unroll
-  for (int dt = 0; dt < kDTiles; ++dt) w.v_off[dt] = (uint32_t)((dt * 16 + r) * a.svd + 4 * g) * ES;
+  w.k_off = (uint32_t)(g * 256 + r * 16);
+  w.v_off = (uint32_t)(r * 64 + g * 16);
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) w.m_off[rb] = (uint32_t)(tok[rb] * a.smask + 4 * g);
   return w;
 }
 
-// Operands of one 32-key step: K tiles (A of S^T = K.Q^T), Vt tiles (A of
+// Operands of one 32-key step: K tiles (A of S^T = K.Q^T), V tiles (A of
 // O^T = Vt.P^T) and, per row block, the 2 x 4 mask bytes of the lane's keys.
 template <int RBW>
 struct StepBuf {
@@ -263,19 +251,15 @@ struct StepBuf {
 
 template <int DT, int RBW>
 SIMSD_DEV void attn_load(const AttnArgs& a, const WaveKV<RBW>& w, int c, StepBuf<RBW>& b) {
-  constexpr int ES = DTypeInfo<DT>::kSize;
-  const uint32_t kc = (uint32_t)c * w.k_step;
+  static_assert(DTypeInfo<DT>::kSize == 2, "16-bit K/V");
+  const uint32_t base = (uint32_t)c * 256u;
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int ds = 0; ds < kDSteps; ++ds) b.kf[t][ds] = buf_load16<kAuxKeep>(w.rk, kc + w.k_off[t] + ds * 32 * ES);
-  // dim dt*16 + r, keys c + 4g .. +4 (k-slots 0..3) and c + 16 + 4g .. +4 (4..7)
+    for (int ds = 0; ds < kDSteps; ++ds)
+      b.kf[t][ds] = buf_load16<kAuxKeep>(w.rk, base + w.k_off + (uint32_t)(t * 4096 + ds * 1024));
 #pragma unroll
-  for (int dt = 0; dt < kDTiles; ++dt) {
-    const u32x2_t lo = buf_load8(w.rv, w.v_off[dt] + (uint32_t)c * ES);
-    const u32x2_t hi = buf_load8(w.rv, w.v_off[dt] + (uint32_t)(c + 16) * ES);
-    b.vf[dt] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
-  }
+  for (int dt = 0; dt < kDTiles; ++dt) b.vf[dt] = buf_load16<kAuxKeep>(w.rv, base + w.v_off + (uint32_t)(dt * 1024));
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb)
 #pragma unroll
@@ -396,7 +380,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   // c_end they read zeros (K) or finite stale slots (Vt) and meet p = 0
   StepBuf<RBW> bA, bB;
   if (c_begin < c_end) {
-    const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, c_end, tok, g, r);
+    const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, tok, g, r);
     const int ce = (int)c_end;
     attn_load<DT, RBW>(a, w, (int)c_begin, bA);
     for (int c = (int)c_begin;; c += 2 * kKeyStep) {
@@ -454,25 +438,27 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 }
 
 // Up to 32 query rows per KV head over a short context: one workgroup per
-// KV head, its 4 waves splitting the valid slots evenly; the four
-// online-softmax states merge in LDS (fixed wave order) and the normalised
-// rows go straight to the output -- one launch, no partials.
-constexpr int kHeadWaves = 4;
-// Each wave walks its slots with one step of loads in flight, so past two
-// 32-key steps per wave the chunked two-launch form, with every step's loads
-// in flight at once, wins.
-constexpr int kHeadMaxSlots = 256;
+// KV head, W waves taking its 32-key steps in turn (step i to wave i % W), so
+// a wave's first step does not depend on the valid length and its loads are
+// issued before that length is read; the next step's loads stay in flight
+// during each step.  The W online-softmax states merge in LDS (fixed wave
+// order) and the normalised rows go straight to the output: one launch, no
+// partials.  W = 8 for one 16-row block, 4 for two.
+#ifndef SIMSD_HEAD_MAX_SLOTS
+#define SIMSD_HEAD_MAX_SLOTS 1024   // measured crossover with the chunked form at 4-8 tokens
+#endif
+constexpr int kHeadMaxSlots = SIMSD_HEAD_MAX_SLOTS;
 
-template <int DT, int RBW>
-__global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnArgs a, char* __restrict__ out, int64_t so_m,
-                                                                    int64_t so_h) {
-  constexpr int ES = DTypeInfo<DT>::kSize;
+template <int DT, int RBW, int W>
+__global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __restrict__ out, int64_t so_m,
+                                                           int64_t so_h) {
   constexpr int ROWS = RBW * 16;
   constexpr int OSTR = kHeadDim + 4;   // padded rows: the b128 writes of 16 rows spread over the banks
-  __shared__ __attribute__((aligned(16))) float o_sh[kHeadWaves][ROWS][OSTR];
-  __shared__ float2 ml_sh[kHeadWaves][ROWS];
-  __shared__ float wt_sh[kHeadWaves][ROWS];
+  __shared__ __attribute__((aligned(16))) float o_sh[W][ROWS][OSTR];
+  __shared__ float2 ml_sh[W][ROWS];
+  __shared__ float wt_sh[W][ROWS];
   __shared__ float l_sh[ROWS];
+  constexpr int ES = DTypeInfo<DT>::kSize;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
@@ -491,6 +477,11 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnArgs a, 
 #pragma unroll
     for (int ds = 0; ds < kDSteps; ++ds) qf[rb][ds] = load16_sel(qp + (ds * 32 + 8 * g) * ES, row_ok[rb]);
   }
+  const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, tok, g, r);
+  StepBuf<RBW> bA, bB;
+  constexpr int kStride = W * kKeyStep;
+  int c = wv * kKeyStep;
+  attn_load<DT, RBW>(a, w, c, bA);   // before the valid length is known
   float m_run[RBW], l_run[RBW];
   f32x4_t acc[RBW][kDTiles];
 #pragma unroll
@@ -505,24 +496,16 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnArgs a, 
     const int64_t d = *a.lv_dev;
     lv = d < 0 ? 0 : (d < lv ? d : lv);
   }
-  const int64_t wc = ((lv + kHeadWaves - 1) / kHeadWaves + kKeyStep - 1) / kKeyStep * kKeyStep;
-  const int64_t c_begin = min(lv, (int64_t)wv * wc);
-  const int64_t c_end = min(lv, c_begin + wc);
-  // the next step's loads are issued before this step's arithmetic; past
-  // c_end they read zeros (K) or finite stale slots (Vt) and meet p = 0
-  StepBuf<RBW> bA, bB;
-  if (c_begin < c_end) {
-    const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, c_end, tok, g, r);
-    const int ce = (int)c_end;
-    attn_load<DT, RBW>(a, w, (int)c_begin, bA);
-    for (int c = (int)c_begin;; c += 2 * kKeyStep) {
-      attn_load<DT, RBW>(a, w, c + kKeyStep, bB);
-      attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
-      if (c + kKeyStep >= ce) break;
-      attn_load<DT, RBW>(a, w, c + 2 * kKeyStep, bA);
-      attn_step<DT, RBW>(a, qf, row_ok, bB, c + kKeyStep, ce, g, m_run, l_run, acc);
-      if (c + 2 * kKeyStep >= ce) break;
-    }
+  const int ce = (int)lv;
+  // past ce the loads read finite stale slots or zeros and meet p = 0
+  while (c < ce) {
+    attn_load<DT, RBW>(a, w, c + kStride, bB);
+    attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
+    c += kStride;
+    if (c >= ce) break;
+    attn_load<DT, RBW>(a, w, c + kStride, bA);
+    attn_step<DT, RBW>(a, qf, row_ok, bB, c, ce, g, m_run, l_run, acc);
+    c += kStride;
   }
   // lane (g, r): acc[rb][dt][j] = O^T[dim dt*16 + 4g + j][row rb*16 + r]
 #pragma unroll
@@ -537,24 +520,24 @@ __global__ __launch_bounds__(64 * kHeadWaves) void attn_head_kernel(AttnArgs a, 
     const int row = threadIdx.x;
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kHeadWaves; ++w) mx = fmaxf(mx, ml_sh[w][row].x);
+    for (int v = 0; v < W; ++v) mx = fmaxf(mx, ml_sh[v][row].x);
     float l = 0.f;
 #pragma unroll
-    for (int w = 0; w < kHeadWaves; ++w) {
-      const float2 ml = ml_sh[w][row];
+    for (int v = 0; v < W; ++v) {
+      const float2 ml = ml_sh[v][row];
       const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
-      wt_sh[w][row] = wt;
+      wt_sh[v][row] = wt;
       l += ml.y * wt;
     }
     l_sh[row] = l;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * kHeadWaves) {
+  for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
     const int row = e / kHeadDim, d = e % kHeadDim;
     if (row >= a.rows) break;
     float o = 0.f;
 #pragma unroll
-    for (int w = 0; w < kHeadWaves; ++w) o += o_sh[w][row][d] * wt_sh[w][row];
+    for (int v = 0; v < W; ++v) o += o_sh[v][row][d] * wt_sh[v][row];
     const float l = l_sh[row];
     const int i = row / (int)a.M;
     const int64_t m = row % (int)a.M;
@@ -759,26 +742,25 @@ using namespace simsd;
 extern "C" int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, const void* k_norm_w,
                                     float eps, const void* cos, const void* sin, int64_t scs, int64_t n_pos,
                                     const int64_t* pos, const int64_t* slots, const int64_t* slots2, void* k_cache,
-                                    int64_t skh, int64_t skl, void* vt_cache, int64_t svh, int64_t svd, int64_t L,
-                                    void* q_out, int64_t sqo_m, int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv,
-                                    int64_t head_dim, int dtype, void* stream) {
+                                    void* v_cache, int64_t kv_head_stride, int64_t L, void* q_out, int64_t sqo_m,
+                                    int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t head_dim, int dtype,
+                                    void* stream) {
   if (dtype != kBF16 && dtype != kF16) return set_error("qkv_rope_cache: dtype must be bf16 or fp16");
   if (head_dim != kHeadDim) return set_error("qkv_rope_cache: head_dim must be %d (got %lld)", kHeadDim, (long long)head_dim);
   if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L <= 0 || n_pos <= 0)
     return set_error("qkv_rope_cache: bad sizes");
-  if (skl < kHeadDim || svd < L || skh < L * skl || svh < kHeadDim * svd)
-    return set_error("qkv_rope_cache: cache strides do not hold [Hkv, L, D] / [Hkv, D, L]");
+  if (L % 32 != 0 || kv_head_stride < L * kHeadDim)
+    return set_error("qkv_rope_cache: the cache needs L %% 32 == 0 and a head stride of at least L * %d", kHeadDim);
   if (M == 0) return 0;
   if (M > 0x7fffffff) return set_error("qkv_rope_cache: too many tokens");
-  if (!qkv || !cos || !sin || !pos || !slots || !k_cache || !vt_cache || !q_out)
+  if (!qkv || !cos || !sin || !pos || !slots || !k_cache || !v_cache || !q_out)
     return set_error("qkv_rope_cache: null pointer");
   QkvArgs a{};
   a.qkv = static_cast<const char*>(qkv); a.sqkv = sqkv;
   a.qn = static_cast<const char*>(q_norm_w); a.kn = static_cast<const char*>(k_norm_w); a.eps = eps;
   a.cos = static_cast<const char*>(cos); a.sin = static_cast<const char*>(sin); a.scs = scs; a.n_pos = n_pos;
   a.pos = pos; a.slots = slots; a.slots2 = slots2;
-  a.kc = static_cast<char*>(k_cache); a.skh = skh; a.skl = skl;
-  a.vt = static_cast<char*>(vt_cache); a.svh = svh; a.svd = svd; a.L = L;
+  a.kc = static_cast<char*>(k_cache); a.vc = static_cast<char*>(v_cache); a.sh = kv_head_stride; a.L = L;
   a.qo = static_cast<char*>(q_out); a.sqo_m = sqo_m; a.sqo_h = sqo_h;
   a.Hq = (int)Hq; a.Hkv = (int)Hkv;
   const int heads = (int)(Hq + 2 * Hkv);
@@ -795,8 +777,8 @@ extern "C" int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, 
   return attn_plan(M, Hq, Hkv, L_valid).bytes;
 }
 
-extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, int64_t skh,
-                                     int64_t skl, const void* vt_cache, int64_t svh, int64_t svd, int64_t L_cap,
+extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache,
+                                     const void* v_cache, int64_t kv_head_stride, int64_t L_cap,
                                      const uint8_t* mask, int64_t smask, void* out, int64_t so_m, int64_t so_h,
                                      int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid,
                                      const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype,
@@ -807,14 +789,16 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
     return set_error("block_attention: bad sizes (M=%lld Hq=%lld Hkv=%lld L_valid=%lld L_cap=%lld)", (long long)M,
                      (long long)Hq, (long long)Hkv, (long long)L_valid, (long long)L_cap);
   if (M == 0) return 0;
-  if (L_cap % 4 != 0) return set_error("block_attention: the cache slot count must be a multiple of 4");
-  if (!q || !k_cache || !vt_cache || !out) return set_error("block_attention: null pointer");
+  if (L_cap % 32 != 0 || kv_head_stride < L_cap * kHeadDim)
+    return set_error("block_attention: the cache needs L_cap %% 32 == 0 and a head stride of at least L_cap * %d",
+                     kHeadDim);
+  if (L_cap * kHeadDim * 2 > (int64_t)0xFFFFFFF0) return set_error("block_attention: L_cap too large");
+  if (!q || !k_cache || !v_cache || !out) return set_error("block_attention: null pointer");
   const AttnPlan pl = attn_plan(M, Hq, Hkv, L_valid);
   if (pl.rows > 65536) return set_error("block_attention: %d query rows per KV head exceed 65536", pl.rows);
-  // 16-byte loads of q and K rows, 8-byte loads of Vt rows
-  if (!al(q, 16) || (sq_m % 8) || (sq_h % 8) || !al(k_cache, 16) || (skh % 8) || (skl % 8) || !al(vt_cache, 8) ||
-      (svh % 4) || (svd % 4) || svd < L_cap || skl < kHeadDim)
-    return set_error("block_attention: q/K need 16-byte aligned rows and Vt 8-byte aligned rows of >= L_cap slots");
+  // 16-byte loads of q rows and of the K / V tiles
+  if (!al(q, 16) || (sq_m % 8) || (sq_h % 8) || !al(k_cache, 16) || !al(v_cache, 16) || (kv_head_stride % 8))
+    return set_error("block_attention: q rows and the K / V tiles must be 16-byte aligned");
   if (mask != nullptr && (!al(mask, 4) || smask % 4 != 0 || smask < (L_valid + 3) / 4 * 4))
     return set_error("block_attention: mask rows must be 4-byte aligned with at least L_valid rounded up to 4 bytes");
   if (pl.bytes > 0 && (workspace == nullptr || workspace_bytes < pl.bytes || !al(workspace, 16)))
@@ -822,8 +806,8 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
                      (long long)workspace_bytes);
   AttnArgs a{};
   a.q = static_cast<const char*>(q); a.sq_m = sq_m; a.sq_h = sq_h;
-  a.kc = static_cast<const char*>(k_cache); a.skh = skh; a.skl = skl;
-  a.vt = static_cast<const char*>(vt_cache); a.svh = svh; a.svd = svd;
+  a.kc = static_cast<const char*>(k_cache); a.vc = static_cast<const char*>(v_cache);
+  a.sh = kv_head_stride; a.L_cap = L_cap;
   a.mask = mask; a.smask = smask;
   a.lv_dev = valid_len_dev;
   a.M = M; a.n_rep = (int)(Hq / Hkv); a.Hkv = (int)Hkv;
@@ -839,9 +823,9 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
     if (pl.head) {
       char* o = static_cast<char*>(out);
       if (pl.rbw == 2)
-        hipLaunchKernelGGL((attn_head_kernel<DT, 2>), dim3((unsigned)Hkv), dim3(64 * kHeadWaves), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 2, 4>), dim3((unsigned)Hkv), dim3(64 * 4), 0, st, a, o, so_m, so_h);
       else
-        hipLaunchKernelGGL((attn_head_kernel<DT, 1>), dim3((unsigned)Hkv), dim3(64 * kHeadWaves), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 1, 8>), dim3((unsigned)Hkv), dim3(64 * 8), 0, st, a, o, so_m, so_h);
       return;
     }
     if (pl.ksplit) {

@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -55,10 +55,10 @@ SIGNATURES = {
     "simsd_denoise_select": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _i64, _vp, _i64,
                                     _vp, _vp, _vp, _i64, _vp]),
     "simsd_qkv_rope_cache": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
-                                    _vp, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                                    _vp, _vp, _i64, _i64, _vp, _i64, _i64,
                                     _i64, _i64, _i64, _i64, _i32, _vp]),
     "simsd_block_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
-    "simsd_block_attention": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+    "simsd_block_attention": (_i32, [_vp, _i64, _i64, _vp, _vp, _i64, _i64,
                                      _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
                                      _f32, _i32, _vp, _i64, _vp]),
     "simsd_block_mask": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),

@@ -13,11 +13,17 @@ StaticBlockCache, speculative_decoding/cache_aware.py:195-298)::
         ...                                                         #  + cache_position)
     out = F.scaled_dot_product_attention(q, key_cache, value_cache, attn_mask=mask_bool)
 
-Here: ``qkv_rope_cache`` (one launch) and ``block_attention`` (two).  The
-cache (``BlockKVCache``) keeps one copy of each KV head (no per-query-head
-replicas) and stores V transposed, [Hkv, D, L], so the P.V product reads
-contiguous slots; the slot space is the reference's: [0, max_cache_len) the
-permanent cache, [max_cache_len, full_len) the scratch of the current forward.
+Here: ``qkv_rope_cache`` (one launch) and ``block_attention`` (one launch up
+to ``ONE_LAUNCH_SLOTS`` slots for up to 32 query rows per KV head, two beyond:
+chunked partials, then their merge).  The choice follows the host's
+``valid_len`` bound, so a caller replaying graphs over a growing context
+captures one graph per bound (``valid_len_dev`` then lowers it at run time).  The cache
+(``BlockKVCache``) keeps one copy of each KV head (no per-query-head replicas)
+in tiles laid out in the order the attention kernels read them, so every
+wave-wide load covers 1 KB of contiguous memory; ``keys`` / ``values`` /
+``store`` convert to and from the reference's [Hkv, L, D] orientation.  The
+slot space is the reference's: [0, max_cache_len) the permanent cache,
+[max_cache_len, full_len) the scratch of the current forward.
 ``rope_tables`` computes cos/sin exactly as the rotary embedding does
 (modeling_sdar.py:418-435).  Head dim 128; bf16 or fp16.
 """
@@ -28,6 +34,7 @@ import torch
 from . import _native
 
 HEAD_DIM = 128
+ONE_LAUNCH_SLOTS = 1024   # block_attention's one-launch form up to this valid_len
 
 
 def rope_tables(inv_freq: torch.Tensor, n_pos: int, dtype: torch.dtype, attention_scaling: float = 1.0):
@@ -47,10 +54,16 @@ def default_inv_freq(head_dim: int = HEAD_DIM, theta: float = 1000000.0, device=
 
 
 class BlockKVCache:
-    """Static per-layer K [Hkv, L, D] and Vt [Hkv, D, L] buffers (zeroed),
-    L = max_cache_len + max_cur_len rounded up to a multiple of 32.  Slots
-    [0, max_cache_len) hold the committed context, [max_cache_len, L) the
-    scratch of the current forward, as in the reference's StaticBlockCache."""
+    """Static per-layer K and V tiles (zeroed), L = max_cache_len + max_cur_len
+    rounded up to a multiple of 32.  Slots [0, max_cache_len) hold the
+    committed context, [max_cache_len, L) the scratch of the current forward,
+    as in the reference's StaticBlockCache.
+
+    Per layer and KV head, (slot s, dim d) lives at
+      K: ((s/16 * 16 + d/8) * 16 + s%16) * 8 + d%8           ``k_tiles[l]`` [Hkv, L/16, 16, 16, 8]
+      V: ((((s/32 * 8 + d/16) * 16 + d%16) * 4 + s/4%4) * 2 + s/16%2) * 4 + s%4
+                                                              ``v_tiles[l]`` [Hkv, L/32, 8, 16, 4, 2, 4]
+    (the order of the attention kernels' MFMA operand loads)."""
 
     def __init__(self, n_layers: int, n_kv_heads: int, max_cache_len: int, max_cur_len: int,
                  device, dtype=torch.bfloat16, head_dim: int = HEAD_DIM):
@@ -60,21 +73,45 @@ class BlockKVCache:
         self.max_cache_len, self.max_cur_len = max_cache_len, max_cur_len
         self.full_len = (max_cache_len + max_cur_len + 31) // 32 * 32
         self.dtype = dtype
-        self.key_cache = [torch.zeros(n_kv_heads, self.full_len, head_dim, device=device, dtype=dtype)
-                          for _ in range(n_layers)]
-        self.value_cache_t = [torch.zeros(n_kv_heads, head_dim, self.full_len, device=device, dtype=dtype)
-                              for _ in range(n_layers)]
+        L, H = self.full_len, n_kv_heads
+        self.k_tiles = [torch.zeros(H, L // 16, 16, 16, 8, device=device, dtype=dtype) for _ in range(n_layers)]
+        self.v_tiles = [torch.zeros(H, L // 32, 8, 16, 4, 2, 4, device=device, dtype=dtype)
+                        for _ in range(n_layers)]
 
     def __len__(self) -> int:
         return self.n_layers
 
+    @property
+    def head_stride(self) -> int:
+        """Elements per KV head in either tile array."""
+        return self.full_len * self.head_dim
+
     def reset(self) -> None:
-        for t in self.key_cache + self.value_cache_t:
+        for t in self.k_tiles + self.v_tiles:
             t.zero_()
 
-    def value_cache(self, layer: int) -> torch.Tensor:
-        """V of a layer in the reference's [Hkv, L, D] orientation (a view)."""
-        return self.value_cache_t[layer].transpose(1, 2)
+    def keys(self, layer: int) -> torch.Tensor:
+        """K of a layer in the reference's [Hkv, L, D] orientation (a copy)."""
+        H, L, D = self.n_kv_heads, self.full_len, self.head_dim
+        return self.k_tiles[layer].permute(0, 1, 3, 2, 4).reshape(H, L, D)
+
+    def values(self, layer: int) -> torch.Tensor:
+        """V of a layer in the reference's [Hkv, L, D] orientation (a copy)."""
+        H, L, D = self.n_kv_heads, self.full_len, self.head_dim
+        return self.v_tiles[layer].permute(0, 1, 5, 4, 6, 2, 3).reshape(H, L, D)
+
+    def store(self, layer: int, k: torch.Tensor, v: torch.Tensor, start: int = 0) -> None:
+        """Write K and V [Hkv, n, D] (the reference's orientation) at slots
+        [start, start + n) of a layer."""
+        H, L, D = self.n_kv_heads, self.full_len, self.head_dim
+        n = k.shape[1]
+        if k.shape != (H, n, D) or v.shape != (H, n, D) or not 0 <= start <= L - n:
+            raise ValueError(f"store: K/V must be [{H}, n, {D}] within {L} slots")
+        kf, vf = self.keys(layer), self.values(layer)
+        kf[:, start:start + n] = k.to(self.dtype)
+        vf[:, start:start + n] = v.to(self.dtype)
+        self.k_tiles[layer].copy_(kf.view(H, L // 16, 16, 16, 8).permute(0, 1, 3, 2, 4))
+        self.v_tiles[layer].copy_(vf.view(H, L // 32, 2, 4, 4, 8, 16).permute(0, 1, 5, 6, 3, 2, 4))
 
 
 def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weight, eps: float,
@@ -111,7 +148,7 @@ def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weig
     for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
         if t is not None and (t.dtype != qkv.dtype or t.shape != (D,) or t.stride(0) != 1):
             raise ValueError(f"qkv_rope_cache: {name} must be [{D}] in {qkv.dtype}")
-    kc, vt = cache.key_cache[layer], cache.value_cache_t[layer]
+    kc, vc = cache.k_tiles[layer], cache.v_tiles[layer]
     if kc.dtype != qkv.dtype:
         raise TypeError("qkv_rope_cache: cache dtype differs from qkv")
     dev = _native.require_device(qkv, cos, sin, position_ids, slots, slots2, kc, q_norm_weight, k_norm_weight)
@@ -125,7 +162,7 @@ def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weig
             k_norm_weight.data_ptr() if k_norm_weight is not None else None, float(eps),
             cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], position_ids.data_ptr(),
             slots.data_ptr(), slots2.data_ptr() if slots2 is not None else None,
-            kc.data_ptr(), kc.stride(0), kc.stride(1), vt.data_ptr(), vt.stride(0), vt.stride(1), cache.full_len,
+            kc.data_ptr(), vc.data_ptr(), cache.head_stride, cache.full_len,
             q.data_ptr(), q.stride(0), q.stride(1), M, n_q_heads, Hkv, D, code, _native.stream_of(dev))
     _native.check(status, "qkv_rope_cache")
     return q
@@ -170,7 +207,7 @@ def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torc
             pad = torch.zeros((M, max(need, (m8.shape[1] + 3) // 4 * 4)), device=m8.device, dtype=torch.uint8)
             pad[:, :m8.shape[1]].copy_(m8)
             m8 = pad
-    kc, vt = cache.key_cache[layer], cache.value_cache_t[layer]
+    kc, vc = cache.k_tiles[layer], cache.v_tiles[layer]
     if valid_len_dev is not None and (valid_len_dev.dtype != torch.int64 or valid_len_dev.numel() != 1):
         raise ValueError("block_attention: valid_len_dev must be one int64 on the device")
     dev = _native.require_device(q, kc, m8, valid_len_dev)
@@ -184,8 +221,8 @@ def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torc
     ws = torch.empty(max(need, 256), device=dev, dtype=torch.uint8)
     with _native.device_guard(dev):
         status = lib.simsd_block_attention(
-            q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), kc.stride(0), kc.stride(1),
-            vt.data_ptr(), vt.stride(0), vt.stride(1), cache.full_len,
+            q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), cache.head_stride,
+            cache.full_len,
             m8.data_ptr() if m8 is not None else None, m8.stride(0) if m8 is not None else 0,
             out.data_ptr(), out.stride(0), out.stride(1), M, Hq, Hkv, L,
             valid_len_dev.data_ptr() if valid_len_dev is not None else None, D,

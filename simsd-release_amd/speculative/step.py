@@ -37,14 +37,17 @@ rows write their K/V at slots ctx.. in row order (past the committed context,
 so a later forward overwrites them), and each row's mask comes from
 block_mask on the device.  Every forward is a captured HIP graph whose
 per-iteration inputs (ids, positions, slots, mask, valid length) are device
-buffers refreshed before the replay.  One host synchronisation per iteration
-reads the 2 x K x 4 ids the acceptance needs.
+buffers refreshed before the replay.  A forward has one graph per bound on
+the attention's valid length: the one-launch attention's limit while the
+context fits it, the whole cache beyond (the device-side valid length then
+lowers the bound at run time).  One host synchronisation per iteration reads
+the 2 x K x 4 ids the acceptance needs.
 """
 from __future__ import annotations
 
 import torch
 
-from kernels.attention_fused import block_mask
+from kernels.attention_fused import ONE_LAUNCH_SLOTS, block_mask
 from kernels.logits_fused import denoise_select, softmax_argmax
 
 from .model import SynthModel
@@ -63,8 +66,16 @@ def unmask_schedule(n_masks: int, steps: int):
     return out
 
 
+def valid_bound(cache_len: int, end: int) -> int:
+    """Host-side bound on the attention's valid length for a forward whose
+    rows end at slot ``end``: the one-launch attention's limit while the
+    context fits it, otherwise the whole cache."""
+    return ONE_LAUNCH_SLOTS if end <= ONE_LAUNCH_SLOTS < cache_len else cache_len
+
+
 class _Graphed:
-    """A forward captured once over static device buffers."""
+    """A forward captured over static device buffers, one graph per key (the
+    attention's valid-length bound)."""
 
     def __init__(self, rows: int, n_cols: int, device):
         self.ids = torch.zeros(rows, dtype=torch.int64, device=device)
@@ -72,7 +83,7 @@ class _Graphed:
         self.slots = torch.zeros(rows, dtype=torch.int64, device=device)
         self.mask = torch.zeros(rows, (n_cols + 3) // 4 * 4, dtype=torch.bool, device=device)
         self.valid = torch.zeros(1, dtype=torch.int64, device=device)
-        self.graph = None
+        self.graphs, self.outs = {}, {}
 
     def set_span(self, start: int, ctx_len: int, rows: int):
         """Rows at positions/slots start.. (row order); valid = start + rows."""
@@ -81,20 +92,21 @@ class _Graphed:
         self.slots.copy_(ar)
         self.valid.fill_(start + rows)
 
-    def capture(self, body):
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            body()                                   # warm: allocations, lazy init
-        torch.cuda.current_stream().wait_stream(s)
-        torch.cuda.synchronize()
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.out = body()
-
-    def replay(self):
-        self.graph.replay()
-        return self.out
+    def replay(self, key, body):
+        """Replay the graph of ``key``, capturing ``body`` first if needed."""
+        if key not in self.graphs:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                body()                               # warm: allocations, lazy init
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self.outs[key] = body()
+            self.graphs[key] = graph
+        self.graphs[key].replay()
+        return self.outs[key]
 
 
 class SpecRunner:
@@ -151,7 +163,7 @@ class SpecRunner:
         torch.cuda.synchronize()
 
     # ------------------------------------------------------------ graphs
-    def _draft_body(self):
+    def _draft_body(self, bound):
         """ds denoise forwards of one block.  The first carries the prefix
         rows, which writes their K/V; the later ones run the block's rows
         alone, reading the prefix from the cache (the reference re-encodes the
@@ -161,32 +173,28 @@ class SpecRunner:
         self._step_map.fill_(-1)
         for step, n_u in enumerate(self.schedule):
             if step == 0:
-                logits = self.draft.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.draft.cache.full_len,
+                logits = self.draft.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound,
                                             valid_len_dev=g.valid, head_rows=slice(bl, 2 * bl))
             else:
                 logits = self.draft.forward(g.ids[bl:], g.pos[bl:], g.slots[bl:], g.mask[bl:],
-                                            valid_len=self.draft.cache.full_len, valid_len_dev=g.valid)
+                                            valid_len=bound, valid_len_dev=g.valid)
             denoise_select(logits, g.ids[bl:], self.mask_id, n_u, step, self._step_map)
         return None
 
-    def _verify_body(self):
+    def _verify_body(self, bound):
         g = self._vg
-        logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.target.cache.full_len,
-                                     valid_len_dev=g.valid)
+        logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid)
         ids, _ = softmax_argmax(logits)
         return ids
 
-    def _extend_body(self, g):
-        self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=self.target.cache.full_len,
-                            valid_len_dev=g.valid, head=False)
+    def _extend_body(self, g, bound):
+        self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid, head=False)
         return None
 
     def _extend_graph(self, n_blocks: int):
         g = self._eg.get(n_blocks)
         if g is None:
             g = _Graphed(n_blocks * self.bl, self.target.cache.full_len, self.dev)
-            g.set_span(self.ctx, self.ctx, n_blocks * self.bl)
-            g.capture(lambda: self._extend_body(g))
             self._eg[n_blocks] = g
         return g
 
@@ -207,9 +215,8 @@ class SpecRunner:
             g.ids[:bl].copy_(last_block if k == 0 else self.draft_blocks[k - 1])
             g.set_span(start, start, 2 * bl)
             block_mask(dcols, start, start, n_prefix=bl, n_free=bl, out=g.mask)
-            if g.graph is None:
-                g.capture(self._draft_body)
-            g.replay()
+            bound = valid_bound(dcols, start + 2 * bl)
+            g.replay(bound, lambda: self._draft_body(bound))
             self.draft_blocks[k].copy_(g.ids[bl:])
             self.step_maps[k].copy_(self._step_map)
 
@@ -228,12 +235,11 @@ class SpecRunner:
         g.valid.fill_(self.ctx + 2 * K * bl)
         block_mask(self.target.cache.full_len, self.ctx, self.ctx, step_maps=self.step_maps,
                    block_length=bl, block_size=self.ds, out=g.mask)
-        if g.graph is None:
-            g.capture(self._verify_body)
+        bound = valid_bound(self.target.cache.full_len, self.ctx + 2 * K * bl)
         # the verify's inputs are set: later work may overwrite draft_blocks / step_maps
         self._verify_ready = torch.cuda.Event()
         self._verify_ready.record()
-        return g.replay().view(K, 2, bl)[:, 1]
+        return g.replay(bound, lambda: self._verify_body(bound)).view(K, 2, bl)[:, 1]
 
     @torch.inference_mode()
     def extend_(self, blocks):
@@ -248,7 +254,8 @@ class SpecRunner:
             g.ids.copy_(ids.to(self.dev, non_blocking=True))
             g.set_span(self.ctx, self.ctx, n * self.bl)
             block_mask(self.target.cache.full_len, self.ctx, self.ctx, n_prefix=n * self.bl, out=g.mask)
-            g.replay()
+            bound = valid_bound(self.target.cache.full_len, self.ctx + n * self.bl)
+            g.replay(bound, lambda: self._extend_body(g, bound))
             if self.overlap:
                 self._extend_done = torch.cuda.Event()
                 self._extend_done.record(stream)

@@ -47,15 +47,16 @@ def bound(ref):
 def fill_cache(cache, layer, L, seed, dtype=torch.bfloat16):
     k = rnd(cache.n_kv_heads, L, D, dtype=dtype, seed=seed)
     v = rnd(cache.n_kv_heads, L, D, dtype=dtype, seed=seed + 1)
-    cache.key_cache[layer][:, :L].copy_(k)
-    cache.value_cache_t[layer][:, :, :L].copy_(v.transpose(1, 2))
+    cache.store(layer, k, v)
     return k, v
 
 
 @pytest.mark.parametrize("M,Hq,Hkv,L_valid,L_total", [(4, 16, 8, 1000, 1004), (32, 32, 8, 1024, 1056),
                                                       (8, 8, 8, 37, 64), (3, 12, 3, 301, 320),
                                                       (64, 32, 8, 530, 600), (1, 16, 8, 1, 32),
-                                                      (8, 32, 8, 250, 288), (16, 16, 8, 256, 288)])
+                                                      (8, 32, 8, 250, 288), (16, 16, 8, 256, 288),
+                                                      (4, 16, 8, 2048, 2080), (4, 16, 8, 3001, 3040),
+                                                      (8, 32, 8, 2600, 2624), (5, 10, 5, 63, 96)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_block_attention_vs_oracle(M, Hq, Hkv, L_valid, L_total, masked):
     from kernels.attention_fused import BlockKVCache, block_attention
@@ -151,7 +152,7 @@ def test_qkv_rope_cache_vs_oracle(M, Hq, Hkv, norm):
     if not norm:
         qn = kn = None
     cache = BlockKVCache(2, Hkv, 512, 64, DEV)
-    before_k = cache.key_cache[1].clone()
+    before_k = cache.keys(1)
     pos = torch.randperm(4096, device=DEV)[:M]
     perm = torch.randperm(cache.full_len, device=DEV)      # two disjoint slot sets
     slots, slots2 = perm[:M], perm[M:2 * M]
@@ -160,16 +161,17 @@ def test_qkv_rope_cache_vs_oracle(M, Hq, Hkv, norm):
     torch.cuda.synchronize()
     rq, rk, rv = _oracle_qkv(qkv, Hq, Hkv, qn, kn, cos, sin, pos)
     _close_ulp(q.float().cpu().numpy(), rq)
-    kc = cache.key_cache[1].float().cpu().numpy()
-    vt = cache.value_cache_t[1].float().cpu().numpy()
+    kc = cache.keys(1).float().cpu().numpy()
+    vc = cache.values(1).float().cpu().numpy()
     for sl in (slots, slots2):
         s = sl.cpu().numpy()
         _close_ulp(kc[:, s].transpose(1, 0, 2), rk)
-        assert np.array_equal(vt[:, :, s].transpose(2, 0, 1), rv)
+        assert np.array_equal(vc[:, s].transpose(1, 0, 2), rv)
     touched = set(slots.cpu().tolist()) | set(slots2.cpu().tolist())
     untouched = [i for i in range(cache.full_len) if i not in touched]
-    assert torch.equal(cache.key_cache[1][:, untouched], before_k[:, untouched])
-    assert torch.count_nonzero(cache.key_cache[0]) == 0      # other layers untouched
+    assert torch.equal(cache.keys(1)[:, untouched], before_k[:, untouched])
+    assert torch.count_nonzero(cache.values(1)[:, untouched]) == 0
+    assert torch.count_nonzero(cache.k_tiles[0]) == 0 and torch.count_nonzero(cache.v_tiles[0]) == 0
 
 
 def test_qkv_rope_cache_bad_positions_and_slots():
@@ -181,9 +183,10 @@ def test_qkv_rope_cache_bad_positions_and_slots():
     with torch.inference_mode():
         q = qkv_rope_cache(qkv, 8, qn, kn, 1e-6, cos, sin, pos, slots, cache, 0)
     assert torch.count_nonzero(q[1:]) == 0
-    assert torch.count_nonzero(cache.key_cache[0][:, 4]) == 0   # no k write for a bad position
-    assert torch.count_nonzero(cache.value_cache_t[0][:, :, 4]) > 0   # v is still written
-    assert torch.count_nonzero(cache.key_cache[0][:, 3]) > 0
+    assert torch.count_nonzero(cache.keys(0)[:, 4]) == 0   # no k write for a bad position
+    assert torch.count_nonzero(cache.values(0)[:, 4]) > 0   # v is still written
+    assert torch.count_nonzero(cache.keys(0)[:, 3]) > 0
+    assert torch.count_nonzero(cache.keys(0)[:, 5:]) == 0 and torch.count_nonzero(cache.values(0)[:, 5:]) == 0
 
 
 def test_reference_sequence_end_to_end():
@@ -263,6 +266,29 @@ def test_graph_capture_replays():
                                   cache, 0, mask)
             torch.cuda.synchronize()
             assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,L_host,L_dev", [(4, 16, 8, 1500, 700), (16, 16, 8, 1100, 333),
+                                                   (4, 16, 8, 3000, 2500), (4, 16, 8, 900, 0)])
+def test_valid_len_dev_lowers_the_range(M, Hq, Hkv, L_host, L_dev):
+    """A device-side valid length below the host's bound gives the attention
+    over [0, L_dev) (rows see nothing when it is 0), on both the one-launch
+    and the chunked path."""
+    from kernels.attention_fused import BlockKVCache, block_attention
+    print(f"valid_len_dev M={M} L_host={L_host} L_dev={L_dev}", flush=True)
+    cache = BlockKVCache(1, Hkv, L_host, 32, DEV)
+    k, v = fill_cache(cache, 0, L_host, seed=L_dev + 3)
+    q = rnd(M, Hq, D, seed=8)
+    lv = torch.tensor([L_dev], dtype=torch.int64, device=DEV)
+    with torch.inference_mode():
+        out = block_attention(q, cache, 0, valid_len=L_host, valid_len_dev=lv)
+    got = out.view(M, Hq, D).float().cpu().numpy()
+    if L_dev == 0:
+        assert np.all(got == 0)
+        return
+    ref = oatt.attention(q.float().cpu().numpy(), k[:, :L_dev].float().cpu().numpy(),
+                         v[:, :L_dev].float().cpu().numpy(), None, D ** -0.5)
+    assert float(np.abs(got - ref).max()) <= bound(ref)
 
 
 def test_errors():
