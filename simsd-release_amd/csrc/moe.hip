@@ -259,6 +259,121 @@ __global__ __launch_bounds__(kAlignThreads) void moe_route_align_kernel(
   align_from_keys(sm, T * k, E, num_tiles, counts, offsets, pad_offsets, perm, slots, tile_expert);
 }
 
+// Route and align for up to 128 picks (T*k <= 128): the tokens are routed
+// as above, then one wave builds every table with no further barrier -- the
+// picks are 2 keys per lane, the histogram and scans live in that wave's LDS
+// (its LDS operations complete in order), ranks among equal experts come
+// from ballots.  The same tables as align_from_keys.
+constexpr int kSmallAlignSlots = 128;
+
+template <int PL>
+__global__ __launch_bounds__(kAlignThreads) void moe_route_align_small_kernel(
+    const float* __restrict__ logits, int T, int E, int64_t stride_t, int k, int scoring, int renorm,
+    float scale, int64_t* __restrict__ ids, float* __restrict__ wout, int num_tiles,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
+  __shared__ int key_sh[kSmallAlignSlots];
+  __shared__ int off_sh[SIMSD_MOE_MAX_EXPERTS + 1];   // counts, then offsets
+  __shared__ int pad_sh[SIMSD_MOE_MAX_EXPERTS + 1];   // padded offsets
+  __shared__ int h0_sh[SIMSD_MOE_MAX_EXPERTS];        // counts among slots 0..63
+  __shared__ int perm_sh[kSmallAlignSlots];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int t = wv; t < T; t += kAlignThreads / 64) {
+    int pick;
+    float weight;
+    route_token<PL>(logits + (int64_t)t * stride_t, E, k, scoring, renorm, scale, pick, weight);
+    if (lane < k) {
+      ids[(int64_t)t * k + lane] = (int64_t)pick;
+      wout[(int64_t)t * k + lane] = weight;
+      key_sh[t * k + lane] = pick;
+    }
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  const int M = T * k;
+  // lane holds slots lane (key a) and 64 + lane (key b); -1 = no slot
+  const int ka = lane < M ? key_sh[lane] : -1;
+  const int kb = 64 + lane < M ? key_sh[64 + lane] : -1;
+  for (int e = lane; e < E; e += 64) {
+    off_sh[e] = 0;
+    h0_sh[e] = 0;
+  }
+  if (ka >= 0) {
+    atomicAdd(&off_sh[ka], 1);
+    atomicAdd(&h0_sh[ka], 1);
+  }
+  if (kb >= 0) atomicAdd(&off_sh[kb], 1);
+  // exclusive scans of the counts and of the 16-padded counts; lane owns the
+  // experts [lane * EPL, lane * EPL + EPL)
+  const int EPL = (E + 63) / 64;
+  int c_sum = 0, p_sum = 0;
+  for (int q = 0; q < EPL; ++q) {
+    const int e = lane * EPL + q;
+    const int c = e < E ? off_sh[e] : 0;
+    c_sum += c;
+    p_sum += (c + kTile - 1) / kTile * kTile;
+  }
+  int c_inc = c_sum, p_inc = p_sum;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int uc = __shfl_up(c_inc, d), up = __shfl_up(p_inc, d);
+    if (lane >= d) {
+      c_inc += uc;
+      p_inc += up;
+    }
+  }
+  int c_run = c_inc - c_sum, p_run = p_inc - p_sum;
+  for (int q = 0; q < EPL; ++q) {
+    const int e = lane * EPL + q;
+    if (e < E) {
+      const int c = off_sh[e];
+      counts[e] = c;
+      offsets[e] = c_run;
+      pad_offsets[e] = p_run;
+      off_sh[e] = c_run;
+      pad_sh[e] = p_run;
+      c_run += c;
+      p_run += (c + kTile - 1) / kTile * kTile;
+    }
+  }
+  if (lane == 63) {
+    offsets[E] = c_inc;
+    pad_offsets[E] = p_inc;
+    off_sh[E] = c_inc;
+    pad_sh[E] = p_inc;
+  }
+  // stable order by expert: rank among equal keys in slot order
+  int key_bits = 1;
+  while ((1 << key_bits) < E) ++key_bits;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  uint64_t sa = __ballot(ka >= 0), sb = __ballot(kb >= 0);
+  for (int b = 0; b < key_bits; ++b) {
+    const bool ba = (ka >> b) & 1, bb = (kb >> b) & 1;
+    const uint64_t wa = __ballot(ba), wb = __ballot(bb);
+    sa &= ba ? wa : ~wa;
+    sb &= bb ? wb : ~wb;
+  }
+  if (ka >= 0) {
+    const int p = off_sh[ka] + __popcll(sa & lt);
+    perm[p] = lane;
+    perm_sh[p] = lane;
+  }
+  if (kb >= 0) {
+    const int p = off_sh[kb] + h0_sh[kb] + __popcll(sb & lt);
+    perm[p] = 64 + lane;
+    perm_sh[p] = 64 + lane;
+  }
+  // padded slot table and per-tile experts: tile t is expert e's when
+  // pad[e] <= 16 t < pad[e + 1]
+  for (int t = lane; t < num_tiles; t += 64) {
+    const int e = upper_bound_lds(pad_sh + 1, E, t * kTile);
+    tile_expert[t] = e;
+    const int cnt = e < E ? off_sh[e + 1] - off_sh[e] : 0;
+    const int r0 = e < E ? t * kTile - pad_sh[e] : 0;
+    for (int r = 0; r < kTile; ++r)
+      slots[(int64_t)t * kTile + r] = r0 + r < cnt ? perm_sh[off_sh[e] + r0 + r] : -1;
+  }
+}
+
 // ======================================================== grouped FFN ======
 struct MoeArgs {
   const char* x;
@@ -782,6 +897,21 @@ extern "C" int simsd_moe_route_align(const float* logits, int64_t T, int64_t E, 
       (T > 0 && (logits == nullptr || ids_out == nullptr || w_out == nullptr || perm == nullptr)))
     return set_error("moe_route_align: null pointer");
   const dim3 grid(1), block(kAlignThreads);
+  if (T * k <= kSmallAlignSlots && T <= kAlignThreads / 64) {
+    if (E <= 64)
+      hipLaunchKernelGGL((moe_route_align_small_kernel<1>), grid, block, 0, stream, logits, (int)T, (int)E, stride_t,
+                         k, scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets, pad_offsets, perm,
+                         slots, tile_expert);
+    else if (E <= 256)
+      hipLaunchKernelGGL((moe_route_align_small_kernel<4>), grid, block, 0, stream, logits, (int)T, (int)E, stride_t,
+                         k, scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets, pad_offsets, perm,
+                         slots, tile_expert);
+    else
+      hipLaunchKernelGGL((moe_route_align_small_kernel<16>), grid, block, 0, stream, logits, (int)T, (int)E,
+                         stride_t, k, scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets,
+                         pad_offsets, perm, slots, tile_expert);
+    return check_launch("moe_route_align");
+  }
   if (E <= 64)
     hipLaunchKernelGGL((moe_route_align_kernel<1>), grid, block, 0, stream, logits, (int)T, (int)E, stride_t, k,
                        scoring, renorm, scale, ids_out, w_out, num_tiles, counts, offsets, pad_offsets, perm,

@@ -124,7 +124,8 @@ def test_route_align_fused_equals_two_calls(scoring, renorm, scale):
     from kernels.moe_dispatch_fused import moe_align, moe_route, moe_route_align
     g = torch.Generator(device=DEV).manual_seed(21)
     for T, E, k in [(1, 8, 1), (4, 256, 8), (16, 256, 8), (64, 256, 8), (5, 13, 3), (33, 1000, 6),
-                    (1024, 256, 8), (3, 64, 64)]:
+                    (1024, 256, 8), (3, 64, 64), (16, 8, 8), (8, 16, 16), (16, 1024, 8), (2, 4, 4),
+                    (2, 64, 64), (17, 256, 7), (11, 300, 11)]:
         logits = torch.randn(T, E, device=DEV, generator=g)
         ids1, w1 = moe_route(logits, k, scoring=scoring, renorm=renorm, scale=scale)
         al1 = moe_align(ids1, E)
