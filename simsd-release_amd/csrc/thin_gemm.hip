@@ -183,6 +183,11 @@ SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, fl
   }
 }
 
+// statistics passes of the norm prologue issued ahead of the first weights
+#ifndef SIMSD_NORM_EARLY
+#define SIMSD_NORM_EARLY 2
+#endif
+
 template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU, bool NORM>
 __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
@@ -232,23 +237,64 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
     const bool ok = (c0 + s < c_lim) && (k < Kb);
     return buf_load16<kAuxStream>(up ? rA2 : rA, ok ? roff + k : kOob);
   };
-  // with the norm prologue, the first chunk's weights are requested before
-  // the prologue so that their latency overlaps the norm's
+  // activations (token 4c + i4) and gamma of step s of the chunk at c0
+  auto load_b = [&](int c0, int s, int c) {
+    const int c_lim = min(w1, c0 + CH);
+    const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
+    const bool ok = (c0 + s < c_lim) && (k < Kb) && (4 * c + i4 < cols_valid);
+    return buf_load16<kAuxKeep>(rB, ok ? (uint32_t)(4 * c + i4) * sxm_b + k : kOob);
+  };
+  auto load_g = [&](int c0, int s) {
+    const int c_lim = min(w1, c0 + CH);
+    const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
+    return buf_load16<kAuxKeep>(rG, (c0 + s < c_lim) && (k < Kb) ? k : kOob);
+  };
+  // small chunks: the first chunk's activations and gamma are requested with
+  // the statistics, so that they are in registers when the scale is known
+  constexpr bool kPreB = NORM && CH <= 2;
+  u32x4_t B0[kPreB ? CH : 1][MS], G0[kPreB ? CH : 1];
+  // With the norm prologue the statistics loads of the first kNormEarly
+  // passes go out first, then the first chunk's weights, so that the wait for
+  // the statistics (loads complete in issue order) does not also wait for the
+  // weights, whose latency then overlaps the norm.
   u32x4_t A0[NORM ? G : 1][NORM ? CH : 1];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int st = 0; st < CH; ++st) A0[g][st] = load_a(w0, g, st);
-  }
   if constexpr (NORM) {
     rG = make_rsrc(a.gamma, Kb);
     constexpr int MT = 4 * MS;
+    constexpr int kNormEarly = SIMSD_NORM_EARLY;
+    const uint32_t x_stride = 64 * KS * kLaneBytes;
+    const uint32_t x_off = (uint32_t)threadIdx.x * kLaneBytes;
     __shared__ float ssq_red[KS][MT];
     float ssq[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) ssq[j] = 0.f;
-    for (uint32_t off = (uint32_t)threadIdx.x * kLaneBytes; off < Kb; off += 64 * KS * kLaneBytes) {
+    u32x4_t v0[kNormEarly][MT];
+#pragma unroll
+    for (int i = 0; i < kNormEarly; ++i) {
+      const uint32_t off = x_off + i * x_stride;
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        v0[i][j] = buf_load16<kAuxKeep>(rB, (j < cols_valid && off < Kb) ? (uint32_t)j * sxm_b + off : kOob);
+    }
+    if constexpr (kPreB) {
+#pragma unroll
+      for (int st = 0; st < CH; ++st) {
+#pragma unroll
+        for (int c = 0; c < MS; ++c) B0[st][c] = load_b(w0, st, c);
+        G0[st] = load_g(w0, st);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int st = 0; st < CH; ++st) A0[g][st] = load_a(w0, g, st);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kNormEarly; ++i)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) ssq[j] = sumsq8<DT>(v0[i][j], ssq[j]);
+    for (uint32_t off = x_off + kNormEarly * x_stride; off < Kb; off += x_stride) {
       u32x4_t v[MT];
 #pragma unroll
       for (int j = 0; j < MT; ++j) v[j] = buf_load16<kAuxKeep>(rB, j < cols_valid ? (uint32_t)j * sxm_b + off : kOob);
@@ -275,36 +321,28 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
 #pragma unroll
     for (int c = 0; c < MS; ++c) acc[g][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int c0 = w0; c0 < w1; c0 += CH) {
-    const int c_lim = min(w1, c0 + CH);
+  // one chunk: get_b / get_g / get_a give the activations, gamma and weight
+  // operands of step s (token set c, row group g)
+  auto run_chunk = [&](int c0, auto&& get_b, auto&& get_g, auto&& get_a) {
     // activations of this chunk: lane (j, b) holds token 4c+j, k chunk b
     u32x4_t B[CH][MS];
 #pragma unroll
     for (int s = 0; s < CH; ++s) {
-      const uint32_t k = (uint32_t)(c0 + s) * kStep4Bytes + lane_k;
-      const bool ok = (c0 + s < c_lim) && (k < Kb);
 #pragma unroll
-      for (int c = 0; c < MS; ++c) {
-        const bool col_ok = 4 * c + i4 < cols_valid;
-        B[s][c] = buf_load16<kAuxKeep>(rB, (ok && col_ok) ? (uint32_t)(4 * c + i4) * sxm_b + k : kOob);
-      }
+      for (int c = 0; c < MS; ++c) B[s][c] = get_b(c0, s, c);
       if constexpr (NORM) {
-        const u32x4_t gm = buf_load16<kAuxKeep>(rG, ok ? k : kOob);
+        const u32x4_t gm = get_g(c0, s);
 #pragma unroll
         for (int c = 0; c < MS; ++c) B[s][c] = rms_scale8<DT>(B[s][c], gm, rr[c]);
       }
     }
-    const bool pre = NORM && c0 == w0;   // weights already requested before the prologue
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GB) {
       u32x4_t A[GB][CH];
 #pragma unroll
       for (int gg = 0; gg < GB; ++gg)
 #pragma unroll
-        for (int s = 0; s < CH; ++s) {
-          if constexpr (NORM) A[gg][s] = pre ? A0[g0 + gg][s] : load_a(c0, g0 + gg, s);
-          else A[gg][s] = load_a(c0, g0 + gg, s);
-        }
+        for (int s = 0; s < CH; ++s) A[gg][s] = get_a(c0, g0 + gg, s);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int gg = 0; gg < GB; ++gg)
@@ -316,7 +354,26 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
             acc[g0 + gg][c] = Mfma4<DT>::step(hi2(A[gg][s]), hi2(B[s][c]), acc[g0 + gg][c]);
           }
     }
+  };
+  int c0 = w0;
+  if constexpr (NORM) {
+    // the first chunk from what the prologue requested
+    if (c0 < w1) {
+      run_chunk(
+          c0,
+          [&](int cc, int s, int c) {
+            if constexpr (kPreB) return B0[s][c];
+            else return load_b(cc, s, c);
+          },
+          [&](int cc, int s) {
+            if constexpr (kPreB) return G0[s];
+            else return load_g(cc, s);
+          },
+          [&](int, int g, int s) { return A0[g][s]; });
+      c0 += CH;
+    }
   }
+  for (; c0 < w1; c0 += CH) run_chunk(c0, load_b, load_g, load_a);
 
   // sum the 16 k-chunk blocks (lane bits 2..5), then the KS waves in wave
   // order through LDS: red[wave][value][col j]
