@@ -513,7 +513,7 @@ def run_head(args, torch, dev):
 # ──────────────────────────────────────── attention over the static cache ───
 def run_attn(args, torch, dev):
     """Per layer: q/k RMSNorm + RoPE + KV-cache write of the block's rows
-    (one launch), then attention over a 1024-slot context (two launches).
+    (one launch), then attention over a 1024-slot context (one launch).
     attn4: 28 draft layers, 4 rows, 16 query / 8 KV heads; attn32: 36 target
     layers, 32 rows (4 verify blocks), 32 / 8 heads.  The unfused timing is the
     reference's sequence (stock norms, apply_rotary_pos_emb, index_copy_ into

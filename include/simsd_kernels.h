@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 11
+#define SIMSD_ABI_VERSION 12
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -292,7 +292,10 @@ int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, co
  * that lowers L_valid at run time (clamped to [0, L_valid]), so a captured
  * graph can follow a growing context.  q [M, Hq, D] and out [M, Hq, D] with
  * (row, head) strides.  Workspace: simsd_block_attention_workspace_bytes(M, Hq, Hkv,
- * L_valid), 16-byte aligned.  Deterministic. */
+ * L_valid), 16-byte aligned; its first bytes hold arrival counters that must
+ * be zero before the first call on that workspace (allocate it zeroed and
+ * keep it), and every completed call leaves them zero.  Calls that share a
+ * workspace must run in stream order.  Deterministic. */
 int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid);
 
 int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void* k_cache, const void* v_cache,

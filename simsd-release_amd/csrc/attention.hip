@@ -35,6 +35,7 @@
 // head); each keeps an online softmax (running max and sum per row) and writes
 // its unnormalised partial output; attn_combine merges the chunks in chunk
 // order.  Both orders are fixed: bit-reproducible.
+#include <algorithm>
 #include <type_traits>
 
 #include "simsd_common.hpp"
@@ -193,6 +194,7 @@ struct AttnArgs {
   const int64_t* lv_dev;      // device-side valid slot count (<= L_valid) or null
   float* o_part;              // [Hkv][n_chunks][rows_pad][D]
   float2* ml_part;            // [Hkv][n_chunks][rows_pad]
+  unsigned* arrivals;         // [Hkv] workgroups of the split head form done (0 between calls)
 };
 
 // Loads are unconditional -- the caller points an unused lane at a valid
@@ -373,6 +375,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     lv = d < 0 ? 0 : (d < lv ? d : lv);
   }
   const int64_t chunk_lo = (int64_t)chunk_id * a.chunk;
+  if (chunk_lo >= lv) return;   // past the valid length: the merge skips this chunk
   const int64_t chunk_hi = min(lv, chunk_lo + a.chunk);
   const int64_t c_begin = KSPLIT ? min(chunk_hi, chunk_lo + (int64_t)wv * a.wave_chunk) : chunk_lo;
   const int64_t c_end = KSPLIT ? min(chunk_hi, c_begin + a.wave_chunk) : chunk_hi;
@@ -437,32 +440,70 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
 }
 
-// Up to 32 query rows per KV head over a short context: one workgroup per
-// KV head, W waves taking its 32-key steps in turn (step i to wave i % W), so
-// a wave's first step does not depend on the valid length and its loads are
-// issued before that length is read; the next step's loads stay in flight
-// during each step.  The W online-softmax states merge in LDS (fixed wave
-// order) and the normalised rows go straight to the output: one launch, no
-// partials.  W = 8 for one 16-row block, 4 for two.
+// Up to 32 query rows per KV head over a short context: grid (S_max, Hkv),
+// W waves per workgroup.  From the valid length the kernel takes S <= S_max
+// workgroups per KV head (one up to kSplitMin slots, else one 32-key step per
+// wave) and deals the steps out in turn (step i to workgroup (i / W) % S,
+// wave i % W), so a wave's first step does not depend on the valid length and
+// its loads are issued before that length is read; the next step's loads stay
+// in flight during each step.  The W online-softmax states merge in LDS
+// (fixed wave order).  S = 1: the normalised rows go straight to the output.
+// S > 1: each workgroup writes its unnormalised rows and (max, sum) to the
+// workspace, and the last to arrive (an arrival counter per KV head, reset to
+// 0 by that workgroup) merges the S partials in workgroup order.  One launch
+// either way.  W = 8 for one 16-row block, 4 for two.
 #ifndef SIMSD_HEAD_MAX_SLOTS
-#define SIMSD_HEAD_MAX_SLOTS 1024   // measured crossover with the chunked form at 4-8 tokens
+#define SIMSD_HEAD_MAX_SLOTS 4096   // measured: the split head form beats the chunked one up to here
 #endif
 constexpr int kHeadMaxSlots = SIMSD_HEAD_MAX_SLOTS;
+// valid lengths up to which one workgroup per KV head takes all the steps
+// (16 and 32 rows): below them the hand-over costs more than the split saves
+#ifndef SIMSD_HEAD_SPLIT_MIN_SLOTS1
+#define SIMSD_HEAD_SPLIT_MIN_SLOTS1 512
+#endif
+#ifndef SIMSD_HEAD_SPLIT_MIN_SLOTS2
+#define SIMSD_HEAD_SPLIT_MIN_SLOTS2 768
+#endif
+constexpr int kHeadSplitMinSlots1 = SIMSD_HEAD_SPLIT_MIN_SLOTS1;
+constexpr int kHeadSplitMinSlots2 = SIMSD_HEAD_SPLIT_MIN_SLOTS2;
+#ifndef SIMSD_HEAD_SPLIT_SYNC
+#define SIMSD_HEAD_SPLIT_SYNC 1
+#endif
+// Partials passed between the workgroups of a KV head (which may sit on
+// different XCDs, each with its own L2): written through to memory and read
+// past every cache level, so that the hand-over needs no L2 write-back or
+// invalidate, only the stores' completion before the arrival is counted.
+SIMSD_DEV void put_through(float* p, float v) {
+  if (SIMSD_HEAD_SPLIT_SYNC) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  else *p = v;
+}
+SIMSD_DEV float get_through(rsrc_t r, uint32_t off) {
+  return __uint_as_float(buf_load4 < SIMSD_HEAD_SPLIT_SYNC ? kAuxThrough : 0 > (r, off));
+}
+#ifndef SIMSD_HEAD_MAX_SPLIT
+#define SIMSD_HEAD_MAX_SPLIT 8
+#endif
+constexpr int kHeadMaxSplit = SIMSD_HEAD_MAX_SPLIT;   // workgroups per KV head in the split head form
 
 template <int DT, int RBW, int W>
 __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __restrict__ out, int64_t so_m,
                                                            int64_t so_h) {
   constexpr int ROWS = RBW * 16;
+  constexpr int kSplitMin = RBW == 1 ? kHeadSplitMinSlots1 : kHeadSplitMinSlots2;
   constexpr int OSTR = kHeadDim + 4;   // padded rows: the b128 writes of 16 rows spread over the banks
   __shared__ __attribute__((aligned(16))) float o_sh[W][ROWS][OSTR];
   __shared__ float2 ml_sh[W][ROWS];
   __shared__ float wt_sh[W][ROWS];
   __shared__ float l_sh[ROWS];
+  __shared__ float mx_sh[ROWS];
+  __shared__ float wts_sh[kHeadMaxSplit][ROWS];
+  __shared__ int last_sh;
   constexpr int ES = DTypeInfo<DT>::kSize;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int h = blockIdx.x;
+  const int sp = (int)blockIdx.x;
+  const int h = blockIdx.y;
 
   u32x4_t qf[RBW][kDSteps];
   int tok[RBW];
@@ -479,8 +520,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   }
   const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, tok, g, r);
   StepBuf<RBW> bA, bB;
-  constexpr int kStride = W * kKeyStep;
-  int c = wv * kKeyStep;
+  int c = (sp * W + wv) * kKeyStep;
   attn_load<DT, RBW>(a, w, c, bA);   // before the valid length is known
   float m_run[RBW], l_run[RBW];
   f32x4_t acc[RBW][kDTiles];
@@ -497,6 +537,13 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     lv = d < 0 ? 0 : (d < lv ? d : lv);
   }
   const int ce = (int)lv;
+  // workgroups taking part: one up to kSplitMin valid slots, else enough for
+  // a step per wave, at most the grid's; the others have nothing dealt
+  const int S = (gridDim.x == 1 || ce <= kSplitMin)
+                    ? 1
+                    : min((int)gridDim.x, (ce + W * kKeyStep - 1) / (W * kKeyStep));
+  if (sp >= S) return;
+  const int kStride = S * W * kKeyStep;
   // past ce the loads read finite stale slots or zeros and meet p = 0
   while (c < ce) {
     attn_load<DT, RBW>(a, w, c + kStride, bB);
@@ -530,19 +577,91 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
       l += ml.y * wt;
     }
     l_sh[row] = l;
+    mx_sh[row] = mx;
   }
   __syncthreads();
+  auto put = [&](int row, int d, float o, float l) {
+    const int i = row / (int)a.M;
+    const int64_t m = row % (int)a.M;
+    store_elem<DT>(out, m * so_m + (int64_t)(h * a.n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
+  };
+  if (S == 1) {
+    for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
+      const int row = e / kHeadDim, d = e % kHeadDim;
+      if (row >= a.rows) break;
+      float o = 0.f;
+#pragma unroll
+      for (int v = 0; v < W; ++v) o += o_sh[v][row][d] * wt_sh[v][row];
+      put(row, d, o, l_sh[row]);
+    }
+    return;
+  }
+  // this workgroup's partial: [h][sp][row][d] and (max, sum) [h][sp][row]
+  const int64_t pbase = ((int64_t)h * S + sp) * ROWS;
   for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
     const int row = e / kHeadDim, d = e % kHeadDim;
     if (row >= a.rows) break;
     float o = 0.f;
 #pragma unroll
     for (int v = 0; v < W; ++v) o += o_sh[v][row][d] * wt_sh[v][row];
-    const float l = l_sh[row];
-    const int i = row / (int)a.M;
-    const int64_t m = row % (int)a.M;
-    store_elem<DT>(out, m * so_m + (int64_t)(h * a.n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
+    put_through(a.o_part + (pbase + row) * kHeadDim + d, o);
   }
+  if (threadIdx.x < a.rows) {
+    float* ml = reinterpret_cast<float*>(a.ml_part + pbase + threadIdx.x);
+    put_through(ml, mx_sh[threadIdx.x]);
+    put_through(ml + 1, l_sh[threadIdx.x]);
+  }
+  // the partial is in memory before the arrival is counted
+  if (SIMSD_HEAD_SPLIT_SYNC) __builtin_amdgcn_s_waitcnt(0);
+  else __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0)
+    last_sh = __hip_atomic_fetch_add(a.arrivals + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(S - 1);
+  __syncthreads();
+  if (!last_sh) return;
+  if (!SIMSD_HEAD_SPLIT_SYNC) __threadfence();   // every partial of this head is visible here
+  // this head's partials; the loads of workgroups q >= S fall outside the
+  // extent and read 0
+  const int64_t hbase = (int64_t)h * S * ROWS;
+  const rsrc_t rO = make_rsrc(a.o_part + hbase * kHeadDim, (uint32_t)(S * ROWS * kHeadDim * 4));
+  const rsrc_t rML = make_rsrc(a.ml_part + hbase, (uint32_t)(S * ROWS * 8));
+  if (threadIdx.x < a.rows) {
+    const int row = threadIdx.x;
+    float pm[kHeadMaxSplit], pl[kHeadMaxSplit];
+#pragma unroll
+    for (int q = 0; q < kHeadMaxSplit; ++q) {
+      const uint32_t off = q < S ? (uint32_t)(q * ROWS + row) * 8u : kOob;
+      pm[q] = get_through(rML, off);
+      pl[q] = get_through(rML, q < S ? off + 4u : kOob);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kHeadMaxSplit; ++q)
+      if (q < S) mx = fmaxf(mx, pm[q]);
+    float l = 0.f;
+#pragma unroll
+    for (int q = 0; q < kHeadMaxSplit; ++q) {
+      const float wt = (q >= S || pm[q] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[q] - mx);
+      wts_sh[q][row] = wt;
+      l += pl[q] * wt;
+    }
+    l_sh[row] = l;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
+    const int row = e / kHeadDim, d = e % kHeadDim;
+    if (row >= a.rows) break;
+    float v[kHeadMaxSplit];
+#pragma unroll
+    for (int q = 0; q < kHeadMaxSplit; ++q)
+      v[q] = get_through(rO, q < S ? (uint32_t)((q * ROWS + row) * kHeadDim + d) * 4u : kOob);
+    float o = 0.f;
+#pragma unroll
+    for (int q = 0; q < kHeadMaxSplit; ++q) o += v[q] * wts_sh[q][row];
+    put(row, d, o, l_sh[row]);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 constexpr int kMaxChunks = 1024;
@@ -555,8 +674,15 @@ template <int DT>
 __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __restrict__ o_part,
                                                                const float2* __restrict__ ml_part, int n_chunks,
                                                                int rows_pad, int64_t M, int Hq, int n_rep,
-                                                               char* __restrict__ out, int64_t so_m, int64_t so_h) {
+                                                               char* __restrict__ out, int64_t so_m, int64_t so_h,
+                                                               const int64_t* __restrict__ lv_dev, int64_t chunk) {
   constexpr int kBatch = 8;
+  const int64_t head_rows = (int64_t)n_chunks * rows_pad;   // partial rows per KV head
+  // chunks past the device-side valid length were skipped: merge the others
+  if (lv_dev != nullptr) {
+    const int64_t v = *lv_dev;
+    n_chunks = v <= 0 ? 0 : (int)min((int64_t)n_chunks, (v + chunk - 1) / chunk);
+  }
   __shared__ float w_sh[kMaxChunks];
   __shared__ float red[kHeadDim / 64][2];
   const int64_t m = blockIdx.x / Hq;
@@ -565,7 +691,7 @@ __global__ __launch_bounds__(kHeadDim) void attn_combine_kernel(const float* __r
   const int64_t row = (int64_t)i * M + m;
   const int d = threadIdx.x;
   const int lane = d & 63, wv = d >> 6;
-  const int64_t base = (int64_t)h * n_chunks * rows_pad;
+  const int64_t base = (int64_t)h * head_rows;
   // running maxima of the chunks: per thread over its chunks, then the block
   float mx = -INFINITY;
   for (int c = d; c < n_chunks; c += kHeadDim) {
@@ -683,8 +809,9 @@ __global__ __launch_bounds__(256) void block_mask_kernel(uint8_t* __restrict__ m
 struct AttnPlan {
   int rows, rows_pad, rb, rbw, waves, groups, n_chunks;
   bool ksplit, head;
+  int split;                  // head form: workgroups per KV head
   int64_t chunk, wave_chunk;
-  int64_t o_bytes, ml_bytes, bytes;
+  int64_t cnt_bytes, o_bytes, ml_bytes, bytes;
 };
 
 inline int64_t up256(int64_t n) { return (n + 255) / 256 * 256; }
@@ -725,10 +852,22 @@ AttnPlan attn_plan(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
     p.wave_chunk = chunk;
   }
   p.n_chunks = (int)((L + p.chunk - 1) / p.chunk);
-  p.head = p.ksplit && L <= kHeadMaxSlots;   // one launch, no partials
-  p.o_bytes = up256(Hkv * (int64_t)p.n_chunks * p.rows_pad * kHeadDim * 4);
-  p.ml_bytes = up256(Hkv * (int64_t)p.n_chunks * p.rows_pad * 8);
-  p.bytes = p.head ? 0 : p.o_bytes + p.ml_bytes;
+  p.head = p.ksplit && L <= kHeadMaxSlots;   // one launch
+  // head form: the grid holds the workgroups the bound L could use; the
+  // kernel takes as many as the device-side length needs
+  p.split = 1;
+  if (p.head && L > (p.rbw == 2 ? kHeadSplitMinSlots2 : kHeadSplitMinSlots1)) {
+    const int64_t per_wg = (p.rbw == 2 ? 4 : 8) * (int64_t)kKeyStep;
+    p.split = (int)std::min<int64_t>(kHeadMaxSplit, (L + per_wg - 1) / per_wg);
+  }
+  // workspace: [arrival counters][o partials][(max, sum) partials]; the
+  // counters come first in every form so that a workspace shared between
+  // calls keeps them at zero
+  const int64_t parts = p.head ? p.split : p.n_chunks;
+  p.cnt_bytes = up256(Hkv * 4);
+  p.o_bytes = up256(Hkv * parts * p.rows_pad * kHeadDim * 4);
+  p.ml_bytes = up256(Hkv * parts * p.rows_pad * 8);
+  p.bytes = (p.head && p.split == 1) ? 0 : p.cnt_bytes + p.o_bytes + p.ml_bytes;
   return p;
 }
 
@@ -814,18 +953,20 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
   a.L_valid = L_valid; a.chunk = pl.chunk; a.wave_chunk = pl.wave_chunk; a.n_chunks = pl.n_chunks;
   a.scale = scale;
   a.rows = pl.rows; a.rows_pad = pl.rows_pad;
-  a.o_part = static_cast<float*>(workspace);
-  a.ml_part = reinterpret_cast<float2*>(static_cast<char*>(workspace) + pl.o_bytes);
+  a.arrivals = static_cast<unsigned*>(workspace);
+  a.o_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.cnt_bytes);
+  a.ml_part = reinterpret_cast<float2*>(static_cast<char*>(workspace) + pl.cnt_bytes + pl.o_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)pl.n_chunks, (unsigned)Hkv, (unsigned)pl.groups), block(64 * pl.waves);
   auto partial = [&](auto dt_tag) {
     constexpr int DT = decltype(dt_tag)::value;
     if (pl.head) {
       char* o = static_cast<char*>(out);
+      const dim3 hgrid((unsigned)pl.split, (unsigned)Hkv);
       if (pl.rbw == 2)
-        hipLaunchKernelGGL((attn_head_kernel<DT, 2, 4>), dim3((unsigned)Hkv), dim3(64 * 4), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 2, 4>), hgrid, dim3(64 * 4), 0, st, a, o, so_m, so_h);
       else
-        hipLaunchKernelGGL((attn_head_kernel<DT, 1, 8>), dim3((unsigned)Hkv), dim3(64 * 8), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 1, 8>), hgrid, dim3(64 * 8), 0, st, a, o, so_m, so_h);
       return;
     }
     if (pl.ksplit) {
@@ -836,7 +977,8 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
       else hipLaunchKernelGGL((attn_partial_kernel<DT, 1, false>), grid, block, 0, st, a);
     }
     hipLaunchKernelGGL(attn_combine_kernel<DT>, dim3((unsigned)(M * Hq)), dim3(kHeadDim), 0, st, a.o_part,
-                       a.ml_part, pl.n_chunks, pl.rows_pad, M, (int)Hq, a.n_rep, static_cast<char*>(out), so_m, so_h);
+                       a.ml_part, pl.n_chunks, pl.rows_pad, M, (int)Hq, a.n_rep, static_cast<char*>(out), so_m, so_h,
+                       a.lv_dev, pl.chunk);
   };
   if (dtype == kBF16) partial(std::integral_constant<int, kBF16>{});
   else partial(std::integral_constant<int, kF16>{});

@@ -238,9 +238,14 @@ SIMSD_DEV u32x4_t buf_load16(rsrc_t r, uint32_t off) {
 __device__ int32_t simsd_raw_buffer_load_i32(i32x4_t rsrc, int32_t voffset, int32_t soffset, int32_t aux)
     __asm("llvm.amdgcn.raw.buffer.load.i32");
 
+template <int AUX = 0>
 SIMSD_DEV uint32_t buf_load4(rsrc_t r, uint32_t off) {
-  return (uint32_t)simsd_raw_buffer_load_i32(r, (int32_t)off, 0, 0);
+  return (uint32_t)simsd_raw_buffer_load_i32(r, (int32_t)off, 0, AUX);
 }
+
+// sc0 | sc1: a load that misses every cache level (reads what another XCD
+// wrote through to memory)
+constexpr int kAuxThrough = 17;
 
 template <int RB, int CB, int U>
 SIMSD_DEV void load_batch(u32x4_t (&A)[U][RB], u32x4_t (&B)[U][CB], const rsrc_t (&ra)[RB],

@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0

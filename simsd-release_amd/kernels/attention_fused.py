@@ -1,6 +1,6 @@
 """Attention of the speculative step on MI355X: q/k norm, RoPE and the KV
 cache write in one launch, then attention of the block's few query rows over
-the static cache (two launches: chunked partials, then their merge).
+the static cache.
 
 Reference path, per attention layer (speculative_decoding/adapters/base.py:
 161-265 with SDAR's qkv, sdar/modeling_sdar.py:250-262, and the cache class
@@ -13,11 +13,14 @@ StaticBlockCache, speculative_decoding/cache_aware.py:195-298)::
         ...                                                         #  + cache_position)
     out = F.scaled_dot_product_attention(q, key_cache, value_cache, attn_mask=mask_bool)
 
-Here: ``qkv_rope_cache`` (one launch) and ``block_attention`` (one launch up
-to ``ONE_LAUNCH_SLOTS`` slots for up to 32 query rows per KV head, two beyond:
-chunked partials, then their merge).  The choice follows the host's
-``valid_len`` bound, so a caller replaying graphs over a growing context
-captures one graph per bound (``valid_len_dev`` then lowers it at run time).  The cache
+Here: ``qkv_rope_cache`` (one launch) and ``block_attention``.  For up to 32
+query rows per KV head the attention is one launch up to ``ONE_LAUNCH_SLOTS``
+slots: one workgroup per KV head over a short valid length, over a longer one
+several, the last of which merges their partials; two launches past it
+(chunked partials, then their merge).  The form and the chunking follow the
+host's ``valid_len`` bound, so a caller replaying graphs over a growing
+context captures one graph per bound; ``valid_len_dev`` then lowers the
+length at run time, and the kernels trim their work to it.  The cache
 (``BlockKVCache``) keeps one copy of each KV head (no per-query-head replicas)
 in tiles laid out in the order the attention kernels read them, so every
 wave-wide load covers 1 KB of contiguous memory; ``keys`` / ``values`` /
@@ -34,7 +37,7 @@ import torch
 from . import _native
 
 HEAD_DIM = 128
-ONE_LAUNCH_SLOTS = 1024   # block_attention's one-launch form up to this valid_len
+ONE_LAUNCH_SLOTS = 4096   # block_attention's one-launch form up to this valid_len
 
 
 def rope_tables(inv_freq: torch.Tensor, n_pos: int, dtype: torch.dtype, attention_scaling: float = 1.0):
@@ -77,6 +80,24 @@ class BlockKVCache:
         self.k_tiles = [torch.zeros(H, L // 16, 16, 16, 8, device=device, dtype=dtype) for _ in range(n_layers)]
         self.v_tiles = [torch.zeros(H, L // 32, 8, 16, 4, 2, 4, device=device, dtype=dtype)
                         for _ in range(n_layers)]
+        # the attention's workspace: zeroed once, its arrival counters left at
+        # zero by every call; outgrown ones stay referenced (captured graphs
+        # may still use them)
+        self._attn_ws = None
+        self._attn_ws_held = []
+
+    def attention_workspace(self, nbytes: int, device) -> torch.Tensor:
+        """The zero-initialised workspace the attention calls on this cache
+        share (grown outside graph capture only)."""
+        ws = self._attn_ws
+        if ws is None or ws.numel() < nbytes or ws.device != torch.device(device):
+            if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("block_attention: the cache's workspace must be sized before graph capture "
+                                   "(run the same call once outside the capture)")
+            ws = torch.zeros(max(int(nbytes), 4096), device=device, dtype=torch.uint8)
+            self._attn_ws_held.append(ws)
+            self._attn_ws = ws
+        return ws
 
     def __len__(self) -> int:
         return self.n_layers
@@ -218,7 +239,7 @@ def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torc
     need = lib.simsd_block_attention_workspace_bytes(M, Hq, Hkv, L)
     if need < 0:
         _native.check(-1, "block_attention")
-    ws = torch.empty(max(need, 256), device=dev, dtype=torch.uint8)
+    ws = cache.attention_workspace(need, dev)
     with _native.device_guard(dev):
         status = lib.simsd_block_attention(
             q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), cache.head_stride,

@@ -66,11 +66,20 @@ def unmask_schedule(n_masks: int, steps: int):
     return out
 
 
+# attention bounds, one captured graph each, up to the one-launch form's
+# limit (the chunked form sizes its chunks for the bound; the device-side
+# length trims the work of either form)
+GRAPH_BOUNDS = (1024, 2048, ONE_LAUNCH_SLOTS)
+
+
 def valid_bound(cache_len: int, end: int) -> int:
     """Host-side bound on the attention's valid length for a forward whose
-    rows end at slot ``end``: the one-launch attention's limit while the
-    context fits it, otherwise the whole cache."""
-    return ONE_LAUNCH_SLOTS if end <= ONE_LAUNCH_SLOTS < cache_len else cache_len
+    rows end at slot ``end``: the first of ``GRAPH_BOUNDS`` that holds it
+    (below the cache's length), otherwise the whole cache."""
+    for bound in GRAPH_BOUNDS:
+        if end <= bound < cache_len:
+            return bound
+    return cache_len
 
 
 class _Graphed:

@@ -108,6 +108,16 @@ def test_workspace_sizes():
     assert lib.simsd_moe_num_tiles(32, 256) == 32 + 2
     w = lib.simsd_moe_workspace_bytes(64, 8, 2048, 512, 512, 0)
     assert w >= 2 * (512 * 512 + 64 * 512 + 512 * 2048 + 64 * 2048)
+    # attention: one workgroup per KV head needs none; the split head form
+    # needs 256 bytes of arrival counters, then S partials of 16 rows x 128
+    # fp32 and their (max, sum) per KV head (S = 5 at 1200 slots, 8 waves x
+    # 32 keys per workgroup)
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 200) == 0
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 512) == 0
+    assert lib.simsd_block_attention_workspace_bytes(16, 16, 8, 768) == 0      # 32 rows
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 1200) == 256 + 8 * 5 * 16 * 128 * 4 + 8 * 5 * 16 * 8
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 5000) > 256
+    assert lib.simsd_block_attention_workspace_bytes(4, 12, 8, 100) == -1      # 12 q heads over 8 KV heads
 
 
 def test_error_string_round_trip():
@@ -338,3 +348,18 @@ def test_rmsnorm_toggle_host():
     assert torch.equal(model[0](x), x)          # CPU tensors keep the stock forward
     assert apply_rmsnorm_to_model(model, enable=False) == 2
     assert "forward" not in model[0].__dict__
+
+
+def test_attention_graph_bounds_host():
+    """The runner captures one graph per attention bound: steps up to the
+    one-launch form's limit, else the whole cache."""
+    from kernels.attention_fused import ONE_LAUNCH_SLOTS
+    from speculative.step import valid_bound
+    assert ONE_LAUNCH_SLOTS == 4096
+    assert valid_bound(8000, 500) == 1024
+    assert valid_bound(8000, 1024) == 1024
+    assert valid_bound(8000, 1025) == 2048
+    assert valid_bound(8000, 3500) == 4096
+    assert valid_bound(8000, 5000) == 8000
+    assert valid_bound(2000, 1800) == 2000
+    assert valid_bound(700, 600) == 700

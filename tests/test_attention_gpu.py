@@ -2,9 +2,11 @@
 (one launch) and the block attention over the static cache, against the
 oracle on the same inputs and against the reference's own torch sequence.
 
-Both attention forms are covered: up to 32 query rows per KV head over at
-most 256 slots run as one launch (a workgroup per KV head), the rest as
-chunked partials and their merge.
+Every attention form is covered: up to 32 query rows per KV head over at
+most 4096 slots run as one launch -- one workgroup per KV head up to 512 (16
+rows) or 768 (32 rows) valid slots, else several whose partials the last to
+finish merges -- and the rest as chunked partials and a merge launch; a
+device-side valid length below the host's bound trims either form's work.
 
 qkv_rope_cache: q rows and every cache slot written equal the oracle within
 one bf16 unit in the last place (the RMSNorm statistic may round either way;
@@ -56,7 +58,10 @@ def fill_cache(cache, layer, L, seed, dtype=torch.bfloat16):
                                                       (64, 32, 8, 530, 600), (1, 16, 8, 1, 32),
                                                       (8, 32, 8, 250, 288), (16, 16, 8, 256, 288),
                                                       (4, 16, 8, 2048, 2080), (4, 16, 8, 3001, 3040),
-                                                      (8, 32, 8, 2600, 2624), (5, 10, 5, 63, 96)])
+                                                      (8, 32, 8, 2600, 2624), (5, 10, 5, 63, 96),
+                                                      (16, 16, 8, 1024, 1056), (2, 16, 8, 513, 544),
+                                                      (16, 16, 8, 1800, 1856), (4, 16, 8, 4500, 4512),
+                                                      (8, 32, 8, 4200, 4224)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_block_attention_vs_oracle(M, Hq, Hkv, L_valid, L_total, masked):
     from kernels.attention_fused import BlockKVCache, block_attention
@@ -236,17 +241,21 @@ def test_reference_sequence_end_to_end():
     assert err <= 2 ** -7 * float(ref.abs().max()) + 1e-3, err
 
 
-def test_graph_capture_replays():
+@pytest.mark.parametrize("max_cache,n_ctx", [(480, 400), (2016, 900)])
+def test_graph_capture_replays(max_cache, n_ctx):
+    """Replays of a captured norm + RoPE + cache write + attention equal eager
+    calls: one workgroup per KV head (512 slots) and the split form with its
+    arrival counters (2048 slots)."""
     from kernels.attention_fused import BlockKVCache, block_attention, qkv_rope_cache
     M, Hq, Hkv = 4, 16, 8
     qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 2048, seed=50)
-    cache = BlockKVCache(1, Hkv, 992, 32, DEV)
-    fill_cache(cache, 0, 900, seed=51)
-    pos = torch.arange(900, 904, device=DEV)
-    slots = torch.arange(992, 996, device=DEV)
+    cache = BlockKVCache(1, Hkv, max_cache, 32, DEV)
+    fill_cache(cache, 0, n_ctx, seed=51)
+    pos = torch.arange(n_ctx, n_ctx + 4, device=DEV)
+    slots = torch.arange(max_cache, max_cache + 4, device=DEV)
     mask = torch.zeros(M, cache.full_len, dtype=torch.bool, device=DEV)
-    mask[:, :900] = True
-    mask[:, 992:996] = True
+    mask[:, :n_ctx] = True
+    mask[:, max_cache:max_cache + 4] = True
     with torch.inference_mode():
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -269,7 +278,9 @@ def test_graph_capture_replays():
 
 
 @pytest.mark.parametrize("M,Hq,Hkv,L_host,L_dev", [(4, 16, 8, 1500, 700), (16, 16, 8, 1100, 333),
-                                                   (4, 16, 8, 3000, 2500), (4, 16, 8, 900, 0)])
+                                                   (4, 16, 8, 3000, 2500), (4, 16, 8, 900, 0),
+                                                   (4, 16, 8, 1200, 45), (16, 16, 8, 2000, 100),
+                                                   (4, 16, 8, 5000, 4500), (16, 32, 8, 3000, 1000)])
 def test_valid_len_dev_lowers_the_range(M, Hq, Hkv, L_host, L_dev):
     """A device-side valid length below the host's bound gives the attention
     over [0, L_dev) (rows see nothing when it is 0), on both the one-launch
@@ -289,6 +300,34 @@ def test_valid_len_dev_lowers_the_range(M, Hq, Hkv, L_host, L_dev):
     ref = oatt.attention(q.float().cpu().numpy(), k[:, :L_dev].float().cpu().numpy(),
                          v[:, :L_dev].float().cpu().numpy(), None, D ** -0.5)
     assert float(np.abs(got - ref).max()) <= bound(ref)
+
+
+def test_split_head_counters_stay_zero_across_forms():
+    """Calls of every form share the cache's workspace: the split head form's
+    arrival counters are back at zero after each call, and each call repeats
+    its first result bit for bit whatever ran before it."""
+    from kernels.attention_fused import BlockKVCache, block_attention
+    M, Hq, Hkv = 4, 16, 8
+    cache = BlockKVCache(1, Hkv, 4992, 32, DEV)
+    k, v = fill_cache(cache, 0, 5024, seed=70)
+    q = rnd(M, Hq, D, seed=71)
+    first = {}
+    with torch.inference_mode():
+        for rep in range(3):
+            for L in (5000, 1000, 2000, 200, 1500, 5024):
+                print(f"split counters rep={rep} L={L}", flush=True)
+                out = block_attention(q, cache, 0, valid_len=L).clone()
+                torch.cuda.synchronize()
+                counters = cache._attn_ws[:4 * Hkv].view(torch.int32)
+                assert int(counters.abs().sum()) == 0
+                if L not in first:
+                    first[L] = out
+                    ref = oatt.attention(q.float().cpu().numpy(), k[:, :L].float().cpu().numpy(),
+                                         v[:, :L].float().cpu().numpy(), None, D ** -0.5)
+                    got = out.view(M, Hq, D).float().cpu().numpy()
+                    assert float(np.abs(got - ref).max()) <= bound(ref)
+                else:
+                    assert torch.equal(out, first[L])
 
 
 def test_errors():
