@@ -183,6 +183,13 @@ SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, fl
   }
 }
 
+// column sets of 4 tokens up to which the norm runs inside the GEMV (2: the
+// GEMV's whole range; at 8 tokens fused is 1.4-1.5 us faster than norm + GEMV)
+#ifndef SIMSD_NORM_MAX_MS
+#define SIMSD_NORM_MAX_MS 2
+#endif
+constexpr int kNormMaxMs = SIMSD_NORM_MAX_MS;
+
 // statistics passes of the norm prologue issued ahead of the first weights
 #ifndef SIMSD_NORM_EARLY
 #define SIMSD_NORM_EARLY 2
@@ -1008,9 +1015,9 @@ extern "C" int simsd_rmsnorm_thin_linear(const void* x, int64_t sxm, int64_t sxk
   args.bias = static_cast<const char*>(bias); args.sb = sb;
   args.y = static_cast<char*>(y); args.sym = sym; args.syn = syn;
   args.M = M; args.N = N; args.K = K;
-  // the norm runs inside the GEMV up to 4 tokens; beyond that, each
-  // workgroup's statistics pass over all rows costs more than a launch
-  if (pl.fast && pl.kind == 1 && pl.ms == 1 && aligned16(gamma)) {
+  // the norm runs inside the GEMV (up to 8 tokens); the MFMA-tile kernels
+  // above take the normalised rows from a separate launch
+  if (pl.fast && pl.kind == 1 && pl.ms <= kNormMaxMs && aligned16(gamma)) {
     pl.norm = true;
     args.x = static_cast<const char*>(x); args.sxm = sxm;
     args.gamma = static_cast<const char*>(gamma); args.eps = eps;
@@ -1061,7 +1068,7 @@ extern "C" int simsd_rmsnorm_thin_linear_silu_mul(const void* x, int64_t sxm, in
   args.w2 = static_cast<const char*>(w_up); args.sw2n = sun;
   args.y = static_cast<char*>(h); args.sym = shm; args.syn = shn;
   args.M = M; args.N = I; args.K = K;
-  if (pl.fast && pl.kind == 1 && pl.ms == 1 && aligned16(gamma)) {
+  if (pl.fast && pl.kind == 1 && pl.ms <= kNormMaxMs && aligned16(gamma)) {
     pl.norm = true;
     args.x = static_cast<const char*>(x); args.sxm = sxm;
     args.gamma = static_cast<const char*>(gamma); args.eps = eps;

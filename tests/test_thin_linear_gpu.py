@@ -480,7 +480,7 @@ def test_rmsnorm_vs_oracle(dtype):
         assert thin_rmsnorm(x.view(2, 4, 512), w, 1e-5).shape == (2, 4, 512)
 
 
-@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 6, 8, 16, 32])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_rmsnorm_linear_vs_oracle(M, dtype):
     """The fused norm + linear (norm inside the GEMV at M <= 8, a separate
@@ -557,7 +557,7 @@ def test_properties_at_full_size():
             assert torch.equal(thin_linear(x, wt[:, 32:32 + K]), y)           # strided view
 
 
-@pytest.mark.parametrize("M", [1, 4, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 6, 8, 16, 32])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_linear_residual_vs_oracle(M, dtype):
     """residual + x w^T in one launch: bit-exact on small-integer data (every
