@@ -189,6 +189,13 @@ SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, fl
 #define SIMSD_NORM_MAX_MS 2
 #endif
 constexpr int kNormMaxMs = SIMSD_NORM_MAX_MS;
+// Every workgroup of the fused form reads its tokens' whole rows for the
+// statistics.  Past this many bytes of such reads in one call (an lm_head's
+// ~9.5K workgroups read 152 MB at 4 tokens) a separate norm launch is cheaper.
+#ifndef SIMSD_NORM_STATS_BUDGET
+#define SIMSD_NORM_STATS_BUDGET (32ll << 20)
+#endif
+
 
 // statistics passes of the norm prologue issued ahead of the first weights
 #ifndef SIMSD_NORM_EARLY
@@ -583,6 +590,12 @@ constexpr int kMaxSplit = 16;
 
 inline int fast_kind(int64_t M, int dtype) { return dtype == kF32 ? 0 : (M <= 8 ? 1 : 2); }
 
+// the RMSNorm prologue runs inside the GEMV (else: norm launch, plain linear)
+inline bool norm_in_gemv(const ThinPlan& pl, int64_t M, int64_t K, int es) {
+  return pl.fast && pl.kind == 1 && pl.ms <= kNormMaxMs &&
+         pl.tiles_n * pl.split * M * K * es <= SIMSD_NORM_STATS_BUDGET;
+}
+
 // Geometry only (no pointers).  block_n = weight rows per workgroup (0 = the
 // most of 16, 8, 4 that still gives every CU a workgroup); split along K only
 // when even 4-row tiles leave more than half the CUs idle (0 = automatic),
@@ -716,10 +729,21 @@ void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t strea
   else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>, pl, args, stream);
 }
 
+// The big chunk holds CH x (row groups + token sets) operand registers; at 8
+// waves (256 VGPRs a wave) with 16 or more rows, or 8 tokens, it would spill,
+// so those shapes keep the small chunk whatever block_k asks for.
+template <int RW, int MS, int KS>
+constexpr bool kBigChunkFits = !(KS == 8 && (RW >= 16 || MS == 2));
+
 template <int DT, int RW, int MS, int KS, bool GLU, bool NORM>
 void launch_gemv4(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
-  if (pl.ch == 8) launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG, GLU, NORM>(pl, args, stream);
-  else launch_gemv4_ch<DT, RW, MS, KS, 2, GLU, NORM>(pl, args, stream);
+  if constexpr (kBigChunkFits<RW, MS, KS>) {
+    if (pl.ch == 8) {
+      launch_gemv4_ch<DT, RW, MS, KS, SIMSD_GEMV_CH_BIG, GLU, NORM>(pl, args, stream);
+      return;
+    }
+  }
+  launch_gemv4_ch<DT, RW, MS, KS, 2, GLU, NORM>(pl, args, stream);
 }
 
 template <int DT, int RW, int MS, bool GLU, bool NORM>
@@ -1017,7 +1041,7 @@ extern "C" int simsd_rmsnorm_thin_linear(const void* x, int64_t sxm, int64_t sxk
   args.M = M; args.N = N; args.K = K;
   // the norm runs inside the GEMV (up to 8 tokens); the MFMA-tile kernels
   // above take the normalised rows from a separate launch
-  if (pl.fast && pl.kind == 1 && pl.ms <= kNormMaxMs && aligned16(gamma)) {
+  if (norm_in_gemv(pl, M, K, es) && aligned16(gamma)) {
     pl.norm = true;
     args.x = static_cast<const char*>(x); args.sxm = sxm;
     args.gamma = static_cast<const char*>(gamma); args.eps = eps;
@@ -1068,7 +1092,7 @@ extern "C" int simsd_rmsnorm_thin_linear_silu_mul(const void* x, int64_t sxm, in
   args.w2 = static_cast<const char*>(w_up); args.sw2n = sun;
   args.y = static_cast<char*>(h); args.sym = shm; args.syn = shn;
   args.M = M; args.N = I; args.K = K;
-  if (pl.fast && pl.kind == 1 && pl.ms <= kNormMaxMs && aligned16(gamma)) {
+  if (norm_in_gemv(pl, M, K, es) && aligned16(gamma)) {
     pl.norm = true;
     args.x = static_cast<const char*>(x); args.sxm = sxm;
     args.gamma = static_cast<const char*>(gamma); args.eps = eps;

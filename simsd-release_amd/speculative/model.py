@@ -12,7 +12,7 @@ of the real shapes (no checkpoint is available offline).  Each layer runs as
     g   = rmsnorm + gate/up projection + SiLU.mul  (thin_rmsnorm_linear_silu_mul)
     h  += down_proj(g)                             (thin_linear_residual)
 
-and the head is rmsnorm + lm_head (thin_rmsnorm, thin_linear).  A forward
+and the head is rmsnorm + lm_head (thin_rmsnorm_linear).  A forward
 takes its rows' token ids, RoPE positions, cache slots and mask rows, all as
 device tensors, so one captured graph serves every step of a growing context.
 """
@@ -24,8 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from kernels.attention_fused import BlockKVCache, block_attention, default_inv_freq, qkv_rope_cache, rope_tables
-from kernels.thin_linear_fused import (thin_linear, thin_linear_residual, thin_rmsnorm, thin_rmsnorm_linear,
-                                       thin_rmsnorm_linear_silu_mul)
+from kernels.thin_linear_fused import thin_linear_residual, thin_rmsnorm_linear, thin_rmsnorm_linear_silu_mul
 
 
 @dataclass(frozen=True)
@@ -105,4 +104,4 @@ class SynthModel:
             return None
         if head_rows is not None:
             h = h[head_rows]
-        return thin_linear(thin_rmsnorm(h, self.lnf, s.eps), self.lm_head)
+        return thin_rmsnorm_linear(h, self.lnf, s.eps, self.lm_head)
