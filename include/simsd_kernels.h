@@ -113,8 +113,9 @@ int simsd_rmsnorm(const void* x, int64_t stride_xm, const void* gamma, float eps
  * it.  At <= 8 tokens (bf16/fp16, vector-aligned operands, 16-byte aligned
  * gamma) the norm runs inside the GEMV: every workgroup derives its tokens'
  * scale and normalises the activations as it loads them, so the normalised
- * rows never go to memory.  Otherwise the norm is written to the workspace
- * and the linear reads it.  workspace: simsd_rmsnorm_linear_workspace_bytes
+ * rows never go to memory.  Otherwise, or when the workgroups' statistics
+ * reads (workgroups x M x K elements) would pass 32 MB, as for an lm_head,
+ * the norm is written to the workspace and the linear reads it.  workspace: simsd_rmsnorm_linear_workspace_bytes
  * (N_rows = N, or 2*I for the gated form). */
 int64_t simsd_rmsnorm_linear_workspace_bytes(int64_t M, int64_t N_rows, int64_t K, int dtype,
                                              int block_n, int split_k, int num_waves);

@@ -472,7 +472,9 @@ def thin_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> to
 def thin_rmsnorm_linear(x: torch.Tensor, weight: torch.Tensor, eps: float, w: torch.Tensor,
                         bias: torch.Tensor | None = None, config=None, num_warps=None) -> torch.Tensor:
     """``thin_linear(thin_rmsnorm(x, weight, eps), w, bias)``; at <= 8 tokens the
-    norm runs inside the GEMV and the normalised rows never reach memory."""
+    norm runs inside the GEMV and the normalised rows never reach memory
+    (unless the output is lm_head-sized: then every workgroup's statistics
+    pass would cost more than a separate norm launch)."""
     if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad):
         raise RuntimeError("thin_rmsnorm_linear is a forward-only inference kernel")
     if w.ndim != 2 or w.shape[1] != x.shape[-1]:
