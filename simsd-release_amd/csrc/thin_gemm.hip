@@ -538,6 +538,43 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const char* __restrict__ x
 
 // Sum the split partials in split order (fixed: bit-reproducible), add bias,
 // round to the output dtype.  One thread per output element.
+// 16-bit rows with K % 8 == 0 and K <= R * 2048, 16-byte aligned: the 256
+// threads hold the row and gamma in registers (R 16-byte chunks each), so x
+// and gamma are requested once, up front, and the row is read only once.
+constexpr int kNormVecChunk = 256 * 8;   // elements per pass of the workgroup
+
+template <int DT, int R>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const char* __restrict__ x, int64_t sxm,
+                                                          const char* __restrict__ gamma, float eps,
+                                                          char* __restrict__ y, int64_t sym, int64_t K) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  __shared__ float part[4];
+  const int64_t m = blockIdx.x;
+  const uint32_t Kb = (uint32_t)(K * ES);
+  const rsrc_t rX = make_rsrc(x + m * sxm * ES, Kb);
+  const rsrc_t rG = make_rsrc(gamma, Kb);
+  u32x4_t v[R], g[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * kLaneBytes;
+    v[i] = buf_load16<kAuxKeep>(rX, off < Kb ? off : kOob);
+    g[i] = buf_load16<kAuxKeep>(rG, off < Kb ? off : kOob);
+  }
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc = sumsq8<DT>(v[i], acc);
+  const float t = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = t;
+  __syncthreads();
+  const float r = 1.f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)K + eps);
+  char* yr = y + m * sym * ES;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * kLaneBytes;
+    if (off < Kb) *reinterpret_cast<u32x4_t*>(yr + off) = rms_scale8<DT>(v[i], g[i], r);
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restrict__ part, int split,
                                                           int64_t M, int64_t N,
@@ -985,6 +1022,23 @@ int launch_rmsnorm(const void* x, int64_t sxm, const void* gamma, float eps, voi
   const char* xc = static_cast<const char*>(x);
   const char* gc = static_cast<const char*>(gamma);
   char* yc = static_cast<char*>(y);
+  const int64_t es = esize_of(dtype);
+  const bool vec = dtype != kF32 && K % 8 == 0 && K <= 4 * kNormVecChunk && aligned16(x) && aligned16(y) &&
+                   aligned16(gamma) && (sxm * es) % 16 == 0 && (sym * es) % 16 == 0;
+  if (vec) {
+    const int R = (int)cdiv(K, kNormVecChunk);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, 0, stream, xc, sxm, gc, eps, yc, sym, K); };
+    if (dtype == kBF16) {
+      if (R == 1) go(rmsnorm_vec_kernel<kBF16, 1>);
+      else if (R == 2) go(rmsnorm_vec_kernel<kBF16, 2>);
+      else go(rmsnorm_vec_kernel<kBF16, 4>);
+    } else {
+      if (R == 1) go(rmsnorm_vec_kernel<kF16, 1>);
+      else if (R == 2) go(rmsnorm_vec_kernel<kF16, 2>);
+      else go(rmsnorm_vec_kernel<kF16, 4>);
+    }
+    return check_launch("rmsnorm");
+  }
   switch (dtype) {
     case kBF16: hipLaunchKernelGGL(rmsnorm_kernel<kBF16>, grid, block, 0, stream, xc, sxm, gc, eps, yc, sym, K); break;
     case kF16: hipLaunchKernelGGL(rmsnorm_kernel<kF16>, grid, block, 0, stream, xc, sxm, gc, eps, yc, sym, K); break;

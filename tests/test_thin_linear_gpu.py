@@ -468,12 +468,22 @@ def test_rmsnorm_vs_oracle(dtype):
     from kernels.thin_linear_fused import thin_rmsnorm
     tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[dtype]
     ulp = {"bf16": 2.0 ** -7, "fp16": 2.0 ** -10, "fp32": 2.0 ** -20}[dtype]
-    for M, K in [(1, 2048), (4, 2048), (32, 4096), (100, 1000), (3, 77)]:
+    # 16-bit rows with K % 8 == 0 up to 8192 take the register-resident kernel
+    # (1, 2, 3 or 4 chunks of 2048); K=77 and fp32 the element-wise one
+    for M, K in [(1, 2048), (4, 2048), (32, 4096), (100, 1000), (3, 77), (5, 6144), (2, 8192), (3, 8200)]:
         x, w = _norm_case(M, K, tdt, seed=M + K)
         with torch.inference_mode():
             got = thin_rmsnorm(x, w, 1e-6).float().cpu().numpy()
         ref = othin.rmsnorm_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), 1e-6, dtype=dtype)
         assert np.all(np.abs(got - ref) <= 2 * ulp * np.abs(ref) + 1e-30), (M, K)   # 2 ulp: see the oracle test
+    # rows of a wider buffer (16-byte aligned stride, then an odd one)
+    for pad in (16, 3):
+        xb, w = _norm_case(4, 2048 + pad, tdt, seed=pad)
+        x, w = xb[:, :2048], w[:2048].contiguous()
+        with torch.inference_mode():
+            got = thin_rmsnorm(x, w, 1e-6).float().cpu().numpy()
+        ref = othin.rmsnorm_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), 1e-6, dtype=dtype)
+        assert np.all(np.abs(got - ref) <= 2 * ulp * np.abs(ref) + 1e-30), pad
     x, w = _norm_case(8, 512, tdt, seed=3)
     with torch.inference_mode():
         assert torch.equal(thin_rmsnorm(x, w, 1e-5), thin_rmsnorm(x, w, 1e-5))     # deterministic
