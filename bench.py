@@ -598,7 +598,8 @@ def run_attn(args, torch, dev):
                    "context_slots": L, "algorithmic_bytes_per_step": step_bytes, "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qkv_rope_cache + attn_partial + attn_combine per layer"},
+                     "kernel": "qkv_rope_cache + block attention per layer (one attn_head_kernel launch "
+                               "up to 4096 slots, else attn_partial + attn_combine)"},
         "us_per_layer": round(us_fused / L_layers, 3),
         "unfused_us_per_layer": None if us_unfused is None else round(us_unfused / L_layers, 3),
         "fused_speedup": None if us_unfused is None else round(us_unfused / us_fused, 3),
