@@ -19,7 +19,8 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           (thin_linear_silu_mul), then down; also times the unfused sequence.
   layer4 / layer16 / layer32
           the linear path of each decoder layer with the fused epilogues:
-          RMSNorm + qkv, o, RMSNorm + gate/up + SiLU-mul, down (four launches),
+          RMSNorm + qkv, o, RMSNorm + gate/up + SiLU-mul, down (four launches;
+          six above 8 tokens, where each norm is a launch of its own),
           against the unfused sequence with the stock PyTorch RMSNorm.
   head4 / head32
           the lm_head with its epilogue: the draft's denoise step on a 4-token
