@@ -151,3 +151,24 @@ def greedy_match_verify(draft_ids, target_argmax):
         if d != t:
             return list(draft_ids[:pos]) + [t], pos, t
     return list(draft_ids), len(draft_ids), None
+
+
+def accept_blocks(draft_blocks, target_argmax, block_length):
+    """K-block greedy acceptance with first-reject truncation,
+    speculative_decoding/speculative_decode.py:895-953 (greedy verify,
+    partial_block_fill = "draft_argmax"): -> (committed blocks, generated
+    tokens, accepted count).  Block k's final ids come from
+    greedy_match_verify; a short block is padded with the draft's own tokens
+    from len(final) on; the loop stops after the first rejected block."""
+    committed, generated, n_acc = [], [], 0
+    for k in range(len(draft_blocks)):
+        final, n, _bonus = greedy_match_verify(draft_blocks[k], target_argmax[k])
+        n_acc += n
+        block = list(final)
+        if len(block) < block_length:
+            block += list(draft_blocks[k][len(block):block_length])
+        committed.append(block)
+        generated.extend(final)
+        if n < block_length:
+            break
+    return committed, generated, n_acc

@@ -218,9 +218,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 //     (dim 16*dt + r, keys c + 4g .. +4 then c + 16 + 4g .. +4: the A operand
 //      of O^T with the k-slots of P^T)
 // so every load instruction covers 1 KB of contiguous memory.  Slots past the
-// valid range read stale cache values, which are finite (the cache starts
-// zeroed and only takes finite values) and meet p = 0; past L_cap they read
-// as zero.  mask: all M rows.
+// valid range read stale cache values: their scores are replaced by -inf
+// (p = 0) and their V by zeros (attn_step); past L_cap they read as zero.
+// mask: all M rows.
 template <int RBW>
 struct WaveKV {
   rsrc_t rk, rv, rm;
@@ -277,6 +277,24 @@ SIMSD_DEV void attn_step(const AttnArgs& a, const u32x4_t (&qf)[RBW][kDSteps], c
                          const StepBuf<RBW>& b, int c, int c_end, int g, float (&m_run)[RBW],
                          float (&l_run)[RBW], f32x4_t (&acc)[RBW][kDTiles]) {
   const float sl2 = a.scale * kLog2e;
+  // V of keys past the valid length is zeroed in the step that straddles it:
+  // those slots hold whatever an earlier forward left, and an Inf there would
+  // turn p = 0 into 0 * Inf = NaN in the product.  Lane (g, r) holds keys
+  // c + 4g + {0..3} (dwords 0, 1) and c + 16 + 4g + {0..3} (dwords 2, 3),
+  // two per dword, the lower key in the low half.  c and c_end are uniform
+  // across the wave, so the branch is too.
+  u32x4_t vf[kDTiles];
+#pragma unroll
+  for (int dt = 0; dt < kDTiles; ++dt) vf[dt] = b.vf[dt];
+  if (c + 32 > c_end) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k0 = c + 4 * g + (j >> 1) * 16 + (j & 1) * 2;
+      const uint32_t keep = (k0 < c_end ? 0x0000ffffu : 0u) | (k0 + 1 < c_end ? 0xffff0000u : 0u);
+#pragma unroll
+      for (int dt = 0; dt < kDTiles; ++dt) vf[dt][j] &= keep;
+    }
+  }
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) {
     f32x4_t s[2];
@@ -321,7 +339,7 @@ SIMSD_DEV void attn_step(const AttnArgs& a, const u32x4_t (&qf)[RBW][kDSteps], c
     const u32x4_t pf = u32x4_t{pack2<DT>(p[0][0], p[0][1]), pack2<DT>(p[0][2], p[0][3]),
                                pack2<DT>(p[1][0], p[1][1]), pack2<DT>(p[1][2], p[1][3])};
 #pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = Mfma<DT>::step(b.vf[dt], pf, acc[rb][dt]);
+    for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = Mfma<DT>::step(vf[dt], pf, acc[rb][dt]);
   }
 }
 
@@ -380,7 +398,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const int64_t c_begin = KSPLIT ? min(chunk_hi, chunk_lo + (int64_t)wv * a.wave_chunk) : chunk_lo;
   const int64_t c_end = KSPLIT ? min(chunk_hi, c_begin + a.wave_chunk) : chunk_hi;
   // the next step's loads are issued before this step's arithmetic; past
-  // c_end they read zeros (K) or finite stale slots (Vt) and meet p = 0
+  // c_end they read zeros or stale slots, whose p is 0 and V zeroed
   StepBuf<RBW> bA, bB;
   if (c_begin < c_end) {
     const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, tok, g, r);
@@ -466,19 +484,38 @@ constexpr int kHeadMaxSlots = SIMSD_HEAD_MAX_SLOTS;
 #endif
 constexpr int kHeadSplitMinSlots1 = SIMSD_HEAD_SPLIT_MIN_SLOTS1;
 constexpr int kHeadSplitMinSlots2 = SIMSD_HEAD_SPLIT_MIN_SLOTS2;
+// Hand-over of the partials between the workgroups of a KV head (which may
+// sit on different XCDs, each with its own L2):
+//   2  formal: every shared value is a relaxed atomic written through to
+//      memory and read past every cache level, and the arrival counter is a
+//      release fetch_add whose last arriver acquires, so the language's memory
+//      model orders the partials before their reads;
+//   1  the same stores and loads, ordered by the stores' completion
+//      (s_waitcnt) before a relaxed arrival;
+//   0  plain stores and loads with device-scope fences.
 #ifndef SIMSD_HEAD_SPLIT_SYNC
-#define SIMSD_HEAD_SPLIT_SYNC 1
+#define SIMSD_HEAD_SPLIT_SYNC 2
 #endif
-// Partials passed between the workgroups of a KV head (which may sit on
-// different XCDs, each with its own L2): written through to memory and read
-// past every cache level, so that the hand-over needs no L2 write-back or
-// invalidate, only the stores' completion before the arrival is counted.
 SIMSD_DEV void put_through(float* p, float v) {
   if (SIMSD_HEAD_SPLIT_SYNC) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   else *p = v;
 }
-SIMSD_DEV float get_through(rsrc_t r, uint32_t off) {
-  return __uint_as_float(buf_load4 < SIMSD_HEAD_SPLIT_SYNC ? kAuxThrough : 0 > (r, off));
+SIMSD_DEV float get_through(const float* p) {
+  if (SIMSD_HEAD_SPLIT_SYNC) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return *p;
+}
+// Count this workgroup's arrival at KV head h; true in the last to arrive.
+SIMSD_DEV bool arrive_last(unsigned* counter, unsigned n) {
+  if (SIMSD_HEAD_SPLIT_SYNC == 2)
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
+  if (SIMSD_HEAD_SPLIT_SYNC == 1) {
+    __builtin_amdgcn_s_waitcnt(0);   // the partial is in memory before the arrival is counted
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
+  }
+  __threadfence();
+  const bool last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n - 1;
+  __threadfence();
+  return last;
 }
 #ifndef SIMSD_HEAD_MAX_SPLIT
 #define SIMSD_HEAD_MAX_SPLIT 8
@@ -544,7 +581,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
                     : min((int)gridDim.x, (ce + W * kKeyStep - 1) / (W * kKeyStep));
   if (sp >= S) return;
   const int kStride = S * W * kKeyStep;
-  // past ce the loads read finite stale slots or zeros and meet p = 0
+  // past ce the loads read stale slots or zeros: p = 0 and V zeroed
   while (c < ce) {
     attn_load<DT, RBW>(a, w, c + kStride, bB);
     attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
@@ -611,29 +648,28 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     put_through(ml, mx_sh[threadIdx.x]);
     put_through(ml + 1, l_sh[threadIdx.x]);
   }
-  // the partial is in memory before the arrival is counted
-  if (SIMSD_HEAD_SPLIT_SYNC) __builtin_amdgcn_s_waitcnt(0);
-  else __threadfence();
+  // Every thread's stores precede the barrier; thread 0's arrival follows it
+  // (the workgroup barrier orders them at workgroup scope, the arrival's
+  // release extends that to the agent).
   __syncthreads();
-  if (threadIdx.x == 0)
-    last_sh = __hip_atomic_fetch_add(a.arrivals + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              (unsigned)(S - 1);
+  if (threadIdx.x == 0) last_sh = arrive_last(a.arrivals + h, (unsigned)S);
   __syncthreads();
   if (!last_sh) return;
-  if (!SIMSD_HEAD_SPLIT_SYNC) __threadfence();   // every partial of this head is visible here
-  // this head's partials; the loads of workgroups q >= S fall outside the
-  // extent and read 0
-  const int64_t hbase = (int64_t)h * S * ROWS;
-  const rsrc_t rO = make_rsrc(a.o_part + hbase * kHeadDim, (uint32_t)(S * ROWS * kHeadDim * 4));
-  const rsrc_t rML = make_rsrc(a.ml_part + hbase, (uint32_t)(S * ROWS * 8));
+  // this head's partials, workgroup q at [q][row]
+  const float* pO = a.o_part + (int64_t)h * S * ROWS * kHeadDim;
+  const float* pML = reinterpret_cast<const float*>(a.ml_part + (int64_t)h * S * ROWS);
   if (threadIdx.x < a.rows) {
     const int row = threadIdx.x;
     float pm[kHeadMaxSplit], pl[kHeadMaxSplit];
+    // loads are unconditional (workgroups q >= S re-read the last one's) so
+    // that none waits behind a branch; their values are dropped by selects
 #pragma unroll
     for (int q = 0; q < kHeadMaxSplit; ++q) {
-      const uint32_t off = q < S ? (uint32_t)(q * ROWS + row) * 8u : kOob;
-      pm[q] = get_through(rML, off);
-      pl[q] = get_through(rML, q < S ? off + 4u : kOob);
+      const int qq = q < S ? q : S - 1;
+      pm[q] = get_through(pML + (qq * ROWS + row) * 2);
+      pl[q] = get_through(pML + (qq * ROWS + row) * 2 + 1);
+      pm[q] = q < S ? pm[q] : -INFINITY;
+      pl[q] = q < S ? pl[q] : 0.f;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -654,11 +690,10 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     if (row >= a.rows) break;
     float v[kHeadMaxSplit];
 #pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q)
-      v[q] = get_through(rO, q < S ? (uint32_t)((q * ROWS + row) * kHeadDim + d) * 4u : kOob);
+    for (int q = 0; q < kHeadMaxSplit; ++q) v[q] = get_through(pO + ((q < S ? q : S - 1) * ROWS + row) * kHeadDim + d);
     float o = 0.f;
 #pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q) o += v[q] * wts_sh[q][row];
+    for (int q = 0; q < kHeadMaxSplit; ++q) o += q < S ? v[q] * wts_sh[q][row] : 0.f;
     put(row, d, o, l_sh[row]);
   }
   if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

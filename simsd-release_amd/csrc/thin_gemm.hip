@@ -536,8 +536,6 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const char* __restrict__ x
     store_elem<DT>(yr, k, load_elem<DT>(gamma, k) * round_to<DT>(load_elem<DT>(xr, k) * r));
 }
 
-// Sum the split partials in split order (fixed: bit-reproducible), add bias,
-// round to the output dtype.  One thread per output element.
 // 16-bit rows with K % 8 == 0 and K <= R * 2048, 16-byte aligned: the 256
 // threads hold the row and gamma in registers (R 16-byte chunks each), so x
 // and gamma are requested once, up front, and the row is read only once.
@@ -575,6 +573,8 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const char* __restrict
   }
 }
 
+// Sum the split partials in split order (fixed: bit-reproducible), add bias,
+// round to the output dtype.  One thread per output element.
 template <int DT>
 __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restrict__ part, int split,
                                                           int64_t M, int64_t N,

@@ -135,7 +135,7 @@ def moe_route(logits: torch.Tensor, k: int, scoring: str = "softmax", renorm: bo
 
 
 def _grouped_ffn(x, topk_ids, topk_weight, w_gate, w_up, w_down, slots, tile_expert,
-                 shared=None) -> torch.Tensor:
+                 shared=None, out=None) -> torch.Tensor:
     T, H = x.shape
     k = topk_ids.shape[1]
     E, I, Hg = w_gate.shape
@@ -163,7 +163,8 @@ def _grouped_ffn(x, topk_ids, topk_weight, w_gate, w_up, w_down, slots, tile_exp
             raise TypeError("shared expert dtype must match x")
     dev = _native.require_device(x, ids, tw, w_gate, w_up, w_down, slots, tile_expert,
                                  *(t for t in (sg, su, sd) if t is not None))
-    out = torch.empty((T, H), device=dev, dtype=x.dtype)
+    if out is None:
+        out = torch.empty((T, H), device=dev, dtype=x.dtype)
     if T == 0:
         return out
     lib = _native.lib()
@@ -201,9 +202,28 @@ def moe_dispatch(x, topk_ids, topk_weight, w_gate, w_up, w_down):
     if x.ndim != 2 or topk_ids.ndim != 2:
         raise ValueError("x must be (T, H) and topk_ids (T, k)")
     E = w_gate.shape[0]
-    M = topk_ids.numel()
-    slots, tile_expert = _align(topk_ids, E, _num_tiles(M, E))
-    return _grouped_ffn(x, topk_ids, topk_weight, w_gate, w_up, w_down, slots, tile_expert)
+    T, k = topk_ids.shape
+    rows = _chunk_rows(k)
+    if T <= rows:
+        slots, tile_expert = _align(topk_ids, E, _num_tiles(T * k, E))
+        return _grouped_ffn(x, topk_ids, topk_weight, w_gate, w_up, w_down, slots, tile_expert)
+    # More slots than one align workgroup sorts: token chunks of fixed size,
+    # each aligned and dispatched on its own into its rows of one output.
+    # Tokens are independent, so the result equals one dispatch over all T.
+    out = torch.empty((T, x.shape[1]), device=x.device, dtype=x.dtype)
+    for t0 in range(0, T, rows):
+        t1 = min(T, t0 + rows)
+        ids_c = topk_ids[t0:t1]
+        slots, tile_expert = _align(ids_c, E, _num_tiles(ids_c.numel(), E))
+        _grouped_ffn(x[t0:t1], ids_c, topk_weight[t0:t1], w_gate, w_up, w_down, slots,
+                     tile_expert, out=out[t0:t1])
+    return out
+
+
+def _chunk_rows(k: int) -> int:
+    """Tokens per align launch: the single align workgroup sorts at most
+    MOE_MAX_SLOTS slots (T * k)."""
+    return max(1, _native.MOE_MAX_SLOTS // max(int(k), 1))
 
 
 # Up to this many tokens (one per wave of the single workgroup), routing and
@@ -271,41 +291,61 @@ def moe_forward(x, router_logits, k, w_gate, w_up, w_down, shared=None,
     T = router_logits.shape[0]
     if 0 < T <= FUSED_ROUTE_MAX_T and T * k <= _native.MOE_MAX_SLOTS:
         ids, w, al = moe_route_align(router_logits, k, E, scoring=scoring, renorm=renorm, scale=scale)
-        slots, tile_expert = al.slots, al.tile_expert
-    else:
-        ids, w = moe_route(router_logits, k, scoring=scoring, renorm=renorm, scale=scale)
+        return _grouped_ffn(x, ids, w, w_gate, w_up, w_down, al.slots, al.tile_expert, shared=shared)
+    ids, w = moe_route(router_logits, k, scoring=scoring, renorm=renorm, scale=scale)
+    rows = _chunk_rows(k)
+    if T <= rows:
         slots, tile_expert = _align(ids, E, _num_tiles(ids.numel(), E))
-    return _grouped_ffn(x, ids, w, w_gate, w_up, w_down, slots, tile_expert, shared=shared)
+        return _grouped_ffn(x, ids, w, w_gate, w_up, w_down, slots, tile_expert, shared=shared)
+    out = torch.empty((T, x.shape[1]), device=x.device, dtype=x.dtype)
+    for t0 in range(0, T, rows):
+        t1 = min(T, t0 + rows)
+        slots, tile_expert = _align(ids[t0:t1], E, _num_tiles((t1 - t0) * k, E))
+        _grouped_ffn(x[t0:t1], ids[t0:t1], w[t0:t1], w_gate, w_up, w_down, slots, tile_expert,
+                     shared=shared, out=out[t0:t1])
+    return out
 
 
 def stack_expert_weights(experts, free_originals: bool = True):
-    """(E,I,H), (E,I,H), (E,H,I) from an ``nn.ModuleList`` of expert MLPs.
+    """(w_gate (E,I,H), w_up (E,I,H), w_down (E,H,I)) from the experts of an
+    MoE block (an ``nn.ModuleList`` of gate/up/down MLPs), the layout the
+    grouped kernels stream.
 
-    Same behaviour as kernels/moe_dispatch_fused.py:195-217: stacks one
-    projection at a time, and with ``free_originals=True`` (destructive)
-    releases each expert's weight as it goes, so peak extra memory is one
-    projection.  The stacks are contiguous, which is what the 128-bit load path
-    of the grouped kernels wants.
+    Behaviour of kernels/moe_dispatch_fused.py:195-217: one projection is
+    stacked at a time, and with ``free_originals=True`` (destructive) each
+    expert's weight is released as soon as it has been copied, so the extra
+    memory never exceeds one projection's stack.  Each stack is allocated once
+    and filled expert by expert; the result is contiguous.
     """
-    stacked = []
-    for name in ("gate_proj", "up_proj", "down_proj"):
-        w = torch.stack([getattr(e, name).weight.data for e in experts]).contiguous()
-        if free_originals:
-            empty = w.new_empty(0)
-            for e in experts:
-                getattr(e, name).weight.data = empty
-        stacked.append(w)
-    return tuple(stacked)
+    experts = list(experts)
+    if not experts:
+        raise ValueError("stack_expert_weights needs at least one expert")
+    out = []
+    for proj in ("gate_proj", "up_proj", "down_proj"):
+        first = getattr(experts[0], proj).weight.data
+        stack = first.new_empty((len(experts), *first.shape))
+        for e, mlp in enumerate(experts):
+            lin = getattr(mlp, proj)
+            stack[e].copy_(lin.weight.data)
+            if free_originals:
+                lin.weight.data = stack.new_empty(0)
+        out.append(stack)
+    return tuple(out)
 
 
 class FusedMoEDispatch(torch.nn.Module):
-    """nn.Module drop-in mirroring the isolated signature."""
+    """``moe_dispatch`` as a module over stacked expert weights (the
+    reference's isolated-signature wrapper, moe_dispatch_fused.py:220-231).
+    The stacks are buffers that follow ``.to()`` but stay out of the
+    state dict."""
+
+    _NAMES = ("w_gate", "w_up", "w_down")
 
     def __init__(self, w_gate, w_up, w_down):
         super().__init__()
-        self.register_buffer("w_gate", w_gate, persistent=False)
-        self.register_buffer("w_up", w_up, persistent=False)
-        self.register_buffer("w_down", w_down, persistent=False)
+        for name, t in zip(self._NAMES, (w_gate, w_up, w_down)):
+            self.register_buffer(name, t, persistent=False)
 
     def forward(self, x, topk_ids, topk_weight):
-        return moe_dispatch(x, topk_ids, topk_weight, self.w_gate, self.w_up, self.w_down)
+        stacks = [getattr(self, n) for n in self._NAMES]
+        return moe_dispatch(x, topk_ids, topk_weight, *stacks)

@@ -87,33 +87,27 @@ def _cdiv(a: int, b: int) -> int:
 # ─────────────────────────────────────────────────────────────────────────────
 # Workspace (kernels/thin_linear_fused.py:173-190)
 # ─────────────────────────────────────────────────────────────────────────────
-# device -> byte buffer for the fp32 split-K partial tiles, reused without
-# reallocation (the hot path allocates nothing once it has grown).  Calls that
-# share a device are ordered on one stream (a captured graph replays them
-# serially); two streams running split-K calls on one device at once would
-# race on it.
-_PARTIALS: dict[torch.device, torch.Tensor] = {}
-
-
+# Split-K partial tiles (fp32) come from the torch caching allocator, one
+# buffer per call.  The reference keeps one staging buffer per device and
+# reuses it; here draft and target graphs replay on two streams at once (the
+# speculative runner's overlap modes), and a captured graph keeps the address
+# it was recorded with, so a shared buffer would be written by both at the
+# same time.  Allocation per call costs host time only: inside a captured
+# graph it is a fixed address in the graph's pool.
 def _partials(dev: torch.device, nbytes: int) -> torch.Tensor:
-    buf = _PARTIALS.get(dev)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 4096), device=dev, dtype=torch.uint8)
-        _PARTIALS[dev] = buf
-    return buf
+    return torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
 
 
 def _scratch(dev: torch.device, nbytes: int) -> torch.Tensor:
     """A call's own scratch (the normalised rows of the RMSNorm + linear forms,
-    plus their split-K partials), from the caching allocator: nothing is shared
-    between calls, so graphs captured at different sizes and calls on two
-    streams stay independent."""
-    return torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
+    plus their split-K partials)."""
+    return _partials(dev, nbytes)
 
 
 def reset_workspace() -> None:
-    """Drop the staging buffers (call before re-capturing graphs in a new pool)."""
-    _PARTIALS.clear()
+    """Kept for the reference's API (kernels/thin_linear_fused.py:186-190).
+    There is no cached staging buffer to drop: partials are per call."""
+    return None
 
 
 # ─────────────────────────────────────────────────────────────────────────────

@@ -2,7 +2,7 @@
 verified by the target in one cached forward, greedy acceptance.
 
 Mirrors the reference's K-block loop (speculative_decoding/speculative_decode.py:
-840-953 with greedy_match_verify, the fused denoise graphs of
+840-953 with the greedy match of mrs.py:111-146, the fused denoise graphs of
 cache_aware.py:840-1075 and the multi-block verify of verify.py:421-700),
 with the target's verify run against its KV cache: its rows are only the K
 draft blocks (data, mask), not the whole prompt.  Per iteration:
@@ -144,6 +144,8 @@ class SpecRunner:
         self.draft_stream = torch.cuda.Stream(device=self.dev)
         self._extend_done = None
         self._verify_ready = None
+        self._verify_logits = {}      # bound -> the verify graph's logits output
+        self._verify_bound = None
         self._draft_done = None       # optimistic drafts still running on draft_stream
         self._have_next = False       # draft_blocks hold valid drafts for the next iteration
         self.stats = {"optimistic_used": 0, "optimistic_dropped": 0}
@@ -193,6 +195,7 @@ class SpecRunner:
     def _verify_body(self, bound):
         g = self._vg
         logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid)
+        self._verify_logits[bound] = logits
         ids, _ = softmax_argmax(logits)
         return ids
 
@@ -248,7 +251,14 @@ class SpecRunner:
         # the verify's inputs are set: later work may overwrite draft_blocks / step_maps
         self._verify_ready = torch.cuda.Event()
         self._verify_ready.record()
+        self._verify_bound = bound
         return g.replay(bound, lambda: self._verify_body(bound)).view(K, 2, bl)[:, 1]
+
+    @property
+    def last_verify_logits(self) -> torch.Tensor:
+        """Logits [K * 2 * bl, V] of the last verify (rows: block k's data,
+        then its mask rows), valid until the next verify replays."""
+        return self._verify_logits[self._verify_bound]
 
     @torch.inference_mode()
     def extend_(self, blocks):

@@ -282,16 +282,18 @@ def test_apply_moe_to_model_host():
     g0 = root.blk.experts[1].gate_proj.weight.detach().clone()
     assert fused_toggle.apply_moe_to_model(root, True) == 1
     assert fused_toggle.is_moe_applied(root)
-    wg, wu, wd = root.blk._simsd_fused_moe
+    wg, wu, wd = fused_toggle.expert_stacks(root.blk)
     assert wg.shape == (4, 8, 16) and wd.shape == (4, 16, 8)
     assert torch.equal(wg[1], g0)
     assert root.blk.experts[1].gate_proj.weight.numel() == 0        # destructive
     assert fused_toggle.apply_moe_to_model(root, True) == 0          # idempotent
     with pytest.raises(NotImplementedError):
         fused_toggle.apply_moe_to_model(root, False)
-    # unpatched instances keep the stock method
+    # unpatched instances keep the stock method; nothing is patched on the class
     other = LLaDA2MoeSparseMoeBlock()
     assert other.moe_infer(None, None, None) == "stock"
+    assert LLaDA2MoeSparseMoeBlock.moe_infer(other, None, None, None) == "stock"
+    assert fused_toggle.apply_moe_to_model(nn.Module(), False) == 0   # nothing switched: no error
     ex = nn.ModuleList(_Expert(16, 8) for _ in range(3))
     a, b, c = stack_expert_weights(ex, free_originals=False)
     assert a.is_contiguous() and ex[0].gate_proj.weight.numel() == 128
@@ -363,3 +365,40 @@ def test_attention_graph_bounds_host():
     assert valid_bound(8000, 5000) == 8000
     assert valid_bound(2000, 1800) == 2000
     assert valid_bound(700, 600) == 700
+
+
+def test_toggle_warmup_and_ledger_host():
+    """warmup on CPU modules returns without launching anything; the ledger
+    holds the model weakly (a collected model leaves no entry)."""
+    import gc
+    from kernels import fused_toggle
+    m = _Tiny().eval()
+    assert fused_toggle.apply_to_model(m, True) == 2
+    fused_toggle.warmup(m, block_length=4)           # (512, *) shapes are not tuned -> F.linear on CPU
+    assert fused_toggle.is_applied(m)
+    n_before = len(fused_toggle._LINEARS._by_model)
+    del m
+    gc.collect()
+    assert len(fused_toggle._LINEARS._by_model) == n_before - 1
+
+
+def test_accept_blocks_matches_oracle_host():
+    """The runner's acceptance equals the oracle's restatement of the
+    reference's K-block loop on hand cases and random draws."""
+    import random
+    from oracle import verify as over
+    from speculative.verify import accept_blocks
+    cases = [([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 2, 3, 4], [5, 6, 7, 8]]),
+             ([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 2, 9, 4], [5, 6, 7, 8]]),
+             ([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 2, 3, 4], [0, 6, 7, 8]]),
+             ([[1, 2, 3, 4]], [[9, 9, 9, 9]])]
+    rng = random.Random(0)
+    for _ in range(200):
+        K = rng.randint(1, 4)
+        d = [[rng.randint(0, 3) for _ in range(4)] for _ in range(K)]
+        t = [[rng.randint(0, 3) for _ in range(4)] for _ in range(K)]
+        cases.append((d, t))
+    for d, t in cases:
+        assert accept_blocks(d, t, 4) == over.accept_blocks(d, t, 4)
+    assert accept_blocks([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 2, 9, 4], [5, 6, 7, 8]], 4) == \
+        ([[1, 2, 9, 4]], [1, 2, 9], 2)

@@ -102,6 +102,32 @@ def test_block_attention_fp16_and_determinism():
     assert float(np.abs(got - ref).max()) <= bound(ref)
 
 
+@pytest.mark.parametrize("M,Hq,L_valid,L_total", [(4, 16, 900, 960), (32, 32, 1000, 1056),
+                                                  (4, 16, 300, 352), (4, 16, 4500, 4544)])
+def test_block_attention_ignores_nonfinite_slots_past_valid(M, Hq, L_valid, L_total):
+    """Slots past the valid length that hold Inf/NaN (left by an earlier
+    forward that overflowed) do not reach the output: every form (one
+    workgroup per KV head, the split head form, the chunked form) matches the
+    oracle over [0, L_valid) only, as the reference's SDPA does."""
+    from kernels.attention_fused import BlockKVCache, block_attention
+    print(f"nonfinite past valid M={M} Hq={Hq} L={L_valid}", flush=True)
+    Hkv = 8
+    cache = BlockKVCache(1, Hkv, L_total - 32, 32, DEV, dtype=torch.float16)
+    k, v = fill_cache(cache, 0, L_valid, seed=41, dtype=torch.float16)
+    n_bad = cache.full_len - L_valid
+    bad = torch.full((Hkv, n_bad, D), float("inf"), device=DEV, dtype=torch.float16)
+    bad[:, 1::2] = float("nan")
+    cache.store(0, bad, bad, start=L_valid)
+    q = rnd(M, Hq, D, dtype=torch.float16, seed=42)
+    with torch.inference_mode():
+        out = block_attention(q, cache, 0, valid_len=L_valid)
+    torch.cuda.synchronize()
+    got = out.view(M, Hq, D).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    ref = oatt.attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), None, D ** -0.5)
+    assert float(np.abs(got - ref).max()) <= bound(ref)
+
+
 def test_block_attention_matches_torch_sdpa_on_expanded_cache():
     """The reference's SDPA on its GQA-expanded [H_q, L, D] cache with the bool
     mask (adapters/base.py:245-262), computed in fp32 on the device."""
