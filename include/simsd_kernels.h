@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 12
+#define SIMSD_ABI_VERSION 13
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -66,6 +66,24 @@ int simsd_thin_linear(const void* x, int64_t stride_xm, int64_t stride_xk,
                       int64_t M, int64_t N, int64_t K, int dtype,
                       int block_n, int block_k, int split_k, int num_waves,
                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/* simsd_thin_linear without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference: its
+ * thin_linear allocates its partials through _partials().  The split-K
+ * partials go to a static per-GPU array of
+ * simsd_thin_linear_noalloc_max_scratch_bytes() bytes (8 MiB) inside the
+ * library; a call whose plan needs more returns -1 with an error.  Nothing is
+ * allocated and nothing needs clearing (every partial is written before it
+ * is read).  All calls on one GPU share that array: calls that overlap on one
+ * GPU (two streams at once) race.  Results equal simsd_thin_linear's. */
+int simsd_thin_linear_noalloc(const void* x, int64_t stride_xm, int64_t stride_xk,
+                              const void* w, int64_t stride_wn, int64_t stride_wk,
+                              const void* bias, int64_t stride_b,
+                              void* y, int64_t stride_ym, int64_t stride_yn,
+                              int64_t M, int64_t N, int64_t K, int dtype,
+                              int block_n, int block_k, int split_k, int num_waves, void* stream);
+int64_t simsd_thin_linear_noalloc_max_scratch_bytes(void);
 
 /* Workspace bytes simsd_thin_linear needs for this shape/config (0 if none).
  * Plays the role of _partials(), kernels/thin_linear_fused.py:177-185. */

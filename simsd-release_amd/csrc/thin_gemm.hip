@@ -16,6 +16,8 @@
 // partials meet in LDS in fixed wave order.  An explicit split along K
 // (SPLIT > 1) writes fp32 partial tiles and a second launch sums them in split
 // order: deterministic, no atomics, no cross-workgroup synchronisation.
+#include <mutex>
+
 #include "simsd_common.hpp"
 #include "simsd_kernels.h"
 
@@ -928,6 +930,61 @@ extern "C" int simsd_thin_linear(const void* x, int64_t sxm, int64_t sxk, const 
     default: dispatch_dt<kF32>(pl, args, stream); break;
   }
   return check_launch("thin_linear");
+}
+
+// ---------------------------------------------------------- allocation-free
+// simsd_thin_linear_noalloc keeps its split-K partials in this file-scope
+// device array instead of a caller workspace: each GPU the library runs on
+// holds its own copy until the process ends.  In host code the name is a
+// host-side stand-in, not a device address; the per-device address comes from
+// hipGetSymbolAddress, taken once per device with that device current, and
+// only that address is passed to kernels.
+constexpr int64_t kNoAllocScratchBytes = 8ll << 20;   // 8 MiB
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on its first use).
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess) return set_error("thin_linear_noalloc: hipGetDevice failed: %s", hipGetErrorString(ge));
+  if (dev < 0 || dev >= kMaxDevices) return set_error("thin_linear_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error("thin_linear_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+
+extern "C" int64_t simsd_thin_linear_noalloc_max_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int simsd_thin_linear_noalloc(const void* x, int64_t sxm, int64_t sxk, const void* w,
+                                         int64_t swn, int64_t swk, const void* bias, int64_t sb, void* y,
+                                         int64_t sym, int64_t syn, int64_t M, int64_t N, int64_t K,
+                                         int dtype, int block_n, int block_k, int split_k, int num_waves,
+                                         void* stream) {
+  if (M < 0 || N < 0 || K < 0) return set_error("thin_linear_noalloc: negative size");
+  const int64_t need = simsd_thin_linear_workspace_bytes(M, N, K, dtype, block_n, split_k, num_waves);
+  if (need < 0) return -1;
+  if (need > kNoAllocScratchBytes)
+    return set_error("thin_linear_noalloc: this shape and split need %lld bytes of split-K scratch, "
+                     "above the static maximum of %lld bytes (use simsd_thin_linear with a workspace)",
+                     (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (scratch_on_current_device(&ws) != 0) return -1;
+  return simsd_thin_linear(x, sxm, sxk, w, swn, swk, bias, sb, y, sym, syn, M, N, K, dtype, block_n,
+                           block_k, split_k, num_waves, ws, kNoAllocScratchBytes, stream);
 }
 
 extern "C" int simsd_thin_linear_plan(int64_t M, int64_t N, int64_t K, int dtype, int block_n,
