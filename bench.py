@@ -44,6 +44,9 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           H=2048, I=512, T tokens; cycled over 8 distinct layers.
 Each step is captured once in a HIP graph and replayed; the timed region is
 K replays bracketed by synchronisations and HIP events on the replay stream.
+The default run (c2) also times c1, c3m16, c3m32, c4t4, c4t16, c4t64 and c5
+and adds them under "extras" in the same JSON line (--no-extras skips them);
+progress goes to stderr.
 
 value = algorithmic bytes per step / time per step (weights read once +
 activations in + outputs out).  The roofline object is for the dominant
@@ -848,6 +851,8 @@ def main():
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
                              "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default workload only: skip the C1/C3/C4/C5 records that ride along")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; --gpus must be 1 (the hot path "
@@ -885,7 +890,45 @@ def main():
         if not args.no_cpu_baseline:
             result["cpu_baseline"] = cpu_baseline_linear(torch, args.workload, M)
     result["device"] = torch.cuda.get_device_name(dev)
+    if args.workload == "c2" and not args.no_extras:
+        result["extras"] = run_extras(args, torch, dev)
     print(json.dumps(result), flush=True)
+
+
+# The other configurations, timed in the same default run so that every
+# number the metric names has a record from one invocation: C1 (the single
+# gate_up), C3 at 16 and 32 rows, C4 at 4/16/64 tokens and C5 (the
+# speculative step).  Each keeps its own algorithmic bytes, roofline fraction
+# and per-op breakdown; the CPU baseline stays with the headline.
+EXTRA_WORKLOADS = ("c1", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "c5")
+_EXTRA_KEYS = ("value", "unit", "ms_per_step", "steps", "config", "roofline", "breakdown", "tflops",
+               "tokens_per_iteration", "accepted_draft_tokens_per_iteration", "committed_blocks_per_iteration",
+               "phase_ms_per_iteration", "ms_per_iteration_extend_in_line", "ms_per_iteration_pipelined",
+               "hbm_bound_ms_per_iteration")
+
+
+def run_extras(args, torch, dev):
+    out = {}
+    for wl in EXTRA_WORKLOADS:
+        sub = argparse.Namespace(**vars(args))
+        sub.workload = wl
+        sub.steps = 10 if wl == "c5" else max(10, args.steps // 2)
+        sub.warmup = 2 if wl == "c5" else max(2, args.warmup // 2)
+        print(f"bench: extra workload {wl} ({sub.steps} steps)", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
+        if wl == "c5":
+            rec, _ = run_c5(sub, torch, dev)
+        elif wl.startswith("c4"):
+            rec, _ = run_moe(sub, torch, dev)
+        else:
+            rec, _ = run_linear(sub, torch, dev)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        rec = {k: rec[k] for k in _EXTRA_KEYS if k in rec}
+        rec["wall_s"] = round(time.perf_counter() - t0, 1)
+        out[wl] = rec
+        print(f"bench: {wl} {rec['value']} {rec['unit']} in {rec['wall_s']} s", file=sys.stderr, flush=True)
+    return out
 
 
 if __name__ == "__main__":

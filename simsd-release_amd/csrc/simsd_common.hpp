@@ -63,12 +63,23 @@ template <> SIMSD_DEV float load_elem<kF32>(const char* base, int64_t idx) {
   return reinterpret_cast<const float*>(base)[idx];
 }
 
+// fp16 roundings take their operand as a value already rounded to fp32, as
+// torch computes an fp16 op (in fp32, then .to(fp16)).  Without the empty
+// register constraint the compiler may fuse a preceding fp32 multiply or add
+// into the conversion (v_fma_mixlo_f16: one rounding, straight to fp16),
+// which differs from the two roundings in rare cases -- and differently from
+// one kernel to the next, depending on where it applies it.
+SIMSD_DEV float keep_f32(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+
 template <int DT> SIMSD_DEV void store_elem(char* base, int64_t idx, float v);
 template <> SIMSD_DEV void store_elem<kBF16>(char* base, int64_t idx, float v) {
   reinterpret_cast<uint16_t*>(base)[idx] = f32_to_bf16_bits(v);
 }
 template <> SIMSD_DEV void store_elem<kF16>(char* base, int64_t idx, float v) {
-  reinterpret_cast<_Float16*>(base)[idx] = (_Float16)v;
+  reinterpret_cast<_Float16*>(base)[idx] = (_Float16)keep_f32(v);
 }
 template <> SIMSD_DEV void store_elem<kF32>(char* base, int64_t idx, float v) {
   reinterpret_cast<float*>(base)[idx] = v;
@@ -80,7 +91,7 @@ template <int DT> SIMSD_DEV float round_to(float v);
 template <> SIMSD_DEV float round_to<kBF16>(float v) {
   return bf16_bits_to_f32(f32_to_bf16_bits(v));
 }
-template <> SIMSD_DEV float round_to<kF16>(float v) { return (float)(_Float16)v; }
+template <> SIMSD_DEV float round_to<kF16>(float v) { return (float)(_Float16)keep_f32(v); }
 template <> SIMSD_DEV float round_to<kF32>(float v) { return v; }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -94,7 +105,7 @@ template <> SIMSD_DEV float h16_to_f32<kF16>(uint32_t h) {
 template <int DT> SIMSD_DEV uint32_t f32_to_h16(float v);
 template <> SIMSD_DEV uint32_t f32_to_h16<kBF16>(float v) { return f32_to_bf16_bits(v); }
 template <> SIMSD_DEV uint32_t f32_to_h16<kF16>(float v) {
-  return __builtin_bit_cast(uint16_t, (_Float16)v);
+  return __builtin_bit_cast(uint16_t, (_Float16)keep_f32(v));
 }
 
 // RMSNorm of 8 packed 16-bit values: out = dtype(gamma * dtype(x * r)), the
