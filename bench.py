@@ -38,6 +38,10 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           denoise steps, 4 blocks verified per target forward, greedy
           acceptance; value in generated tokens / s.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
+  floor   the floors of one launch: an empty kernel, and the fastest pure
+          read of C1's 48 MiB weight in the GEMV's access pattern over a sweep
+          of rows per workgroup x waves, beside the C1 GEMV on the same 24
+          weights.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
           gate_up + SiLU.mul -> down -> combine, + one shared expert),
@@ -97,11 +101,12 @@ def cpu_model() -> str:
 
 
 def measured_traffic(workload: str):
-    """HBM bytes per launch of the dominant kernel for this workload, as
-    recorded in a committed rocprofv3 PMC summary under profiles/ (FETCH_SIZE
-    + WRITE_SIZE per dispatch, scaled by a plain copy kernel's reading); None
-    when no summary covers the workload."""
-    pat = re.compile(r"^traffic_bytes_per_launch:\s*(\w+)\s*=\s*(\d+)")
+    """HBM bytes per launch of the dominant kernel for this workload (per
+    step for the MoE step, whose roofline is per step), as recorded in a
+    committed rocprofv3 PMC summary under profiles/ (FETCH_SIZE + WRITE_SIZE
+    per dispatch, scaled by a plain copy kernel's reading); None when no
+    summary covers the workload."""
+    pat = re.compile(r"^traffic_bytes_per_(?:launch|step):\s*(\w+)\s*=\s*(\d+)")
     for path in sorted(glob.glob(os.path.join(REPO, "profiles", "*.md"))):
         for line in open(path):
             m = pat.match(line.strip())
@@ -772,8 +777,9 @@ def run_moe(args, torch, dev):
                    "layers_cycled": L, "graph_replays": args.steps, "algorithmic_bytes_per_step": total_bytes // L,
                    "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "moe step (5 launches)"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.workload),
+                     "kernel": "moe step (route+align, gate_up, down, combine; traffic per step)",
+                     "bytes_per_step": total_bytes // L},
     }, T
 
 
@@ -817,6 +823,59 @@ def cpu_baseline_moe(torch, T):
                       f"({med * 1e3:.1f} ms); cpu={cpu_model()}"}
 
 
+def run_floor(args, torch, dev):
+    """The floors of a single launch, in HIP graphs: an empty kernel (what a
+    kernel boundary costs), and a pure read of C1's 48 MiB weight in the
+    GEMV's access pattern (4 rows x 256 B per load, non-temporal) at every
+    rows-per-workgroup x waves geometry, the fastest kept, over 24 distinct
+    weights so the MALL cannot serve repeats; beside it the C1 GEMV on the
+    same weights."""
+    from kernels import _native
+    from kernels.thin_linear_fused import thin_linear
+
+    lib = _native.lib()
+    N, K, M, n_w = 12288, 2048, 4, 24
+    ws = [(torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_w)]
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    sink = torch.zeros(N // 4, dtype=torch.int32, device=dev)
+
+    def empty():
+        _native.check(lib.simsd_probe_empty(_native.stream_of(dev)), "probe_empty")
+
+    def reader(w, rows, waves):
+        return lambda: _native.check(lib.simsd_probe_read(w.data_ptr(), N, K * BF16, rows, waves, sink.data_ptr(),
+                                                          sink.numel(), _native.stream_of(dev)), "probe_read")
+
+    with torch.inference_mode():
+        reps = max(10, args.steps)
+        empty_us = graph_us_per_call(torch, [empty] * 112, reps=reps)
+        sweep = {}
+        for rows in (4, 8, 16):
+            for waves in (1, 2, 4, 8):
+                sweep[f"{rows}x{waves}"] = round(graph_us_per_call(
+                    torch, [reader(w, rows, waves) for w in ws], reps=reps), 3)
+        best = min(sweep, key=sweep.get)
+        read_us = sweep[best]
+        gemv_us = graph_us_per_call(torch, [lambda w=w: thin_linear(x, w) for w in ws], reps=reps)
+    wbytes = N * K * BF16
+    gemv_bytes = linear_bytes(M, K, N)
+    return {
+        "metric": "launch floors: empty-kernel us/launch and 48 MiB read GB/s in a HIP graph",
+        "value": round(wbytes / (read_us * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": reps, "warmup": 1, "ms_per_step": round(read_us * 1e-3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "launch-floors-empty-and-read48MiB", "weights": n_w, "rows": N, "row_bytes": K * BF16,
+                   "best_read_rows_x_waves": best, "parallelism": "single-gpu"},
+        "empty_us_per_launch": round(empty_us, 3),
+        "read_us_per_48MiB": round(read_us, 3),
+        "read_us_by_rows_x_waves": sweep,
+        "read_frac_of_8TBps": round(wbytes / (read_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "c1_gemv_us": round(gemv_us, 3),
+        "c1_gemv_frac_of_8TBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "c1_gemv_over_read": round(gemv_us / read_us, 4),
+    }, M
+
+
 def run_copy(args, torch, dev):
     """A plain 1 GiB device copy (torch's elementwise copy kernel): the known
     byte count that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
@@ -849,7 +908,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy",
+                             "floor"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
@@ -868,6 +928,11 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
+        return
+    if args.workload == "floor":
+        result, _ = run_floor(args, torch, dev)
+        result["device"] = torch.cuda.get_device_name(dev)
+        print(json.dumps(result), flush=True)
         return
     if args.workload == "c5":
         result, _ = run_c5(args, torch, dev)

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 13
+#define SIMSD_ABI_VERSION 14
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -35,6 +35,17 @@ extern "C" {
 
 #define SIMSD_MOE_MAX_EXPERTS 1024
 #define SIMSD_MOE_MAX_SLOTS 8192
+
+/* ---- measurement probes (no reference counterpart) ----------------------
+ * The floors the skinny linear is measured against: an empty launch, and a
+ * pure read of a [rows, row_bytes] matrix in thin_gemv4_kernel's access
+ * pattern (rows_per_wg 4/8/16 rows per workgroup, waves 1/2/4/8 splitting
+ * each row, 4 rows x 256 contiguous bytes per load instruction,
+ * non-temporal), folding what it reads into one 4-byte word per workgroup
+ * (sink: ceil(rows / rows_per_wg) words). */
+int simsd_probe_empty(void* stream);
+int simsd_probe_read(const void* w, int64_t rows, int64_t row_bytes, int rows_per_wg, int waves,
+                     void* sink, int64_t sink_words, void* stream);
 
 /* ---- housekeeping ---------------------------------------------------- */
 int simsd_abi_version(void);

@@ -23,7 +23,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "kernels", "libsimsd_kernels.so")
 
-SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip", "logits.hip", "attention.hip"]
+SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip", "logits.hip", "attention.hip", "probe.hip"]
 ARCH = os.environ.get("SIMSD_OFFLOAD_ARCH", "gfx950")
 
 

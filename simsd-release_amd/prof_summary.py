@@ -4,6 +4,7 @@
     python simsd-release_amd/prof_summary.py stats DIR [--match SUBSTR ...]
     python simsd-release_amd/prof_summary.py pmc DIR [--match SUBSTR ...]
         [--calib DIR --calib-match SUBSTR --calib-bytes N]
+    python simsd-release_amd/prof_summary.py mfma DIR [--match SUBSTR ...] [--stats-dir DIR]
 
 ``stats`` reads ``*_kernel_stats.csv`` (from ``rocprofv3 --kernel-trace
 --stats``) and prints calls / average / min / max per kernel plus the
@@ -111,17 +112,46 @@ def pmc(directory: str, subs, calib=None, calib_subs=None, calib_bytes=0) -> str
     return "\n".join(out)
 
 
+def mfma(directory: str, subs, simds: int, stats_dir=None) -> str:
+    """MFMA utilisation per kernel from a run with SQ_VALU_MFMA_BUSY_CYCLES,
+    GRBM_GUI_ACTIVE and SQ_INSTS_VALU_MFMA_MOPS_BF16: busy MFMA cycles summed
+    over the SIMDs / (GPU-active cycles x SIMDs), the rocprofv3 MfmaUtil
+    formula; with a stats run of the same workload, also the achieved bf16
+    MFMA rate (MOPS x 512 flops per dispatch / average kernel time)."""
+    acc = _pmc_table(directory, subs)
+    avg_ns = {}
+    if stats_dir:
+        for r in _rows(stats_dir, "_kernel_stats.csv"):
+            avg_ns[short_name(r["Name"])] = float(r["AverageNs"])
+    out = [f"{'kernel':<60} {'disp':>5} {'mfma_busy':>12} {'gui_active':>11} {'util_%':>7} {'mfma_flop':>13} "
+           f"{'TFLOP/s':>8}"]
+    for kern in sorted(acc):
+        c = acc[kern]
+        mean = lambda n: sum(c[n]) / len(c[n]) if c.get(n) else float("nan")
+        busy, gui, mops = mean("SQ_VALU_MFMA_BUSY_CYCLES"), mean("GRBM_GUI_ACTIVE"), mean("SQ_INSTS_VALU_MFMA_MOPS_BF16")
+        util = 100.0 * busy / (gui * simds) if gui > 0 else float("nan")
+        flop = mops * 512.0
+        rate = flop / avg_ns[kern] / 1e3 if kern in avg_ns and avg_ns[kern] > 0 else float("nan")
+        n = len(c.get("GRBM_GUI_ACTIVE", []))
+        out.append(f"{kern[:60]:<60} {n:>5} {busy:>12.0f} {gui:>11.0f} {util:>7.2f} {flop:>13.0f} {rate:>8.2f}")
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["stats", "pmc"])
+    ap.add_argument("mode", choices=["stats", "pmc", "mfma"])
     ap.add_argument("dir")
     ap.add_argument("--match", nargs="*", default=[])
     ap.add_argument("--calib")
     ap.add_argument("--calib-match", nargs="*", default=[])
     ap.add_argument("--calib-bytes", type=int, default=0)
+    ap.add_argument("--simds", type=int, default=1024, help="SIMDs on the device (256 CUs x 4 on MI355X)")
+    ap.add_argument("--stats-dir", help="mfma: a --kernel-trace --stats run of the same workload")
     a = ap.parse_args()
     if a.mode == "stats":
         print(stats(a.dir, a.match))
+    elif a.mode == "mfma":
+        print(mfma(a.dir, a.match, a.simds, a.stats_dir))
     else:
         print(pmc(a.dir, a.match, a.calib, a.calib_match, a.calib_bytes))
 
