@@ -521,6 +521,12 @@ SIMSD_DEV bool arrive_last(unsigned* counter, unsigned n) {
 #define SIMSD_HEAD_MAX_SPLIT 8
 #endif
 constexpr int kHeadMaxSplit = SIMSD_HEAD_MAX_SPLIT;   // workgroups per KV head in the split head form
+// waves per workgroup of the split head form: one 16-row block, two
+#ifndef SIMSD_HEAD_W1
+#define SIMSD_HEAD_W1 8
+#endif
+constexpr int kHeadW1 = SIMSD_HEAD_W1;
+constexpr int kHeadW2 = 4;
 
 template <int DT, int RBW, int W>
 __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __restrict__ out, int64_t so_m,
@@ -655,14 +661,25 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   if (threadIdx.x == 0) last_sh = arrive_last(a.arrivals + h, (unsigned)S);
   __syncthreads();
   if (!last_sh) return;
-  // this head's partials, workgroup q at [q][row]
+  // this head's partials, workgroup q at [q][row].  The partial rows and the
+  // (max, sum) pairs are all loaded before any is used, so the merge waits
+  // for one round trip.  Loads are unconditional (workgroups q >= S re-read
+  // the last one's; rows past a.rows read the workspace's row padding) so that
+  // none waits behind a branch; unused values are dropped by selects.
+  constexpr int kPerThread = ROWS * kHeadDim / (64 * W);
   const float* pO = a.o_part + (int64_t)h * S * ROWS * kHeadDim;
   const float* pML = reinterpret_cast<const float*>(a.ml_part + (int64_t)h * S * ROWS);
+  float v[kPerThread][kHeadMaxSplit];
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;
+    const int row = e / kHeadDim, d = e % kHeadDim;
+#pragma unroll
+    for (int q = 0; q < kHeadMaxSplit; ++q) v[i][q] = get_through(pO + ((q < S ? q : S - 1) * ROWS + row) * kHeadDim + d);
+  }
   if (threadIdx.x < a.rows) {
     const int row = threadIdx.x;
     float pm[kHeadMaxSplit], pl[kHeadMaxSplit];
-    // loads are unconditional (workgroups q >= S re-read the last one's) so
-    // that none waits behind a branch; their values are dropped by selects
 #pragma unroll
     for (int q = 0; q < kHeadMaxSplit; ++q) {
       const int qq = q < S ? q : S - 1;
@@ -685,16 +702,16 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     l_sh[row] = l;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;
     const int row = e / kHeadDim, d = e % kHeadDim;
-    if (row >= a.rows) break;
-    float v[kHeadMaxSplit];
+    if (row < a.rows) {
+      float o = 0.f;
 #pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q) v[q] = get_through(pO + ((q < S ? q : S - 1) * ROWS + row) * kHeadDim + d);
-    float o = 0.f;
-#pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q) o += q < S ? v[q] * wts_sh[q][row] : 0.f;
-    put(row, d, o, l_sh[row]);
+      for (int q = 0; q < kHeadMaxSplit; ++q) o += q < S ? v[i][q] * wts_sh[q][row] : 0.f;
+      put(row, d, o, l_sh[row]);
+    }
   }
   if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -892,7 +909,7 @@ AttnPlan attn_plan(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
   // kernel takes as many as the device-side length needs
   p.split = 1;
   if (p.head && L > (p.rbw == 2 ? kHeadSplitMinSlots2 : kHeadSplitMinSlots1)) {
-    const int64_t per_wg = (p.rbw == 2 ? 4 : 8) * (int64_t)kKeyStep;
+    const int64_t per_wg = (p.rbw == 2 ? kHeadW2 : kHeadW1) * (int64_t)kKeyStep;
     p.split = (int)std::min<int64_t>(kHeadMaxSplit, (L + per_wg - 1) / per_wg);
   }
   // workspace: [arrival counters][o partials][(max, sum) partials]; the
@@ -999,9 +1016,9 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
       char* o = static_cast<char*>(out);
       const dim3 hgrid((unsigned)pl.split, (unsigned)Hkv);
       if (pl.rbw == 2)
-        hipLaunchKernelGGL((attn_head_kernel<DT, 2, 4>), hgrid, dim3(64 * 4), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 2, kHeadW2>), hgrid, dim3(64 * kHeadW2), 0, st, a, o, so_m, so_h);
       else
-        hipLaunchKernelGGL((attn_head_kernel<DT, 1, 8>), hgrid, dim3(64 * 8), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 1, kHeadW1>), hgrid, dim3(64 * kHeadW1), 0, st, a, o, so_m, so_h);
       return;
     }
     if (pl.ksplit) {
