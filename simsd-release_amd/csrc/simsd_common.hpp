@@ -489,6 +489,15 @@ SIMSD_DEV void accum_lds_ab(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB]
   }
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every global load the wave has in flight, which drains a
+// prefetch issued ahead of the barrier; these fences are scoped to LDS.
+SIMSD_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum the per-wave accumulators of KS waves that split the reduction, in a
 // fixed wave order (bit-reproducible).  Wave 0 ends up with the total.
 template <int KS, int NFRAG>

@@ -513,6 +513,179 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// 9..32 tokens, wide row tiles: the waves of a workgroup split its weight rows
+// (wave w owns rows [16 RB w, 16 RB (w + 1)) of the tile, or, gated, 16 gate
+// rows and the same 16 up rows) instead of K, so every wave needs the same
+// activation chunk.  The workgroup loads each batch of U 256-byte activation
+// chunks once -- its waves share the load instructions -- into one of two LDS
+// slots, and all waves read their B operands from it; one barrier per batch
+// (the double buffer makes the slot written next one that every wave has
+// finished reading).  Each wave's weight chunks go through its own LDS tile as
+// in accum_lds.  Activation bytes from L2 per weight byte: CB * 16 / (16 RB KS)
+// instead of CB * 16 / (16 RB) -- a quarter at 128 rows.  No cross-wave sum:
+// each wave writes its own outputs.
+template <int DT, int RB, int CB, int KS, int U, bool PARTIAL, bool GLU>
+__global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(ThinArgs a) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  static_assert(!GLU || RB == 2, "gated: block 0 = gate rows, block 1 = the same rows of up");
+  constexpr int WROWS = 16 * RB;                  // weight rows per wave
+  constexpr int WOUT = GLU ? 16 : WROWS;          // output columns per wave
+  constexpr int XROWS = 16 * CB;                  // activation rows (tokens) per tile
+  constexpr int kXLoads = U * CB * 4;             // 4-row load instructions per activation batch
+  constexpr int kXPer = (kXLoads + KS - 1) / KS;  // ... per wave
+  constexpr int kSlot = U * XROWS * kLdsRow;
+  __shared__ __attribute__((aligned(16))) char xs[2 * kSlot];
+  __shared__ __attribute__((aligned(16))) char wt[KS * WROWS * kLdsRow];
+  const int lane = threadIdx.x & 63;
+  // wave-uniform (the weight descriptors depend on it: a per-lane value would
+  // put every buffer load in a readfirstlane loop)
+  const int wk = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int g = lane >> 4, r = lane & 15;       // MFMA operand layout
+  const int lr = lane >> 4, lc = lane & 15;     // loader layout: row l/16 of 4, chunk l%16
+  const int64_t n_tile = (int64_t)blockIdx.x * (KS * WOUT);
+  const int64_t n_wave = n_tile + (int64_t)wk * WOUT;
+  const int64_t m_tile = (int64_t)blockIdx.z * XROWS;
+  const int split_id = blockIdx.y;
+  const int c0 = split_id * a.steps_per_split;
+  const int c1 = min(a.steps, c0 + a.steps_per_split);
+
+  const uint32_t Kb = (uint32_t)(a.K * ES);
+  const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
+  // a wave past N keeps loading (zeros) and meeting the barriers
+  const int64_t rows_w = max((int64_t)0, min((int64_t)WOUT, a.N - n_wave));
+  const int64_t cols_valid = min((int64_t)XROWS, a.M - m_tile);
+  rsrc_t ra[RB];
+  uint32_t a_row0[RB], a_sn[RB];
+  {
+    const rsrc_t rw = make_rsrc(a.w + (rows_w > 0 ? n_wave * a.swn * ES : 0),
+                                rows_w > 0 ? (uint32_t)(rows_w - 1) * swn_b + Kb : 0u);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      ra[rb] = rw;
+      a_row0[rb] = (uint32_t)(16 * rb) * swn_b;
+      a_sn[rb] = swn_b;
+    }
+    if (GLU) {
+      const uint32_t sw2n_b = (uint32_t)(a.sw2n * ES);
+      ra[RB - 1] = make_rsrc(a.w2 + (rows_w > 0 ? n_wave * a.sw2n * ES : 0),
+                             rows_w > 0 ? (uint32_t)(rows_w - 1) * sw2n_b + Kb : 0u);
+      a_row0[RB - 1] = 0u;
+      a_sn[RB - 1] = sw2n_b;
+    }
+  }
+  const rsrc_t rx = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+  f32x4_t acc[RB][CB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  char* tile = wt + wk * WROWS * kLdsRow;
+  // one batch: U chunks of this wave's weight rows and this wave's share of
+  // the activation load instructions
+  struct Batch {
+    u32x4_t W[U][RB][4];
+    u32x4_t X[kXPer];
+  };
+  // Past c1 every offset is out of range (zeros, no traffic).  The activation
+  // loads go first: put_x then waits for them alone, with the weights still
+  // in flight.
+  auto load = [&](Batch& b, int c) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int li = wk + i * KS;   // this wave's i-th activation load instruction
+      const int u = li / (CB * 4), row = (li % (CB * 4)) * 4 + lr;
+      const uint32_t k = (uint32_t)(c + u) * kStep4Bytes + lc * kLaneBytes;
+      const bool ok = li < kXLoads && c + u < c1 && k < Kb && row < cols_valid;
+      b.X[i] = buf_load16<kAuxKeep>(rx, ok ? (uint32_t)row * sxm_b + k : kOob);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t k = (uint32_t)(c + u) * kStep4Bytes + lc * kLaneBytes;
+      const bool kok = c + u < c1 && k < Kb;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          b.W[u][rb][q] = buf_load16<kAuxStream>(
+              ra[rb], kok ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob);
+    }
+  };
+  auto put_x = [&](const Batch& b, char* xslot) {
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int li = wk + i * KS;
+      if (li < kXLoads) {
+        const int u = li / (CB * 4), row = (li % (CB * 4)) * 4 + lr;
+        *reinterpret_cast<u32x4_t*>(xslot + (u * XROWS + row) * kLdsRow + lc * kLaneBytes) = b.X[i];
+      }
+    }
+  };
+  auto compute = [&](const Batch& b, const char* xslot) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<u32x4_t*>(tile + (16 * rb + 4 * q + lr) * kLdsRow + lc * kLaneBytes) = b.W[u][rb][q];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x4_t A[RB], B[CB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          A[rb] = *reinterpret_cast<const u32x4_t*>(tile + (16 * rb + r) * kLdsRow + j * kStepBytes +
+                                                    g * kLaneBytes);
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          B[cb] = *reinterpret_cast<const u32x4_t*>(xslot + (u * XROWS + 16 * cb + r) * kLdsRow +
+                                                    j * kStepBytes + g * kLaneBytes);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = Mfma<DT>::step(A[rb], B[cb], acc[rb][cb]);
+      }
+    }
+  };
+  // Two batches in registers, used in turn: the next batch's loads are issued
+  // after the barrier that publishes this batch's activations and before its
+  // arithmetic, so they are in flight through the arithmetic and the next
+  // barrier.  The loop is unrolled by hand over the two buffers.
+  if (c0 < c1) {
+    Batch bA, bB;
+    load(bA, c0);
+    for (int c = c0;;) {
+      put_x(bA, xs);
+      lds_barrier();   // batch c's activations are in slot 0
+      load(bB, c + U);
+      compute(bA, xs);
+      c += U;
+      if (c >= c1) break;
+      put_x(bB, xs + kSlot);
+      lds_barrier();   // slot 1
+      load(bA, c + U);
+      compute(bB, xs + kSlot);
+      c += U;
+      if (c >= c1) break;
+    }
+  }
+  if (rows_w == 0) return;
+#pragma unroll
+  for (int rb = 0; rb < (GLU ? 1 : RB); ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int64_t m = m_tile + cb * 16 + r;
+      const int64_t nb = n_wave + rb * 16 + 4 * g;
+      if (m < a.M) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t n = nb + j;
+          if (n < a.N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm, one workgroup per token row: y = dtype(gamma * dtype(x * r)),
 // r = 1 / sqrt(sum(x^2) / K + eps) in fp32 -- the stock PyTorch RMSNorm
 // (sdar/run_native_tp2.py:42-47).  Sum order fixed (strided per thread, then
@@ -659,14 +832,26 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
       if (cdiv(N, cand) * pl.tiles_m >= kMinWorkgroups) { rows = cand; break; }
     }
   }
-  if (rows != 4 && rows != 8 && rows != 16 && rows != 32)
-    return set_error("thin_linear: block_n must be 4, 8, 16 or 32 (got %d)", block_n);
+  if (rows != 4 && rows != 8 && rows != 16 && rows != 32 && rows != 64 && rows != 96 && rows != 128)
+    return set_error("thin_linear: block_n must be 4, 8, 16, 32, 64, 96 or 128 (got %d)", block_n);
+  if (rows > 32 && kind != 2) rows = 32;   // 64, 96, 128: the 9..32-token kernel's shared-activation tiles
   if (kind == 2 && rows < 16) rows = 16;   // whole 16-row MFMA blocks
   if (glu && kind == 1 && rows < 8) rows = 8;    // gated GEMV: a gate and an up row group
-  if (glu && kind == 2) rows = 32;               // gated LDS kernel: a gate and an up block
+  if (glu && kind == 2 && rows < 64) rows = 32;  // gated LDS kernel: a gate and an up block
   pl.rows = rows;
   pl.rt = rows >= 16 ? 16 : rows;
   pl.rb = rows >= 16 ? rows / 16 : 1;
+  if (kind == 2 && rows > 32) {
+    // thin_gemm_xs_kernel: the waves split the rows, 16 or 32 each (gated: 32,
+    // a gate and an up block); wave counts that do not divide the rows that
+    // way take 32 rows per wave (96 rows: always 3 waves of 32)
+    pl.kind = 3;
+    pl.rb = rows % (16 * pl.ks) == 0 ? rows / (16 * pl.ks) : 0;
+    if (pl.rb < 1 || pl.rb > 2 || (glu && pl.rb != 2)) {
+      pl.rb = 2;
+      pl.ks = rows / 32;
+    }
+  }
   pl.tiles_n = cdiv(N, rows);
   pl.steps = (int)cdiv(K * es, kind == 0 ? kStepBytes : kStep4Bytes);
   int split = split_k;
@@ -826,10 +1011,43 @@ void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   }
 }
 
+#ifndef SIMSD_XS_U
+#define SIMSD_XS_U 2
+#endif
+
+template <int DT, int RB, int CB, int KS, bool GLU>
+void launch_xs(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  constexpr int U = SIMSD_XS_U;
+  if (pl.split > 1) launch<true>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
+  else launch<false>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
+}
+
+// (rb, ks) of a shared-activation plan: (2, 2), (2, 3), (2, 4); ungated also
+// (1, 4), (1, 8)
+template <int DT, int CB, bool GLU>
+void xs_shape(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  if (pl.rb == 2) {
+    if (pl.ks == 2) launch_xs<DT, 2, CB, 2, GLU>(pl, args, stream);
+    else if (pl.ks == 3) launch_xs<DT, 2, CB, 3, GLU>(pl, args, stream);
+    else launch_xs<DT, 2, CB, 4, GLU>(pl, args, stream);
+  } else if constexpr (!GLU) {
+    if (pl.ks == 4) launch_xs<DT, 1, CB, 4, false>(pl, args, stream);
+    else launch_xs<DT, 1, CB, 8, false>(pl, args, stream);
+  }
+}
+
 template <int DT>
 void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   if constexpr (DT != kF32) {
-    if (pl.norm) {   // RMSNorm prologue: GEMV plans only
+    if (pl.kind == 3) {
+      if (pl.glu) {
+        if (pl.cb == 1) xs_shape<DT, 1, true>(pl, args, stream);
+        else xs_shape<DT, 2, true>(pl, args, stream);
+      } else {
+        if (pl.cb == 1) xs_shape<DT, 1, false>(pl, args, stream);
+        else xs_shape<DT, 2, false>(pl, args, stream);
+      }
+    } else if (pl.norm) {   // RMSNorm prologue: GEMV plans only
       if (pl.glu) {
         if (pl.ms == 1) gemv4_rows<DT, 1, true, true>(pl, args, stream);
         else gemv4_rows<DT, 2, true, true>(pl, args, stream);

@@ -40,7 +40,11 @@ load stream carries no branches.
 
 A workgroup owns 4, 8, 16 or 32 weight rows and splits K over its waves,
 which sum their fp32 partials in fixed order; narrow N uses fewer rows per
-workgroup so every CU still gets work without a cross-workgroup reduction.  An
+workgroup so every CU still gets work without a cross-workgroup reduction.
+Above 8 tokens a workgroup may also own 64, 96 or 128 rows
+(``thin_gemm_xs_kernel``): its waves then split the rows instead of K and
+share each activation chunk, loaded once per workgroup into LDS, so the
+activation bytes read from L2 per weight byte drop by the wave count.  An
 explicit SPLIT_K > 1 splits K over workgroups too: fp32 partial tiles, then a
 second launch sums them in split order.
 
@@ -48,8 +52,9 @@ Config tuples keep the reference's shape ``(BLOCK_M, BLOCK_N, BLOCK_K,
 SPLIT_K[, num_warps, num_stages])`` and describe the MI355X kernels:
 BLOCK_M is the token envelope (``TUNED``: dispatch for M up to 16 or 32) or
 column-block width (heuristic: 4 or 8 for the GEMV, 16 or 32 otherwise),
-BLOCK_N the weight rows per workgroup (4, 8, 16 or 32; other values round down
-to one of these; at least 16 above 8 tokens), BLOCK_K the K elements of
+BLOCK_N the weight rows per workgroup (4, 8, 16, 32, 64, 96 or 128; other
+values round down to one of these; at least 16 above 8 tokens; 64, 96 and 128
+apply above 8 tokens in bf16/fp16 and act as 32 elsewhere), BLOCK_K the K elements of
 activations a wave holds at once in the GEMV (256 or 1024),
 SPLIT_K the workgroups along K, num_warps the waves per workgroup (2, 4 or 8);
 num_stages is accepted and ignored.
@@ -70,7 +75,7 @@ from . import _native
 TARGET_CTAS = 256              # at least one workgroup on every CU
 MAX_SPLIT_K = 16
 MIN_K_PER_SPLIT = 512          # bf16 elements of every row per split (256 B per wave)
-_ROWS = (4, 8, 16, 32)         # weight rows per workgroup the kernel is built for
+_ROWS = (4, 8, 16, 32, 64, 96, 128)   # weight rows per workgroup the kernels are built for
 
 _DEFAULT_WAVES = 4
 
@@ -138,6 +143,15 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     (4096, 151936): (32, 32, 256, 1, 4, 2),   # lm_head
 }
 
+# Shared-activation tiles (64 weight rows per workgroup, waves splitting the
+# rows) where they beat the entry above, for a token range inside its
+# envelope: (K, N) -> ((M_lo, M_hi), 6-tuple).  Same sweep as TUNED, at M=16
+# and M=32; below 9 tokens the GEMV takes every call.
+TUNED_WIDE: dict[tuple[int, int], tuple[tuple[int, int], tuple[int, int, int, int, int, int]]] = {
+    (12288, 4096): ((9, 32), (32, 64, 256, 4, 4, 2)),     # down_proj   22.0 / 23.3 us (M=16 / 32)
+    (4096, 151936): ((17, 32), (32, 64, 256, 1, 4, 2)),   # lm_head      234 us (M=32)
+}
+
 
 def pick_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, int, int, int]:
     """(BLOCK_M, BLOCK_N, BLOCK_K, SPLIT_K) -- tuned where known, else heuristic."""
@@ -153,12 +167,16 @@ def _tuned_for(M: int, N: int, K: int):
     An entry covers every M whose rounded-up block ``max(16, next_pow2(M))``
     fits its BLOCK_M: draft entries (BLOCK_M=16) stop at M=16, exactly the
     reference's rule (kernels/thin_linear_fused.py:232-242); target entries
-    (BLOCK_M=32) extend to the 32-row multi-block verify.
+    (BLOCK_M=32) extend to the 32-row multi-block verify.  Inside the
+    envelope, a ``TUNED_WIDE`` entry whose token range holds M takes over.
     """
     c = TUNED.get((K, N))
-    if c is None:
+    if c is None or max(16, _next_pow2(max(M, 1))) > c[0]:
         return None
-    return c if max(16, _next_pow2(max(M, 1))) <= c[0] else None
+    wide = TUNED_WIDE.get((K, N))
+    if wide is not None and wide[0][0] <= M <= wide[0][1]:
+        return wide[1]
+    return c
 
 
 def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, int, int, int]:

@@ -138,6 +138,13 @@ def test_tuned_table_envelope():
     assert _tuned_for(4, 2048, 2048) is not None
     assert _tuned_for(16, 2048, 2048) is not None
     assert _tuned_for(96, 2048, 2048) is None
+    # shared-activation entries inside their token range only
+    from kernels.thin_linear_fused import TUNED_WIDE
+    for (K, N), ((lo, hi), cfg) in TUNED_WIDE.items():
+        assert (K, N) in TUNED and cfg[1] >= 64
+        assert _tuned_for(lo, N, K) == cfg and _tuned_for(hi, N, K) == cfg
+        assert _tuned_for(lo - 1, N, K) == TUNED[(K, N)]
+        assert _tuned_for(4, N, K) == TUNED[(K, N)]
     assert _tuned_for(4, 999, 2048) is None
     assert should_fuse(4, 2048, 2048) and should_fuse(16, 2048, 2048)
     assert not should_fuse(32, 2048, 2048) and not should_fuse(96, 2048, 2048)

@@ -161,7 +161,7 @@ def test_every_launch_shape(M):
     x, w = rnd(M, 1000, seed=31 + M), rnd(531, 1000, scale=0.02, seed=32)
     with torch.inference_mode():
         ref = F.linear(x, w)
-        for rows in (4, 8, 16, 32):
+        for rows in (4, 8, 16, 32, 64, 96, 128):
             for waves in (2, 4, 8):
                 for split in (1, 3):
                     for block_k in (256, 1024):
@@ -345,6 +345,49 @@ def test_oracle_lm_head_target(M):
     _oracle_check(M, 4096, 151936, seed=99 + M)
 
 
+XS_TILES = [(64, 2), (64, 4), (96, 4), (128, 4), (128, 8)]   # (rows per workgroup, waves)
+
+
+@pytest.mark.parametrize("M", [9, 16, 17, 32])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_shared_activation_tiles_vs_oracle(M, dtype):
+    """The 64-, 96- and 128-row tiles (waves split the rows and share each
+    activation chunk through LDS) against the oracle, on the target's gate_up
+    and qkv shapes and on dims that leave a partial row tile, a partial token
+    block and a partial last k chunk; split 1, 2 and 3.  Bitwise stable across
+    calls."""
+    from kernels.thin_linear_fused import thin_linear, thin_linear_silu_mul
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    for K, N, split in [(4096, 24576, 1), (4096, 6144, 2), (1000, 531, 3)]:
+        x = rnd(M, K, dtype=tdt, seed=70 + M + K)
+        w = rnd(N, K, dtype=tdt, scale=0.02, seed=71 + N)
+        ref = othin.linear_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), dtype=dtype)
+        amax = float(np.abs(ref).max())
+        for rows, waves in XS_TILES:
+            cfg = (32, rows, 256, split)
+            with torch.inference_mode():
+                got_t = thin_linear(x, w, config=cfg, num_warps=waves)
+                assert torch.equal(thin_linear(x, w, config=cfg, num_warps=waves), got_t)
+            got = got_t.float().cpu().numpy()
+            err = float(np.abs(got - ref).max())
+            assert err <= othin.tolerance(amax, dtype), (K, N, rows, waves, split, err)
+            assert othin.max_abs_rel(got, ref) <= 1e-2
+    # gated: the target MLP's gate and up halves (odd I at the other M)
+    K, I = (4096, 12288) if M in (9, 32) else (1000, 531)
+    x = rnd(M, K, dtype=tdt, seed=80 + M)
+    merged = rnd(2 * I, K, dtype=tdt, scale=0.02, seed=81)
+    wg, wu = merged[:I], merged[I:]
+    ref = othin.gated_exact(x.float().cpu().numpy(), wg.float().cpu().numpy(), wu.float().cpu().numpy(),
+                            dtype=dtype)
+    amax = float(np.abs(ref).max())
+    for rows, waves in XS_TILES:
+        with torch.inference_mode():
+            got = thin_linear_silu_mul(x, wg, wu, config=(32, rows, 256, 1), num_warps=waves)
+        got = got.float().cpu().numpy()
+        assert float(np.abs(got - ref).max()) <= othin.tolerance(amax, dtype), (rows, waves)
+        assert othin.max_abs_rel(got, ref) <= 1e-2
+
+
 @pytest.mark.parametrize("M", [3, 5, 13, 17, 31, 33, 64, 96])
 def test_oracle_other_row_counts(M):
     _oracle_check(M, 2048, 1536, seed=M)
@@ -391,14 +434,14 @@ def test_silu_mul_vs_oracle(M, dtype):
         assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("M", [4, 16])
+@pytest.mark.parametrize("M", [4, 16, 32])
 def test_silu_mul_every_launch_shape(M):
     from kernels.thin_linear_fused import thin_linear_silu_mul
     x = rnd(M, 1000, seed=60 + M)
     wg, wu = rnd(261, 1000, scale=0.03, seed=61), rnd(261, 1000, scale=0.03, seed=62)
     with torch.inference_mode():
         ref = F.silu(F.linear(x, wg)) * F.linear(x, wu)
-        for rows in (8, 16, 32):
+        for rows in (8, 16, 32, 64, 96, 128):
             for waves in (2, 4, 8):
                 for split in (1, 3):
                     got = thin_linear_silu_mul(x, wg, wu, config=(16, rows, 256, split), num_warps=waves)
