@@ -59,8 +59,9 @@ average launch duration is the region time / launches.  "traffic" is the
 HBM bytes per launch from the committed rocprofv3 PMC summary under
 profiles/ for the workload (null if none).  "breakdown" times each op's
 calls alone in a graph of their own.  The CPU baseline is the reference's CPU path -- torch
-F.linear in bf16 (its oracle ref_thin_linear) or the stock MoE loop --
-timed on a bounded sample of the same workload.
+F.linear in bf16 (its oracle ref_thin_linear), the stock MoE loop, or (c5)
+the reference's decoder layer forward -- timed on a bounded sample of the
+same workload; in the default run's extras only c5 carries one.
 """
 from __future__ import annotations
 
@@ -687,7 +688,9 @@ def run_c5(args, torch, dev):
     t_fwd = TARGET_8B.n_layers * layer_bytes(TARGET_8B)
     t_head = 2 * TARGET_8B.vocab * TARGET_8B.hidden
     d_fwds = runner.K * len(runner.schedule)
-    it_bytes = d_fwds * d_fwd + (t_fwd + t_head) + t_fwd * (n_blocks / steps)
+    # per iteration: the draft forwards, the verify (layers and lm_head) and
+    # one extend forward of the committed blocks (layers only)
+    it_bytes = d_fwds * d_fwd + (t_fwd + t_head) + t_fwd
     gbs = it_bytes / (it_ms * 1e-3) / 1e9
     return {
         "metric": METRIC, "value": round(n_tok / secs, 2), "unit": "tok/s", "n_gpus": 1,
@@ -713,10 +716,96 @@ def run_c5(args, torch, dev):
         "pipelined_optimistic_drafts": dict(runner.stats),
         "hbm_bound_ms_per_iteration": round(it_bytes / 8e12 * 1e3, 3),
         "init_s": round(init_s, 1),
-        "cpu_baseline": None,
-        "cpu_baseline_note": "not timed: one iteration is 16 draft + 2 target forwards of 1.7B/8B models "
-                             "(minutes per iteration on the host cores)",
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_c5(
+            torch, (DRAFT_1P7B, TARGET_8B), d_fwds, 2, runner.ctx, n_tok / steps),
     }, 4
+
+
+def cpu_baseline_c5(torch, shapes, d_fwds, t_fwds, ctx, tokens_per_iteration):
+    """The reference's dense decoder forward in torch on the host cores
+    (sdar/modeling_sdar.py: stock RMSNorm, F.linear q/k/v/o and gate/up/down,
+    q/k RMSNorm, rotate-half RoPE, SDPA with a bool mask over a GQA-expanded
+    cache of ``ctx`` slots, the static-cache path of adapters/base.py:186-265),
+    bf16.  Bounded sample: one draft layer at 4 rows and one target layer at
+    32 rows, each timed a few times, and both lm_heads once; the iteration is
+    those times scaled by the iteration's forward counts (d_fwds draft
+    forwards, t_fwds target forwards: the verify and the extend),
+    tok/s = tokens per iteration / that."""
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(0)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+    def norm(t, w, eps):
+        t32 = t.float()
+        return w * (t32 * torch.rsqrt(t32.pow(2).mean(-1, keepdim=True) + eps)).to(t.dtype)
+
+    def layer_fn(sh, M):
+        H, D, Hq, Hkv, I = sh.hidden, sh.head_dim, sh.n_q_heads, sh.n_kv_heads, sh.intermediate
+        w = {"ln1": 1 + rnd(H, scale=0.1), "wq": rnd(Hq * D, H, scale=0.02), "wk": rnd(Hkv * D, H, scale=0.02),
+             "wv": rnd(Hkv * D, H, scale=0.02), "qn": 1 + rnd(D, scale=0.1), "kn": 1 + rnd(D, scale=0.1),
+             "wo": rnd(H, Hq * D, scale=0.02), "ln2": 1 + rnd(H, scale=0.1), "wg": rnd(I, H, scale=0.02),
+             "wu": rnd(I, H, scale=0.02), "wd": rnd(H, I, scale=0.02)}
+        L = ctx + M
+        kc, vc = rnd(1, Hq, L, D), rnd(1, Hq, L, D)          # the reference's expanded cache
+        pos = torch.arange(ctx, ctx + M)
+        inv = 1.0 / (sh.rope_theta ** (torch.arange(0, D, 2).float() / D))
+        ang = torch.cat([pos[:, None].float() * inv[None]] * 2, dim=-1)
+        cos, sin = ang.cos().to(torch.bfloat16)[:, None], ang.sin().to(torch.bfloat16)[:, None]
+        mask = torch.ones(M, L, dtype=torch.bool)
+        mask[:, ctx:] = torch.tril(torch.ones(M, M, dtype=torch.bool))
+        x = rnd(M, H)
+        slots = torch.arange(ctx, ctx + M)
+
+        def rope(t):
+            return t * cos + torch.cat((-t[..., D // 2:], t[..., :D // 2]), dim=-1) * sin
+
+        def fwd():
+            h = norm(x, w["ln1"], sh.eps)
+            q = rope(norm(F.linear(h, w["wq"]).view(M, Hq, D), w["qn"], sh.eps))
+            k = rope(norm(F.linear(h, w["wk"]).view(M, Hkv, D), w["kn"], sh.eps))
+            v = F.linear(h, w["wv"]).view(M, Hkv, D)
+            n_rep = Hq // Hkv
+            kc.index_copy_(2, slots, k.repeat_interleave(n_rep, 1).transpose(0, 1)[None])
+            vc.index_copy_(2, slots, v.repeat_interleave(n_rep, 1).transpose(0, 1)[None])
+            a = F.scaled_dot_product_attention(q.transpose(0, 1)[None], kc, vc, attn_mask=mask[None, None])
+            h2 = x + F.linear(a[0].transpose(0, 1).reshape(M, Hq * D), w["wo"])
+            m = norm(h2, w["ln2"], sh.eps)
+            return h2 + F.linear(F.silu(F.linear(m, w["wg"])) * F.linear(m, w["wu"]), w["wd"])
+        return fwd
+
+    def timed(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    draft, target = shapes
+    with torch.inference_mode():
+        t_d = timed(layer_fn(draft, 4), 5)
+        t_t = timed(layer_fn(target, 32), 3)
+        hd = (rnd(4, draft.hidden), rnd(draft.vocab, draft.hidden, scale=0.02))
+        t_dh = timed(lambda: F.linear(*hd), 2)
+        del hd
+        ht = (rnd(32, target.hidden), rnd(target.vocab, target.hidden, scale=0.02))
+        t_th = timed(lambda: F.linear(*ht), 2)
+        del ht
+    it_s = d_fwds * (draft.n_layers * t_d + t_dh) + t_fwds * target.n_layers * t_t + t_th
+    return {
+        "value": round(tokens_per_iteration / it_s, 4),
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"reference decoder forward in torch on the host (bf16): one draft layer at 4 rows "
+                   f"{t_d * 1e3:.2f} ms, one target layer at 32 rows {t_t * 1e3:.2f} ms, draft lm_head "
+                   f"{t_dh * 1e3:.1f} ms, target lm_head {t_th * 1e3:.1f} ms (context {ctx} slots), scaled to "
+                   f"{d_fwds} draft + {t_fwds} target forwards per iteration = {it_s * 1e3:.0f} ms for "
+                   f"{tokens_per_iteration:.2f} tokens; cpu={cpu_model()}; os.cpu_count={os.cpu_count()}"),
+    }
 
 
 # ────────────────────────────────────────────────────────────────── MoE ───
@@ -969,7 +1058,7 @@ EXTRA_WORKLOADS = ("c1", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "c5")
 _EXTRA_KEYS = ("value", "unit", "ms_per_step", "steps", "config", "roofline", "breakdown", "tflops",
                "tokens_per_iteration", "accepted_draft_tokens_per_iteration", "committed_blocks_per_iteration",
                "phase_ms_per_iteration", "ms_per_iteration_extend_in_line", "ms_per_iteration_pipelined",
-               "hbm_bound_ms_per_iteration")
+               "hbm_bound_ms_per_iteration", "cpu_baseline")
 
 
 def run_extras(args, torch, dev):
@@ -977,6 +1066,9 @@ def run_extras(args, torch, dev):
     for wl in EXTRA_WORKLOADS:
         sub = argparse.Namespace(**vars(args))
         sub.workload = wl
+        # host-core baselines: the headline's, and C5's (one iteration scaled
+        # from one timed layer of each model); the others would add minutes
+        sub.no_cpu_baseline = args.no_cpu_baseline or wl != "c5"
         sub.steps = 10 if wl == "c5" else max(10, args.steps // 2)
         sub.warmup = 2 if wl == "c5" else max(2, args.warmup // 2)
         print(f"bench: extra workload {wl} ({sub.steps} steps)", file=sys.stderr, flush=True)
