@@ -38,6 +38,9 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           denoise steps, 4 blocks verified per target forward, greedy
           acceptance; value in generated tokens / s.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
+  gemv_valu
+          the M=4 draft set in two designs: the 4x4x4-MFMA GEMV and the VALU
+          form first specified for it (probe), per op, best geometry each.
   floor   the floors of one launch: an empty kernel, and the fastest pure
           read of C1's 48 MiB weight in the GEMV's access pattern over a sweep
           of rows per workgroup x waves, beside the C1 GEMV on the same 24
@@ -965,6 +968,60 @@ def run_floor(args, torch, dev):
     }, M
 
 
+def run_gemv_valu(args, torch, dev):
+    """The M=4 linear in two designs on the same shapes and weights, in HIP
+    graphs: the product's 4x4x4-MFMA GEMV (thin_linear, tuned configs) and
+    the VALU form the path was first specified with (simsd_probe_gemv_valu:
+    128-bit weight loads, activations staged in LDS, v_dot2_f32_bf16), the
+    latter at its best rows-per-workgroup x waves per op.  Each op: 28
+    distinct weights (the C2 layer count; 24 for the C1 gate_up), so the MALL
+    cannot serve repeats.  value = the VALU form's C2 step in GB/s."""
+    from kernels import _native
+    from kernels.thin_linear_fused import thin_linear
+
+    lib = _native.lib()
+    M = 4
+    ops = [("qkv", 2048, 4096, 28), ("o", 2048, 2048, 28), ("gate_up", 2048, 12288, 28), ("down", 6144, 2048, 28)]
+    per_op = {}
+    step_mfma = step_valu = 0.0
+    step_bytes = 0
+    with torch.inference_mode():
+        reps = max(10, args.steps)
+        for name, K, N, n_w in ops:
+            ws = [(torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_w)]
+            x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+            y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+
+            def valu(w, rows, waves):
+                return lambda: _native.check(lib.simsd_probe_gemv_valu(
+                    x.data_ptr(), K, w.data_ptr(), K, y.data_ptr(), N, M, N, K, rows, waves,
+                    _native.stream_of(dev)), "probe_gemv_valu")
+
+            mfma_us = graph_us_per_call(torch, [lambda w=w: thin_linear(x, w) for w in ws], reps=reps)
+            sweep = {f"{r}x{v}": round(graph_us_per_call(torch, [valu(w, r, v) for w in ws], reps=reps), 3)
+                     for r in (8, 16) for v in (2, 4, 8)}
+            best = min(sweep, key=sweep.get)
+            b = linear_bytes(M, K, N)
+            per_op[name] = {"K": K, "N": N, "mfma_us": round(mfma_us, 3), "valu_us": sweep[best],
+                            "valu_best_rows_x_waves": best, "valu_us_by_rows_x_waves": sweep,
+                            "mfma_frac": round(b / (mfma_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                            "valu_frac": round(b / (sweep[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+            step_mfma += 28 * mfma_us
+            step_valu += 28 * sweep[best]
+            step_bytes += 28 * b
+            del ws
+            torch.cuda.empty_cache()
+    return {
+        "metric": "M=4 linear, VALU vs 4x4x4-MFMA GEMV: C2-step GB/s of the VALU form",
+        "value": round(step_bytes / (step_valu * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": reps, "warmup": 1, "ms_per_step": round(step_valu * 1e-3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "gemv-valu-vs-mfma-M4-draft-set", "M": M, "parallelism": "single-gpu"},
+        "c2_step_ms_mfma": round(step_mfma * 1e-3, 4), "c2_step_ms_valu": round(step_valu * 1e-3, 4),
+        "per_op": per_op,
+    }, M
+
+
 def run_copy(args, torch, dev):
     """A plain 1 GiB device copy (torch's elementwise copy kernel): the known
     byte count that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
@@ -998,7 +1055,7 @@ def main():
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
                              "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy",
-                             "floor"])
+                             "floor", "gemv_valu"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
@@ -1018,8 +1075,8 @@ def main():
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
         return
-    if args.workload == "floor":
-        result, _ = run_floor(args, torch, dev)
+    if args.workload in ("floor", "gemv_valu"):
+        result, _ = (run_floor if args.workload == "floor" else run_gemv_valu)(args, torch, dev)
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)
         return

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 14
+#define SIMSD_ABI_VERSION 15
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -46,6 +46,14 @@ extern "C" {
 int simsd_probe_empty(void* stream);
 int simsd_probe_read(const void* w, int64_t rows, int64_t row_bytes, int rows_per_wg, int waves,
                      void* sink, int64_t sink_words, void* stream);
+/* The M <= 4 bf16 linear y[M, N] = x[M, K] . w[N, K]^T in the VALU form the
+ * hot path was first specified with (128-bit weight loads of one row x 1 KB,
+ * the tokens' rows staged in LDS, v_dot2_f32_bf16, lanes and waves reduced
+ * in fixed order), beside simsd_thin_linear's 4x4x4-MFMA GEMV for A/B runs.
+ * 1 <= M <= 4, K a multiple of 8 up to 6144, 16-byte aligned rows (strides in
+ * elements), rows_per_wg 8 or 16, waves 2, 4 or 8. */
+int simsd_probe_gemv_valu(const void* x, int64_t sxm, const void* w, int64_t swn, void* y, int64_t sym,
+                          int64_t M, int64_t N, int64_t K, int rows_per_wg, int waves, void* stream);
 
 /* ---- housekeeping ---------------------------------------------------- */
 int simsd_abi_version(void);
