@@ -41,6 +41,10 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
   gemv_valu
           the M=4 draft set in two designs: the 4x4x4-MFMA GEMV and the VALU
           form first specified for it (probe), per op, best geometry each.
+  timeline
+          where an M=4 GEMV call's time goes (launch gap, ramp, first data,
+          stream, tail), per C2 op, from the timeline build of the library
+          (python simsd-release_amd/build_lib.py --timeline first).
   floor   the floors of one launch: an empty kernel, and the fastest pure
           read of C1's 48 MiB weight in the GEMV's access pattern over a sweep
           of rows per workgroup x waves, beside the C1 GEMV on the same 24
@@ -1022,6 +1026,90 @@ def run_gemv_valu(args, torch, dev):
     }, M
 
 
+def run_timeline(args, torch, dev):
+    """Where an M=4 GEMV call's time goes, from the timeline build of the
+    library (build_lib.py --timeline: every wave of thin_gemv4_kernel stamps
+    the 100 MHz clock at entry, after its first chunk, after its last chunk
+    and at its end).  Each C2 op's 28 distinct weights (24 for gate_up) run
+    in one graph, timed first without stamps, then replayed once with them.
+    Per call: the gap from the previous call's last wave end to this call's
+    first wave start, the dispatch ramp (waves' starts), the time to the
+    first chunk's data, the stream (first to last chunk), the tail (last wave
+    end past the median end); medians over the calls.  Writing the stamps
+    happens after the end stamp and lengthens the gap that follows by a
+    constant, which is subtracted (the stamped replay's time per call minus
+    the plain one's)."""
+    import ctypes
+
+    import numpy as np
+    from kernels import _native
+    from kernels.thin_linear_fused import thin_linear
+
+    path = os.path.join(REPO, "simsd-release_amd", "kernels", "libsimsd_timeline.so")
+    if not os.path.exists(path):
+        raise SystemExit("bench.py: the timeline workload needs simsd-release_amd/kernels/libsimsd_timeline.so "
+                         "(python simsd-release_amd/build_lib.py --timeline)")
+    _native.LIB_PATH = path
+    _native.lib()
+    tl = ctypes.CDLL(path)
+    tl.simsd_gemv_timeline_set.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
+    tl.simsd_gemv_timeline_bytes.restype = ctypes.c_int64
+    stamps = torch.zeros(tl.simsd_gemv_timeline_bytes() // 8, dtype=torch.int64, device=dev)
+    M = 4
+    ops = [("qkv", 2048, 4096, 28), ("o", 2048, 2048, 28), ("gate_up", 2048, 12288, 24), ("down", 6144, 2048, 28)]
+    per_op = {}
+    with torch.inference_mode():
+        for name, K, N, L in ops:
+            g = torch.Generator(device=dev).manual_seed(5)
+            ws = [(torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16() for _ in range(L)]
+            x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+            fns = [lambda w=w: thin_linear(x, w) for w in ws]
+            plain_us = graph_us_per_call(torch, fns, reps=max(10, args.steps))
+            w_list = (ctypes.c_void_p * L)(*[w.data_ptr() for w in ws])
+            _native.check(tl.simsd_gemv_timeline_set(stamps.data_ptr(), w_list, L), "gemv_timeline")
+            stamped_us = graph_us_per_call(torch, fns, reps=1)
+            _native.check(tl.simsd_gemv_timeline_set(None, None, 0), "gemv_timeline")
+            torch.cuda.synchronize()
+            t = stamps.view(64, 1024, 8, 4)[:L].cpu().numpy().astype(np.int64)
+            stamps.zero_()
+            rows = {k: [] for k in ("gap", "ramp_p50", "ramp_max", "first_data", "stream", "tail", "span")}
+            prev_end = None
+            for c in t:
+                used = c[:, :, 0] > 0
+                starts, ends = c[:, :, 0][used], c[:, :, 3][used]
+                t0 = starts.min()
+                ok = used & (c[:, :, 1] > 0)
+                if prev_end is not None:
+                    rows["gap"].append(t0 - prev_end)
+                rows["ramp_p50"].append(np.median(starts) - t0)
+                rows["ramp_max"].append(starts.max() - t0)
+                rows["first_data"].append(np.median((c[:, :, 1] - c[:, :, 0])[ok]))
+                rows["stream"].append(np.median((c[:, :, 2] - c[:, :, 1])[ok]))
+                rows["tail"].append(ends.max() - np.median(ends))
+                rows["span"].append(ends.max() - t0)
+                prev_end = ends.max()
+            med = {k: round(float(np.median(v)) / 100.0, 3) for k, v in rows.items()}   # 100 MHz ticks -> us
+            med["gap"] = round(med["gap"] - (stamped_us - plain_us), 3)
+            per_op[name] = {"K": K, "N": N, "us_per_call": round(plain_us, 3),
+                            "us_per_call_stamped": round(stamped_us, 3),
+                            "workgroups": int(used.any(1).sum()), "waves_per_workgroup": int(used.any(0).sum()),
+                            "gap_us": med["gap"], "dispatch_ramp_p50_us": med["ramp_p50"],
+                            "dispatch_ramp_max_us": med["ramp_max"], "first_data_us": med["first_data"],
+                            "stream_us": med["stream"], "tail_us": med["tail"], "kernel_span_us": med["span"],
+                            "ideal_us_at_8TBps": round(linear_bytes(M, K, N) / 8e6, 3)}
+            del ws
+            torch.cuda.empty_cache()
+    o = per_op["o"]
+    return {
+        "metric": "M=4 GEMV call timeline: launch gap, ramp, first data, stream, tail (us)",
+        "value": o["us_per_call"], "unit": "us per o_proj call", "n_gpus": 1, "steps": max(10, args.steps),
+        "warmup": 1, "ms_per_step": round(o["us_per_call"] * 1e-3, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "gemv-timeline-M4-draft-set", "M": M, "parallelism": "single-gpu"},
+        "per_op": per_op,
+    }, M
+
+
 def run_copy(args, torch, dev):
     """A plain 1 GiB device copy (torch's elementwise copy kernel): the known
     byte count that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
@@ -1055,7 +1143,7 @@ def main():
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
                              "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy",
-                             "floor", "gemv_valu"])
+                             "floor", "gemv_valu", "timeline"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
@@ -1075,8 +1163,9 @@ def main():
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
         return
-    if args.workload in ("floor", "gemv_valu"):
-        result, _ = (run_floor if args.workload == "floor" else run_gemv_valu)(args, torch, dev)
+    if args.workload in ("floor", "gemv_valu", "timeline"):
+        result, _ = {"floor": run_floor, "gemv_valu": run_gemv_valu, "timeline": run_timeline}[args.workload](
+            args, torch, dev)
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)
         return

@@ -204,8 +204,31 @@ constexpr int kNormMaxMs = SIMSD_NORM_MAX_MS;
 #define SIMSD_NORM_EARLY 2
 #endif
 
+// Timeline build (SIMSD_GEMV_TIMELINE=1, a separate library: build_lib.py
+// --timeline): every wave of thin_gemv4_kernel takes the 100 MHz clock at
+// entry, after its first chunk's arithmetic, after its last and at its end,
+// and stores the four stamps for calls whose weight pointer is registered
+// (simsd_gemv_timeline_set).  What it measures: the gap between launches, the
+// dispatch ramp, the time to the first data, the stream and the tail.  The
+// product library is built without it.
+#ifndef SIMSD_GEMV_TIMELINE
+#define SIMSD_GEMV_TIMELINE 0
+#endif
+#if SIMSD_GEMV_TIMELINE
+constexpr int kTimelineCalls = 64;
+constexpr int kTimelineWgs = 1024;
+constexpr int kTimelineWaves = 8;
+__device__ unsigned long long* g_timeline;
+__device__ const void* g_timeline_w[kTimelineCalls];
+__device__ int g_timeline_n;
+#endif
+
 template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU, bool NORM>
 __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
+#if SIMSD_GEMV_TIMELINE
+  const unsigned long long tl0 = __builtin_amdgcn_s_memrealtime();
+  unsigned long long tl1 = 0;
+#endif
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int G = RW / 4;
   static_assert(RW % 4 == 0 && G % GB == 0, "row groups");
@@ -389,7 +412,17 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
       c0 += CH;
     }
   }
+#if SIMSD_GEMV_TIMELINE
+  if (c0 < w1) {
+    run_chunk(c0, load_b, load_g, load_a);
+    c0 += CH;
+    tl1 = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
   for (; c0 < w1; c0 += CH) run_chunk(c0, load_b, load_g, load_a);
+#if SIMSD_GEMV_TIMELINE
+  const unsigned long long tl2 = __builtin_amdgcn_s_memrealtime();
+#endif
 
   // sum the 16 k-chunk blocks (lane bits 2..5), then the KS waves in wave
   // order through LDS: red[wave][value][col j]
@@ -421,6 +454,19 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
       put_out<DT, PARTIAL, GLU>(a, split_id, m, n, t, u);
     }
   }
+#if SIMSD_GEMV_TIMELINE
+  const unsigned long long tl3 = __builtin_amdgcn_s_memrealtime();
+  if (g_timeline != nullptr && lane == 0 && blockIdx.x < kTimelineWgs && wk < kTimelineWaves) {
+    int call = -1;
+    for (int q = 0; q < g_timeline_n; ++q)
+      if (g_timeline_w[q] == a.w) call = q;
+    if (call >= 0) {
+      unsigned long long* t =
+          g_timeline + (((int64_t)call * kTimelineWgs + blockIdx.x) * kTimelineWaves + wk) * 4;
+      t[0] = tl0; t[1] = tl1; t[2] = tl2; t[3] = tl3;
+    }
+  }
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1470,3 +1516,19 @@ extern "C" int simsd_thin_linear_residual(const void* x, int64_t sxm, int64_t sx
   args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
   return run_planned(pl, args, dtype, workspace, workspace_bytes, stream, "thin_linear_residual");
 }
+
+#if SIMSD_GEMV_TIMELINE
+// stamps: [call][workgroup][wave][4] u64 (kTimelineCalls x 1024 x 8 x 4), the
+// calls matched by weight pointer against w_list[0..n); p = nullptr stops.
+extern "C" int simsd_gemv_timeline_set(void* stamps, const void* const* w_list, int n) {
+  if (n < 0 || n > kTimelineCalls) return set_error("gemv_timeline: at most %d calls", kTimelineCalls);
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), &stamps, sizeof(stamps)) != hipSuccess ||
+      (n > 0 && hipMemcpyToSymbol(HIP_SYMBOL(g_timeline_w), w_list, sizeof(void*) * n) != hipSuccess) ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_timeline_n), &n, sizeof(n)) != hipSuccess)
+    return set_error("gemv_timeline: setting the stamp buffer failed");
+  return 0;
+}
+extern "C" int64_t simsd_gemv_timeline_bytes(void) {
+  return (int64_t)kTimelineCalls * kTimelineWgs * kTimelineWaves * 4 * 8;
+}
+#endif
