@@ -616,6 +616,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
 // moe_combine_kernel then runs on them: one launch instead of two, and no
 // [T*k, H] round trip through memory.
 constexpr int kSmallT = 4;
+#ifndef SIMSD_MOE_SMALL_NB
+#define SIMSD_MOE_SMALL_NB 2
+#endif
+constexpr int kSmallNB = SIMSD_MOE_SMALL_NB;   // unit buffers in flight per wave
 constexpr int kSmallSlots = 64;   // T * k limit of the LDS table
 
 template <int DT, int G, int S>
@@ -638,21 +642,29 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
   const uint32_t lane_k = (uint32_t)b4 * kLaneBytes;
 
   // descriptors of this wave's units: expert (-1 shared, -2 none) and the
-  // lane's first-set column (a slot, or a token for the shared expert)
-  int ue[UM], ucol[UM];
+  // lane's column in each set of 4 (a slot, or a token for the shared
+  // expert), all read in the first round trip -- a set past the first is
+  // used only when a token picked the expert twice, and reading it later
+  // would put a dependent load between consecutive units
+  constexpr int kSets = kTile / 4;
+  int ue[UM], ucol[UM][kSets];
 #pragma unroll
   for (int i = 0; i < UM; ++i) {
     const int u = wv + i * W;
     if (u < a.num_tiles) {
       const int e = a.tile_expert[u];
       ue[i] = (e >= 0 && e < a.E) ? e : -2;
-      ucol[i] = a.slots[(int64_t)u * kTile + i4];
+#pragma unroll
+      for (int cs = 0; cs < kSets; ++cs) ucol[i][cs] = a.slots[(int64_t)u * kTile + 4 * cs + i4];
     } else if (u < n_units) {
       ue[i] = -1;
-      ucol[i] = i4 < a.T ? i4 : -1;
+      ucol[i][0] = i4 < a.T ? i4 : -1;
+#pragma unroll
+      for (int cs = 1; cs < kSets; ++cs) ucol[i][cs] = -1;
     } else {
       ue[i] = -2;
-      ucol[i] = -1;
+#pragma unroll
+      for (int cs = 0; cs < kSets; ++cs) ucol[i][cs] = -1;
     }
   }
   auto w_rsrc = [&](int e, uint32_t& sn_b, uint32_t& Kb) {
@@ -684,7 +696,7 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
         const uint32_t k = (uint32_t)st * kStep4Bytes + lane_k;
         U.A[g][st] = buf_load16<kAuxStream>(rW, k < Kb ? (uint32_t)(4 * g + i4) * sn_b + k : kOob);
       }
-    load_b(h_rsrc(ue[i], Kb), Kb, ucol[i], U.B);
+    load_b(h_rsrc(ue[i], Kb), Kb, ucol[i][0], U.B);
   };
   // one column set: MFMAs, the 16 k blocks summed (lane bits 2..5), lanes
   // with bits 2..3 clear hold feature q0 + p of column i4
@@ -716,14 +728,14 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
   auto compute = [&](int i, const SmallUnit<DT, G, S>& U) {
     if (ue[i] == -2) return;
     const bool shared = ue[i] == -1;
-    finish(U, U.B, ucol[i], shared);
+    finish(U, U.B, ucol[i][0], shared);
     if (shared) return;
     // further sets of 4 slots: only when a token picked this expert twice
-    const int u = wv + i * W;
     uint32_t Kb = (uint32_t)(a.I * ES);
     const rsrc_t rH = h_rsrc(ue[i], Kb);
-    for (int cs = 1; cs < kTile / 4; ++cs) {
-      const int col = a.slots[(int64_t)u * kTile + 4 * cs + i4];
+#pragma unroll
+    for (int cs = 1; cs < kSets; ++cs) {
+      const int col = ucol[i][cs];
       if (!__any(col >= 0)) break;       // slots fill a tile from the front
       u32x4_t B[S];
       load_b(rH, Kb, col, B);
@@ -731,17 +743,18 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
     }
   };
 
-  SmallUnit<DT, G, S> U0, U1;
-  issue(0, U0);
-  if (UM > 1) issue(1, U1);
+  // NB unit buffers used in turn: the loads of the next NB - 1 units are in
+  // flight while a unit's arithmetic runs (every index is a constant after
+  // unrolling, so the buffers stay in registers)
+  constexpr int kNB = S <= 4 ? kSmallNB : 2;   // 8 k steps a unit: two buffers fill the registers
+  constexpr int NB = kNB < UM ? kNB : UM;
+  SmallUnit<DT, G, S> U[NB];
 #pragma unroll
-  for (int i = 0; i < UM; i += 2) {
-    compute(i, U0);
-    if (i + 2 < UM) issue(i + 2, U0);
-    if (i + 1 < UM) {
-      compute(i + 1, U1);
-      if (i + 3 < UM) issue(i + 3, U1);
-    }
+  for (int b = 0; b + 1 < NB; ++b) issue(b, U[b]);
+#pragma unroll
+  for (int i = 0; i < UM; ++i) {
+    if (i + NB - 1 < UM) issue(i + NB - 1, U[(i + NB - 1) % NB]);
+    compute(i, U[i % NB]);
   }
   __syncthreads();
   for (int e = threadIdx.x; e < (int)a.T * R; e += 64 * W) {
