@@ -143,13 +143,17 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     (4096, 151936): (32, 32, 256, 1, 4, 2),   # lm_head
 }
 
-# Shared-activation tiles (64 weight rows per workgroup, waves splitting the
-# rows) where they beat the entry above, for a token range inside its
-# envelope: (K, N) -> ((M_lo, M_hi), 6-tuple).  Same sweep as TUNED, at M=16
-# and M=32; below 9 tokens the GEMV takes every call.
-TUNED_WIDE: dict[tuple[int, int], tuple[tuple[int, int], tuple[int, int, int, int, int, int]]] = {
-    (12288, 4096): ((9, 32), (32, 64, 256, 4, 4, 2)),     # down_proj   22.0 / 23.3 us (M=16 / 32)
-    (4096, 151936): ((17, 32), (32, 64, 256, 1, 4, 2)),   # lm_head      234 us (M=32)
+# Token ranges inside an entry's envelope where another geometry wins:
+# (K, N) -> (((M_lo, M_hi), 6-tuple), ...), first match taken.  Same sweep as
+# TUNED.  Above 8 tokens these are the shared-activation tiles (64 weight rows
+# per workgroup, waves splitting the rows); at 5-8 tokens the merged qkv with
+# its RMSNorm prologue, where 16 rows per workgroup halve the workgroups that
+# read both column sets' rows for the statistics (7.0-7.1 against 8.0-8.9 us
+# with 8 rows; the plain projection moves by at most 0.4 us either way).
+TUNED_RANGES: dict[tuple[int, int], tuple[tuple[tuple[int, int], tuple[int, int, int, int, int, int]], ...]] = {
+    (2048, 4096): (((5, 8), (16, 16, 256, 1, 4, 2)),),      # merged qkv      7.1 us (M=8)
+    (12288, 4096): (((9, 32), (32, 64, 256, 4, 4, 2)),),    # down_proj   22.0 / 23.3 us (M=16 / 32)
+    (4096, 151936): (((17, 32), (32, 64, 256, 1, 4, 2)),),  # lm_head      234 us (M=32)
 }
 
 
@@ -168,14 +172,15 @@ def _tuned_for(M: int, N: int, K: int):
     fits its BLOCK_M: draft entries (BLOCK_M=16) stop at M=16, exactly the
     reference's rule (kernels/thin_linear_fused.py:232-242); target entries
     (BLOCK_M=32) extend to the 32-row multi-block verify.  Inside the
-    envelope, a ``TUNED_WIDE`` entry whose token range holds M takes over.
+    envelope, the first ``TUNED_RANGES`` entry whose token range holds M
+    takes over.
     """
     c = TUNED.get((K, N))
     if c is None or max(16, _next_pow2(max(M, 1))) > c[0]:
         return None
-    wide = TUNED_WIDE.get((K, N))
-    if wide is not None and wide[0][0] <= M <= wide[0][1]:
-        return wide[1]
+    for (lo, hi), cfg in TUNED_RANGES.get((K, N), ()):
+        if lo <= M <= hi:
+            return cfg
     return c
 
 

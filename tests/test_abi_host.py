@@ -139,12 +139,18 @@ def test_tuned_table_envelope():
     assert _tuned_for(16, 2048, 2048) is not None
     assert _tuned_for(96, 2048, 2048) is None
     # shared-activation entries inside their token range only
-    from kernels.thin_linear_fused import TUNED_WIDE
-    for (K, N), ((lo, hi), cfg) in TUNED_WIDE.items():
-        assert (K, N) in TUNED and cfg[1] >= 64
-        assert _tuned_for(lo, N, K) == cfg and _tuned_for(hi, N, K) == cfg
-        assert _tuned_for(lo - 1, N, K) == TUNED[(K, N)]
+    from kernels.thin_linear_fused import TUNED_RANGES
+    for (K, N), ranges in TUNED_RANGES.items():
+        assert (K, N) in TUNED
+        for (lo, hi), cfg in ranges:
+            assert 1 <= lo <= hi <= TUNED[(K, N)][0]
+            assert cfg[1] >= 64 if lo > 8 else hi <= 8     # wide tiles only above 8 tokens
+            assert _tuned_for(lo, N, K) == cfg and _tuned_for(hi, N, K) == cfg
+            assert _tuned_for(lo - 1, N, K) == TUNED[(K, N)] or any(
+                a <= lo - 1 <= b for (a, b), _ in ranges)
         assert _tuned_for(4, N, K) == TUNED[(K, N)]
+    assert _tuned_for(8, 4096, 2048) == (16, 16, 256, 1, 4, 2)
+    assert _tuned_for(9, 4096, 2048) == TUNED[(2048, 4096)]
     assert _tuned_for(4, 999, 2048) is None
     assert should_fuse(4, 2048, 2048) and should_fuse(16, 2048, 2048)
     assert not should_fuse(32, 2048, 2048) and not should_fuse(96, 2048, 2048)
