@@ -43,6 +43,10 @@ def flags(extra=()) -> list[str]:
         f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument",
+        # leading scalar kernel arguments arrive in SGPRs (no kernarg fetch
+        # before a kernel's first loads); kernels whose first argument is a
+        # struct are unaffected
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         "-I", INCLUDE, "-I", CSRC, *extra,
     ]
 

@@ -223,8 +223,16 @@ __device__ const void* g_timeline_w[kTimelineCalls];
 __device__ int g_timeline_n;
 #endif
 
+// The fields the first loads depend on come as separate scalar arguments
+// ahead of ThinArgs: the build preloads leading scalar kernel arguments into
+// SGPRs (-amdgpu-kernarg-preload-count), so the first weight and activation
+// loads wait for no kernarg fetch.  Kb, swn_b, sxm_b, sw2n_b: K and the row
+// strides in bytes; the rest of ThinArgs is read where it is used.
 template <int DT, int RW, int MS, int KS, int CH, int GB, bool PARTIAL, bool GLU, bool NORM>
-__global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
+__global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(const char* __restrict__ w, const char* __restrict__ x,
+                                                             const char* __restrict__ w2, uint32_t Kb, uint32_t swn_b,
+                                                             uint32_t sxm_b, uint32_t sw2n_b, int N, int M, int steps,
+                                                             int steps_per_split, ThinArgs a) {
 #if SIMSD_GEMV_TIMELINE
   const unsigned long long tl0 = __builtin_amdgcn_s_memrealtime();
   unsigned long long tl1 = 0;
@@ -243,22 +251,18 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
   const int64_t m_tile = (int64_t)blockIdx.z * (4 * MS);
   const int split_id = blockIdx.y;
 
-  const int s_lo = split_id * a.steps_per_split;
-  const int s_hi = min(a.steps, s_lo + a.steps_per_split);
+  const int s_lo = split_id * steps_per_split;
+  const int s_hi = min(steps, s_lo + steps_per_split);
   const int span = max(0, s_hi - s_lo);
   const int per_w = (span + KS - 1) / KS;
   const int w0 = s_lo + wk * per_w;
   const int w1 = min(s_hi, w0 + per_w);
 
-  const uint32_t Kb = (uint32_t)(a.K * ES);
-  const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
-  const uint32_t sw2n_b = (uint32_t)(a.sw2n * ES);
-  const int64_t rows_valid = min((int64_t)OUT, a.N - n_tile);
-  const int64_t cols_valid = min((int64_t)(4 * MS), a.M - m_tile);
-  const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
-  const rsrc_t rA2 = GLU ? make_rsrc(a.w2 + n_tile * a.sw2n * ES, (uint32_t)(rows_valid - 1) * sw2n_b + Kb)
-                         : rA;
-  const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+  const int64_t rows_valid = min((int64_t)OUT, (int64_t)N - n_tile);
+  const int64_t cols_valid = min((int64_t)(4 * MS), (int64_t)M - m_tile);
+  const rsrc_t rA = make_rsrc(w + n_tile * swn_b, (uint32_t)(rows_valid - 1) * swn_b + Kb);
+  const rsrc_t rA2 = GLU ? make_rsrc(w2 + n_tile * sw2n_b, (uint32_t)(rows_valid - 1) * sw2n_b + Kb) : rA;
+  const rsrc_t rB = make_rsrc(x + m_tile * sxm_b, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
   const uint32_t lane_k = (uint32_t)(b4 * kLaneBytes);
 
   // RMSNorm prologue: every workgroup derives the scale of its <= 8 tokens
@@ -446,7 +450,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(ThinArgs a) {
     const int j = e & 3, v = (e >> 2) & 3, c = (e >> 4) % MS, g = (e >> 4) / MS;
     const int64_t n = n_tile + 4 * g + v;
     const int64_t m = m_tile + 4 * c + j;
-    if (n < a.N && m < a.M) {
+    if (n < N && m < M) {
       float t = 0.f, u = 0.f;
       for (int w = 0; w < KS; ++w) t += red[((w * G + g) * MS + c) * 16 + v * 4 + j];
       if (GLU)
@@ -861,6 +865,8 @@ inline bool norm_in_gemv(const ThinPlan& pl, int64_t M, int64_t K, int es) {
 int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int dtype, int block_n,
                   int block_k, int num_waves, int split_k, bool glu = false) {
   const int es = esize_of(dtype);
+  if (N > 0x7fffffff || M > 0x7fffffff)   // the GEMV takes them as 32-bit kernel arguments
+    return set_error("thin_linear: N=%lld and M=%lld must be below 2^31", (long long)N, (long long)M);
   pl.kind = kind;
   pl.glu = glu;
   // GEMV activations held per chunk: 256 (2 load steps) or 1024 (8) k elements
@@ -995,8 +1001,15 @@ void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t strea
   constexpr int G = RW / 4;
   constexpr int GB = GLU ? (SIMSD_GEMV_GB_ALL ? G / 2 : (G >= 4 ? 2 : 1))
                          : (SIMSD_GEMV_GB_ALL ? G : (RW >= 8 ? 2 : 1));
-  if (pl.split > 1) launch<true>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>, pl, args, stream);
-  else launch<false>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>, pl, args, stream);
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  auto run = [&](auto kern) {
+    const dim3 grid((unsigned)pl.tiles_n, (unsigned)pl.split, (unsigned)pl.tiles_m);
+    hipLaunchKernelGGL(kern, grid, dim3(64 * KS), 0, stream, args.w, args.x, args.w2, (uint32_t)(args.K * ES),
+                       (uint32_t)(args.swn * ES), (uint32_t)(args.sxm * ES), (uint32_t)(args.sw2n * ES), (int)args.N,
+                       (int)args.M, args.steps, args.steps_per_split, args);
+  };
+  if (pl.split > 1) run(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>);
+  else run(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>);
 }
 
 // The big chunk holds CH x (row groups + token sets) operand registers; at 8
