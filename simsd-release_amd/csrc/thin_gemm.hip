@@ -479,7 +479,10 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(const char* __restr
 // tile (accum_lds).  Activations are the B operand as in thin_gemm_kernel.
 
 template <int DT, int RB, int CB, int KS, int U, bool PARTIAL, bool GLU>
-__global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
+__global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __restrict__ w, const char* __restrict__ x,
+                                                                const char* __restrict__ w2, uint32_t Kb,
+                                                                uint32_t swn_b, uint32_t sxm_b, uint32_t sw2n_b, int N,
+                                                                int M, int steps, int steps_per_split, ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int NF = RB * CB;
   constexpr int ROWS = 16 * RB;
@@ -499,19 +502,17 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
   const int split_id = blockIdx.y;
 
   // chunks of 256 B per row (4 MFMA k-steps) of this workgroup, then of this wave
-  const int s_lo = split_id * a.steps_per_split;
-  const int s_hi = min(a.steps, s_lo + a.steps_per_split);
+  const int s_lo = split_id * steps_per_split;
+  const int s_hi = min(steps, s_lo + steps_per_split);
   const int span = max(0, s_hi - s_lo);
   const int per_w = (span + KS - 1) / KS;
   const int w0 = s_lo + wk * per_w;
   const int w1 = min(s_hi, w0 + per_w);
 
-  const uint32_t Kb = (uint32_t)(a.K * ES);
-  const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
-  const int64_t rows_valid = min((int64_t)OUT, a.N - n_tile);
-  const int64_t cols_valid = min((int64_t)(CB * 16), a.M - m_tile);
-  const rsrc_t rA = make_rsrc(a.w + n_tile * a.swn * ES, (uint32_t)(rows_valid - 1) * swn_b + Kb);
-  const rsrc_t rB = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+  const int64_t rows_valid = min((int64_t)OUT, (int64_t)N - n_tile);
+  const int64_t cols_valid = min((int64_t)(CB * 16), (int64_t)M - m_tile);
+  const rsrc_t rA = make_rsrc(w + n_tile * swn_b, (uint32_t)(rows_valid - 1) * swn_b + Kb);
+  const rsrc_t rB = make_rsrc(x + m_tile * sxm_b, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
   f32x4_t acc[RB][CB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -527,8 +528,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
     a_sn[rb] = swn_b;
   }
   if (GLU) {
-    const uint32_t sw2n_b = (uint32_t)(a.sw2n * ES);
-    ra[RB - 1] = make_rsrc(a.w2 + n_tile * a.sw2n * ES, (uint32_t)(rows_valid - 1) * sw2n_b + Kb);
+    ra[RB - 1] = make_rsrc(w2 + n_tile * sw2n_b, (uint32_t)(rows_valid - 1) * sw2n_b + Kb);
     a_row0[RB - 1] = 0u;
     a_sn[RB - 1] = sw2n_b;
   }
@@ -552,11 +552,11 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
     for (int cb = 0; cb < CB; ++cb) {
       const int64_t m = m_tile + cb * 16 + r;
       const int64_t nb = n_tile + rb * 16 + 4 * g;
-      if (m < a.M) {
+      if (m < M) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t n = nb + j;
-          if (n < a.N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
+          if (n < N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
         }
       }
     }
@@ -575,7 +575,10 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(ThinArgs a) {
 // instead of CB * 16 / (16 RB) -- a quarter at 128 rows.  No cross-wave sum:
 // each wave writes its own outputs.
 template <int DT, int RB, int CB, int KS, int U, bool PARTIAL, bool GLU>
-__global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(ThinArgs a) {
+__global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(const char* __restrict__ w, const char* __restrict__ x,
+                                                               const char* __restrict__ w2, uint32_t Kb,
+                                                               uint32_t swn_b, uint32_t sxm_b, uint32_t sw2n_b, int N,
+                                                               int M, int steps, int steps_per_split, ThinArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   static_assert(!GLU || RB == 2, "gated: block 0 = gate rows, block 1 = the same rows of up");
   constexpr int WROWS = 16 * RB;                  // weight rows per wave
@@ -596,18 +599,16 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(ThinArgs a) {
   const int64_t n_wave = n_tile + (int64_t)wk * WOUT;
   const int64_t m_tile = (int64_t)blockIdx.z * XROWS;
   const int split_id = blockIdx.y;
-  const int c0 = split_id * a.steps_per_split;
-  const int c1 = min(a.steps, c0 + a.steps_per_split);
+  const int c0 = split_id * steps_per_split;
+  const int c1 = min(steps, c0 + steps_per_split);
 
-  const uint32_t Kb = (uint32_t)(a.K * ES);
-  const uint32_t swn_b = (uint32_t)(a.swn * ES), sxm_b = (uint32_t)(a.sxm * ES);
   // a wave past N keeps loading (zeros) and meeting the barriers
-  const int64_t rows_w = max((int64_t)0, min((int64_t)WOUT, a.N - n_wave));
-  const int64_t cols_valid = min((int64_t)XROWS, a.M - m_tile);
+  const int64_t rows_w = max((int64_t)0, min((int64_t)WOUT, (int64_t)N - n_wave));
+  const int64_t cols_valid = min((int64_t)XROWS, (int64_t)M - m_tile);
   rsrc_t ra[RB];
   uint32_t a_row0[RB], a_sn[RB];
   {
-    const rsrc_t rw = make_rsrc(a.w + (rows_w > 0 ? n_wave * a.swn * ES : 0),
+    const rsrc_t rw = make_rsrc(w + (rows_w > 0 ? n_wave * swn_b : 0),
                                 rows_w > 0 ? (uint32_t)(rows_w - 1) * swn_b + Kb : 0u);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -616,14 +617,13 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(ThinArgs a) {
       a_sn[rb] = swn_b;
     }
     if (GLU) {
-      const uint32_t sw2n_b = (uint32_t)(a.sw2n * ES);
-      ra[RB - 1] = make_rsrc(a.w2 + (rows_w > 0 ? n_wave * a.sw2n * ES : 0),
+      ra[RB - 1] = make_rsrc(w2 + (rows_w > 0 ? n_wave * sw2n_b : 0),
                              rows_w > 0 ? (uint32_t)(rows_w - 1) * sw2n_b + Kb : 0u);
       a_row0[RB - 1] = 0u;
       a_sn[RB - 1] = sw2n_b;
     }
   }
-  const rsrc_t rx = make_rsrc(a.x + m_tile * a.sxm * ES, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
+  const rsrc_t rx = make_rsrc(x + m_tile * sxm_b, (uint32_t)(cols_valid - 1) * sxm_b + Kb);
   f32x4_t acc[RB][CB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -725,11 +725,11 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(ThinArgs a) {
     for (int cb = 0; cb < CB; ++cb) {
       const int64_t m = m_tile + cb * 16 + r;
       const int64_t nb = n_wave + rb * 16 + 4 * g;
-      if (m < a.M) {
+      if (m < M) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t n = nb + j;
-          if (n < a.N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
+          if (n < N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
         }
       }
     }
@@ -958,6 +958,18 @@ void launch(Kern k, const ThinPlan& pl, const ThinArgs& args, hipStream_t stream
   hipLaunchKernelGGL(k, grid, dim3(64 * pl.ks), 0, stream, args);
 }
 
+// The vector-capable kernels (GEMV, LDS and shared-activation tiles) take the
+// fields their first loads depend on as leading scalar arguments, which the
+// build preloads into SGPRs, then ThinArgs for the rest.
+template <int DT, typename Kern>
+void launch_hot(Kern k, const ThinPlan& pl, const ThinArgs& a, hipStream_t stream) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const dim3 grid((unsigned)pl.tiles_n, (unsigned)pl.split, (unsigned)pl.tiles_m);
+  hipLaunchKernelGGL(k, grid, dim3(64 * pl.ks), 0, stream, a.w, a.x, a.w2, (uint32_t)(a.K * ES),
+                     (uint32_t)(a.swn * ES), (uint32_t)(a.sxm * ES), (uint32_t)(a.sw2n * ES), (int)a.N, (int)a.M,
+                     a.steps, a.steps_per_split, a);
+}
+
 template <int DT, int RT, int RB, int CB, int KS, bool FAST>
 void launch_gemm(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = (RB * CB == 1) ? SIMSD_THIN_U : SIMSD_THIN_U / 2;
@@ -1001,15 +1013,8 @@ void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t strea
   constexpr int G = RW / 4;
   constexpr int GB = GLU ? (SIMSD_GEMV_GB_ALL ? G / 2 : (G >= 4 ? 2 : 1))
                          : (SIMSD_GEMV_GB_ALL ? G : (RW >= 8 ? 2 : 1));
-  constexpr int ES = DTypeInfo<DT>::kSize;
-  auto run = [&](auto kern) {
-    const dim3 grid((unsigned)pl.tiles_n, (unsigned)pl.split, (unsigned)pl.tiles_m);
-    hipLaunchKernelGGL(kern, grid, dim3(64 * KS), 0, stream, args.w, args.x, args.w2, (uint32_t)(args.K * ES),
-                       (uint32_t)(args.swn * ES), (uint32_t)(args.sxm * ES), (uint32_t)(args.sw2n * ES), (int)args.N,
-                       (int)args.M, args.steps, args.steps_per_split, args);
-  };
-  if (pl.split > 1) run(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>);
-  else run(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>);
+  if (pl.split > 1) launch_hot<DT>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>, pl, args, stream);
+  else launch_hot<DT>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>, pl, args, stream);
 }
 
 // The big chunk holds CH x (row groups + token sets) operand registers; at 8
@@ -1057,8 +1062,8 @@ void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 template <int DT, int RB, int CB, int KS, bool GLU>
 void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = (RB * CB == 1) ? SIMSD_LDS_U : (SIMSD_LDS_U + 1) / 2;
-  if (pl.split > 1) launch<true>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
-  else launch<false>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
+  if (pl.split > 1) launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
+  else launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
 }
 
 template <int DT, int RB, int CB, bool GLU = false>
@@ -1077,8 +1082,8 @@ void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 template <int DT, int RB, int CB, int KS, bool GLU>
 void launch_xs(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = SIMSD_XS_U;
-  if (pl.split > 1) launch<true>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
-  else launch<false>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
+  if (pl.split > 1) launch_hot<DT>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
+  else launch_hot<DT>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
 }
 
 // (rb, ks) of a shared-activation plan: (2, 2), (2, 3), (2, 4); ungated also
