@@ -500,6 +500,11 @@ SIMSD_DEV void put_through(float* p, float v) {
   if (SIMSD_HEAD_SPLIT_SYNC) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   else *p = v;
 }
+SIMSD_DEV void put_through2(float* p, float v0, float v1) {   // p 8-byte aligned
+  const uint64_t b = (uint64_t)__float_as_uint(v0) | ((uint64_t)__float_as_uint(v1) << 32);
+  if (SIMSD_HEAD_SPLIT_SYNC) __hip_atomic_store(reinterpret_cast<uint64_t*>(p), b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  else *reinterpret_cast<uint64_t*>(p) = b;
+}
 SIMSD_DEV float get_through(const float* p) {
   if (SIMSD_HEAD_SPLIT_SYNC) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   return *p;
@@ -639,21 +644,22 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     }
     return;
   }
-  // this workgroup's partial: [h][sp][row][d] and (max, sum) [h][sp][row]
+  // this workgroup's partial: [h][sp][row][d] and (max, sum) [h][sp][row],
+  // two values per write-through store
   const int64_t pbase = ((int64_t)h * S + sp) * ROWS;
-  for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
-    const int row = e / kHeadDim, d = e % kHeadDim;
+  for (int e = threadIdx.x; e < ROWS * kHeadDim / 2; e += 64 * W) {
+    const int row = e / (kHeadDim / 2), d = (e % (kHeadDim / 2)) * 2;
     if (row >= a.rows) break;
-    float o = 0.f;
+    float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (int v = 0; v < W; ++v) o += o_sh[v][row][d] * wt_sh[v][row];
-    put_through(a.o_part + (pbase + row) * kHeadDim + d, o);
+    for (int v = 0; v < W; ++v) {
+      o0 += o_sh[v][row][d] * wt_sh[v][row];
+      o1 += o_sh[v][row][d + 1] * wt_sh[v][row];
+    }
+    put_through2(a.o_part + (pbase + row) * kHeadDim + d, o0, o1);
   }
-  if (threadIdx.x < a.rows) {
-    float* ml = reinterpret_cast<float*>(a.ml_part + pbase + threadIdx.x);
-    put_through(ml, mx_sh[threadIdx.x]);
-    put_through(ml + 1, l_sh[threadIdx.x]);
-  }
+  if (threadIdx.x < a.rows)
+    put_through2(reinterpret_cast<float*>(a.ml_part + pbase + threadIdx.x), mx_sh[threadIdx.x], l_sh[threadIdx.x]);
   // Every thread's stores precede the barrier; thread 0's arrival follows it
   // (the workgroup barrier orders them at workgroup scope, the arrival's
   // release extends that to the agent).
@@ -663,30 +669,32 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   if (!last_sh) return;
   // this head's partials, workgroup q at [q][row].  The partial rows and the
   // (max, sum) pairs are all loaded before any is used, so the merge waits
-  // for one round trip.  Loads are unconditional (workgroups q >= S re-read
-  // the last one's; rows past a.rows read the workspace's row padding) so that
-  // none waits behind a branch; unused values are dropped by selects.
-  constexpr int kPerThread = ROWS * kHeadDim / (64 * W);
-  const float* pO = a.o_part + (int64_t)h * S * ROWS * kHeadDim;
-  const float* pML = reinterpret_cast<const float*>(a.ml_part + (int64_t)h * S * ROWS);
-  float v[kPerThread][kHeadMaxSplit];
+  // for one round trip: plain 16-byte loads, ordered after the writers'
+  // stores by the arrival's release and the last arriver's acquire (which
+  // also drops this CU's stale cache lines).  Loads are unconditional
+  // (workgroups q >= S re-read the last one's; rows past a.rows read the
+  // workspace's row padding) so that none waits behind a branch; unused
+  // values are dropped by selects.
+  constexpr int kPer4 = ROWS * kHeadDim / 4 / (64 * W);
+  static_assert(kPer4 >= 1 && ROWS * kHeadDim % (4 * 64 * W) == 0, "whole float4 units per thread");
+  const float4* pO = reinterpret_cast<const float4*>(a.o_part + (int64_t)h * S * ROWS * kHeadDim);
+  const float2* pML = a.ml_part + (int64_t)h * S * ROWS;
+  float4 v4[kPer4][kHeadMaxSplit];
 #pragma unroll
-  for (int i = 0; i < kPerThread; ++i) {
-    const int e = (int)threadIdx.x + i * 64 * W;
-    const int row = e / kHeadDim, d = e % kHeadDim;
+  for (int i = 0; i < kPer4; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;   // float4 unit: row e / 32, dims 4 (e % 32) ..
 #pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q) v[i][q] = get_through(pO + ((q < S ? q : S - 1) * ROWS + row) * kHeadDim + d);
+    for (int q = 0; q < kHeadMaxSplit; ++q)
+      v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
   }
   if (threadIdx.x < a.rows) {
     const int row = threadIdx.x;
     float pm[kHeadMaxSplit], pl[kHeadMaxSplit];
 #pragma unroll
     for (int q = 0; q < kHeadMaxSplit; ++q) {
-      const int qq = q < S ? q : S - 1;
-      pm[q] = get_through(pML + (qq * ROWS + row) * 2);
-      pl[q] = get_through(pML + (qq * ROWS + row) * 2 + 1);
-      pm[q] = q < S ? pm[q] : -INFINITY;
-      pl[q] = q < S ? pl[q] : 0.f;
+      const float2 ml = pML[(q < S ? q : S - 1) * ROWS + row];
+      pm[q] = q < S ? ml.x : -INFINITY;
+      pl[q] = q < S ? ml.y : 0.f;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -703,14 +711,24 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kPerThread; ++i) {
+  for (int i = 0; i < kPer4; ++i) {
     const int e = (int)threadIdx.x + i * 64 * W;
-    const int row = e / kHeadDim, d = e % kHeadDim;
+    const int row = e / (kHeadDim / 4), d = (e % (kHeadDim / 4)) * 4;
     if (row < a.rows) {
-      float o = 0.f;
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
 #pragma unroll
-      for (int q = 0; q < kHeadMaxSplit; ++q) o += q < S ? v[i][q] * wts_sh[q][row] : 0.f;
-      put(row, d, o, l_sh[row]);
+      for (int q = 0; q < kHeadMaxSplit; ++q) {
+        const float wt = wts_sh[q][row];
+        o0 += q < S ? v4[i][q].x * wt : 0.f;
+        o1 += q < S ? v4[i][q].y * wt : 0.f;
+        o2 += q < S ? v4[i][q].z * wt : 0.f;
+        o3 += q < S ? v4[i][q].w * wt : 0.f;
+      }
+      const float l = l_sh[row];
+      put(row, d, o0, l);
+      put(row, d + 1, o1, l);
+      put(row, d + 2, o2, l);
+      put(row, d + 3, o3, l);
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
