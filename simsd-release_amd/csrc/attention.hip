@@ -104,24 +104,28 @@ struct QkvArgs {
 // issued before its arithmetic.  Rounding points of the bf16 reference: the
 // norm is the stock RMSNorm (weight * dtype(x * r), r in fp32), then
 // q_embed = dtype(dtype(q * cos) + dtype(rotate_half(q) * sin)).
+// The fields the first loads depend on come as leading scalar arguments,
+// which the build preloads into SGPRs; the rest of QkvArgs is read after.
 template <int DT>
-__global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
+__global__ __launch_bounds__(512) void qkv_rope_cache_kernel(const char* __restrict__ qkv, const int64_t* __restrict__ pos,
+                                                             const int64_t* __restrict__ slots, const char* qn,
+                                                             const char* kn, int sqkv, int Hq, int Hkv, QkvArgs a) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   const int lane = threadIdx.x & 63;
   const int hh = (int)blockIdx.y * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
-  if (hh >= a.Hq + 2 * a.Hkv) return;
+  if (hh >= Hq + 2 * Hkv) return;
   const int64_t m = blockIdx.x;
-  const int64_t p = a.pos[m];
-  const int64_t s1 = a.slots[m];
+  const int64_t p = pos[m];
+  const int64_t s1 = slots[m];
   const int64_t s2 = a.slots2 != nullptr ? a.slots2[m] : -1;
   const bool pos_ok = p >= 0 && p < a.n_pos;
   const bool s1_ok = s1 >= 0 && s1 < a.L;
   const bool s2_ok = s2 >= 0 && s2 < a.L;
   const int d0 = lane, d1 = lane + 64;
-  const char* src = a.qkv + (m * a.sqkv + (int64_t)hh * kHeadDim) * ES;
-  const bool is_v = hh >= a.Hq + a.Hkv;
-  const bool is_q = hh < a.Hq;
-  const char* nwt = is_q ? a.qn : a.kn;
+  const char* src = qkv + (m * sqkv + (int64_t)hh * kHeadDim) * ES;
+  const bool is_v = hh >= Hq + Hkv;
+  const bool is_q = hh < Hq;
+  const char* nwt = is_q ? qn : kn;
   float x0 = load_elem<DT>(src, d0), x1 = load_elem<DT>(src, d1);
   float w0 = 1.f, w1 = 1.f, c0 = 0.f, c1 = 0.f, n0 = 0.f, n1 = 0.f;
   if (!is_v) {
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
     }
   }
   if (is_v) {   // v head: copy into the V tiles
-    char* base = a.vc + (int64_t)(hh - a.Hq - a.Hkv) * a.sh * ES;
+    char* base = a.vc + (int64_t)(hh - Hq - Hkv) * a.sh * ES;
     if (s1_ok) {
       store_elem<DT>(base, v_tile_index(s1, d0), x0);
       store_elem<DT>(base, v_tile_index(s1, d1), x1);
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(QkvArgs a) {
     store_elem<DT>(dst, d0, y0);
     store_elem<DT>(dst, d1, y1);
   } else if (pos_ok) {
-    char* base = a.kc + (int64_t)(hh - a.Hq) * a.sh * ES;
+    char* base = a.kc + (int64_t)(hh - Hq) * a.sh * ES;
     if (s1_ok) {
       store_elem<DT>(base, k_tile_index(s1, d0), y0);
       store_elem<DT>(base, k_tile_index(s1, d1), y1);
@@ -228,18 +232,22 @@ struct WaveKV {
 };
 
 template <int DT, int RBW>
-SIMSD_DEV WaveKV<RBW> wave_kv(const AttnArgs& a, int h, const int (&tok)[RBW], int g, int r) {
+SIMSD_DEV WaveKV<RBW> wave_kv(const char* kc, const char* vc, int64_t sh, uint32_t head_bytes, const AttnArgs& a, int h,
+                              const int (&tok)[RBW], int g, int r) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   WaveKV<RBW> w;
-  const uint32_t head_bytes = (uint32_t)(a.L_cap * kHeadDim * ES);
-  w.rk = make_rsrc(a.kc + (int64_t)h * a.sh * ES, head_bytes);
-  w.rv = make_rsrc(a.vc + (int64_t)h * a.sh * ES, head_bytes);
+  w.rk = make_rsrc(kc + (int64_t)h * sh * ES, head_bytes);
+  w.rv = make_rsrc(vc + (int64_t)h * sh * ES, head_bytes);
   w.rm = make_rsrc(a.mask, a.mask != nullptr ? (uint32_t)(a.M * a.smask) : 0u);
   w.k_off = (uint32_t)(g * 256 + r * 16);
   w.v_off = (uint32_t)(r * 64 + g * 16);
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) w.m_off[rb] = (uint32_t)(tok[rb] * a.smask + 4 * g);
   return w;
+}
+template <int DT, int RBW>
+SIMSD_DEV WaveKV<RBW> wave_kv(const AttnArgs& a, int h, const int (&tok)[RBW], int g, int r) {
+  return wave_kv<DT, RBW>(a.kc, a.vc, a.sh, (uint32_t)(a.L_cap * kHeadDim * DTypeInfo<DT>::kSize), a, h, tok, g, r);
 }
 
 // Operands of one 32-key step: K tiles (A of S^T = K.Q^T), V tiles (A of
@@ -535,10 +543,16 @@ constexpr int kHeadMaxSplit = SIMSD_HEAD_MAX_SPLIT;   // workgroups per KV head 
 constexpr int kHeadW1 = SIMSD_HEAD_W1;
 constexpr int kHeadW2 = 4;
 
+// The fields the first loads depend on come as leading scalar arguments,
+// which the build preloads into SGPRs; the rest of AttnArgs is read after.
 template <int DT, int RBW, int W>
-__global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __restrict__ out, int64_t so_m,
-                                                           int64_t so_h) {
+__global__ __launch_bounds__(64 * W) void attn_head_kernel(const char* __restrict__ q, const char* __restrict__ kc,
+                                                           const char* __restrict__ vc,
+                                                           const int64_t* __restrict__ lv_dev, int sq_m, int sq_h,
+                                                           int sh, uint32_t head_bytes, int M, int n_rep, AttnArgs a,
+                                                           char* __restrict__ out, int64_t so_m, int64_t so_h) {
   constexpr int ROWS = RBW * 16;
+  const int rows = n_rep * M;   // query rows of this KV head's group
   constexpr int kSplitMin = RBW == 1 ? kHeadSplitMinSlots1 : kHeadSplitMinSlots2;
   constexpr int OSTR = kHeadDim + 4;   // padded rows: the b128 writes of 16 rows spread over the banks
   __shared__ __attribute__((aligned(16))) float o_sh[W][ROWS][OSTR];
@@ -561,14 +575,14 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) {
     const int row = rb * 16 + r;
-    row_ok[rb] = row < a.rows;
-    const int i = row_ok[rb] ? row / (int)a.M : 0;
-    tok[rb] = row_ok[rb] ? row % (int)a.M : 0;
-    const char* qp = a.q + ((int64_t)tok[rb] * a.sq_m + (int64_t)(h * a.n_rep + i) * a.sq_h) * ES;
+    row_ok[rb] = row < rows;
+    const int i = row_ok[rb] ? row / (int)M : 0;
+    tok[rb] = row_ok[rb] ? row % (int)M : 0;
+    const char* qp = q + ((int64_t)tok[rb] * sq_m + (int64_t)(h * n_rep + i) * sq_h) * ES;
 #pragma unroll
     for (int ds = 0; ds < kDSteps; ++ds) qf[rb][ds] = load16_sel(qp + (ds * 32 + 8 * g) * ES, row_ok[rb]);
   }
-  const WaveKV<RBW> w = wave_kv<DT, RBW>(a, h, tok, g, r);
+  const WaveKV<RBW> w = wave_kv<DT, RBW>(kc, vc, sh, head_bytes, a, h, tok, g, r);
   StepBuf<RBW> bA, bB;
   int c = (sp * W + wv) * kKeyStep;
   attn_load<DT, RBW>(a, w, c, bA);   // before the valid length is known
@@ -582,8 +596,8 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   int64_t lv = a.L_valid;
-  if (a.lv_dev != nullptr) {
-    const int64_t d = *a.lv_dev;
+  if (lv_dev != nullptr) {
+    const int64_t d = *lv_dev;
     lv = d < 0 ? 0 : (d < lv ? d : lv);
   }
   const int ce = (int)lv;
@@ -631,14 +645,14 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   }
   __syncthreads();
   auto put = [&](int row, int d, float o, float l) {
-    const int i = row / (int)a.M;
-    const int64_t m = row % (int)a.M;
-    store_elem<DT>(out, m * so_m + (int64_t)(h * a.n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
+    const int i = row / (int)M;
+    const int64_t m = row % (int)M;
+    store_elem<DT>(out, m * so_m + (int64_t)(h * n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
   };
   if (S == 1) {
     for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
       const int row = e / kHeadDim, d = e % kHeadDim;
-      if (row >= a.rows) break;
+      if (row >= rows) break;
       float o = 0.f;
 #pragma unroll
       for (int v = 0; v < W; ++v) o += o_sh[v][row][d] * wt_sh[v][row];
@@ -651,7 +665,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   const int64_t pbase = ((int64_t)h * S + sp) * ROWS;
   for (int e = threadIdx.x; e < ROWS * kHeadDim / 2; e += 64 * W) {
     const int row = e / (kHeadDim / 2), d = (e % (kHeadDim / 2)) * 2;
-    if (row >= a.rows) break;
+    if (row >= rows) break;
     float o0 = 0.f, o1 = 0.f;
 #pragma unroll
     for (int v = 0; v < W; ++v) {
@@ -660,7 +674,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     }
     put_through2(a.o_part + (pbase + row) * kHeadDim + d, o0, o1);
   }
-  if (threadIdx.x < a.rows)
+  if (threadIdx.x < rows)
     put_through2(reinterpret_cast<float*>(a.ml_part + pbase + threadIdx.x), mx_sh[threadIdx.x], l_sh[threadIdx.x]);
   // Every thread's stores precede the barrier; thread 0's arrival follows it
   // (the workgroup barrier orders them at workgroup scope, the arrival's
@@ -674,7 +688,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   // for one round trip: plain 16-byte loads, ordered after the writers'
   // stores by the arrival's release and the last arriver's acquire (which
   // also drops this CU's stale cache lines).  Loads are unconditional
-  // (workgroups q >= S re-read the last one's; rows past a.rows read the
+  // (workgroups q >= S re-read the last one's; rows past rows read the
   // workspace's row padding) so that none waits behind a branch; unused
   // values are dropped by selects.
   constexpr int kPer4 = ROWS * kHeadDim / 4 / (64 * W);
@@ -689,7 +703,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
     for (int q = 0; q < kHeadMaxSplit; ++q)
       v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
   }
-  if (threadIdx.x < a.rows) {
+  if (threadIdx.x < rows) {
     const int row = threadIdx.x;
     float pm[kHeadMaxSplit], pl[kHeadMaxSplit];
 #pragma unroll
@@ -716,7 +730,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(AttnArgs a, char* __r
   for (int i = 0; i < kPer4; ++i) {
     const int e = (int)threadIdx.x + i * 64 * W;
     const int row = e / (kHeadDim / 4), d = (e % (kHeadDim / 4)) * 4;
-    if (row < a.rows) {
+    if (row < rows) {
       float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
 #pragma unroll
       for (int q = 0; q < kHeadMaxSplit; ++q) {
@@ -964,6 +978,7 @@ extern "C" int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q
     return set_error("qkv_rope_cache: the cache needs L %% 32 == 0 and a head stride of at least L * %d", kHeadDim);
   if (M == 0) return 0;
   if (M > 0x7fffffff) return set_error("qkv_rope_cache: too many tokens");
+  if (sqkv < 0 || sqkv > 0x7fffffff) return set_error("qkv_rope_cache: row stride out of range");
   if (!qkv || !cos || !sin || !pos || !slots || !k_cache || !v_cache || !q_out)
     return set_error("qkv_rope_cache: null pointer");
   QkvArgs a{};
@@ -978,8 +993,9 @@ extern "C" int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q
   const int waves = heads < 8 ? heads : 8;
   const dim3 grid((unsigned)M, (unsigned)((heads + waves - 1) / waves));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == kBF16) hipLaunchKernelGGL(qkv_rope_cache_kernel<kBF16>, grid, dim3(64 * waves), 0, st, a);
-  else hipLaunchKernelGGL(qkv_rope_cache_kernel<kF16>, grid, dim3(64 * waves), 0, st, a);
+  auto kern = dtype == kBF16 ? qkv_rope_cache_kernel<kBF16> : qkv_rope_cache_kernel<kF16>;
+  hipLaunchKernelGGL(kern, grid, dim3(64 * waves), 0, st, a.qkv, a.pos, a.slots, a.qn, a.kn, (int)a.sqkv, a.Hq,
+                     a.Hkv, a);
   return check_launch("qkv_rope_cache");
 }
 
@@ -1005,6 +1021,8 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
                      kHeadDim);
   if (L_cap * kHeadDim * 2 > (int64_t)0xFFFFFFF0) return set_error("block_attention: L_cap too large");
   if (!q || !k_cache || !v_cache || !out) return set_error("block_attention: null pointer");
+  if (sq_m < 0 || sq_m > 0x7fffffff || sq_h < 0 || sq_h > 0x7fffffff || kv_head_stride > 0x7fffffff)
+    return set_error("block_attention: strides must fit 31 bits");   // 32-bit kernel arguments
   const AttnPlan pl = attn_plan(M, Hq, Hkv, L_valid);
   if (pl.rows > 65536) return set_error("block_attention: %d query rows per KV head exceed 65536", pl.rows);
   // 16-byte loads of q rows and of the K / V tiles
@@ -1035,10 +1053,15 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
     if (pl.head) {
       char* o = static_cast<char*>(out);
       const dim3 hgrid((unsigned)pl.split, (unsigned)Hkv);
+      const uint32_t head_bytes = (uint32_t)(L_cap * kHeadDim * 2);
       if (pl.rbw == 2)
-        hipLaunchKernelGGL((attn_head_kernel<DT, 2, kHeadW2>), hgrid, dim3(64 * kHeadW2), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 2, kHeadW2>), hgrid, dim3(64 * kHeadW2), 0, st, a.q, a.kc, a.vc,
+                           a.lv_dev, (int)a.sq_m, (int)a.sq_h, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, o, so_m,
+                           so_h);
       else
-        hipLaunchKernelGGL((attn_head_kernel<DT, 1, kHeadW1>), hgrid, dim3(64 * kHeadW1), 0, st, a, o, so_m, so_h);
+        hipLaunchKernelGGL((attn_head_kernel<DT, 1, kHeadW1>), hgrid, dim3(64 * kHeadW1), 0, st, a.q, a.kc, a.vc,
+                           a.lv_dev, (int)a.sq_m, (int)a.sq_h, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, o, so_m,
+                           so_h);
       return;
     }
     if (pl.ksplit) {
