@@ -925,7 +925,8 @@ def run_floor(args, torch, dev):
     GEMV's access pattern (4 rows x 256 B per load, non-temporal) at every
     rows-per-workgroup x waves geometry, the fastest kept, over 24 distinct
     weights so the MALL cannot serve repeats; beside it the C1 GEMV on the
-    same weights."""
+    same weights.  Then the same read on 8..256 workgroups of 512 KB each:
+    the rate one CU sustains."""
     from kernels import _native
     from kernels.thin_linear_fused import thin_linear
 
@@ -953,6 +954,25 @@ def run_floor(args, torch, dev):
         best = min(sweep, key=sweep.get)
         read_us = sweep[best]
         gemv_us = graph_us_per_call(torch, [lambda w=w: thin_linear(x, w) for w in ws], reps=reps)
+        # what one CU streams: the same read on a few workgroups (one per CU),
+        # 512 KB each (4 rows x 128 KB, 8 waves), over enough distinct
+        # buffers that the MALL cannot serve repeats
+        per_wg = {}
+        per_wg_bytes, rpw = 512 << 10, 4
+        for wgs in (8, 32, 128, 256):
+            rows = wgs * rpw
+            nb = rows * (per_wg_bytes // rpw)
+            bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(max(2, min(24, (1 << 30) // nb)))]
+            sink_w = torch.zeros(rows, dtype=torch.int32, device=dev)
+
+            def rd(b, rows=rows, sink_w=sink_w):
+                return lambda: _native.check(lib.simsd_probe_read(b.data_ptr(), rows, per_wg_bytes // rpw, rpw, 8,
+                                                                  sink_w.data_ptr(), sink_w.numel(),
+                                                                  _native.stream_of(dev)), "probe_read")
+            us = graph_us_per_call(torch, [rd(b) for b in bufs], reps=reps)
+            per_wg[str(wgs)] = {"us": round(us, 3), "GBps_per_workgroup": round(per_wg_bytes / (us * 1e-6) / 1e9, 1),
+                                "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
+            del bufs
     wbytes = N * K * BF16
     gemv_bytes = linear_bytes(M, K, N)
     return {
@@ -969,6 +989,7 @@ def run_floor(args, torch, dev):
         "c1_gemv_us": round(gemv_us, 3),
         "c1_gemv_frac_of_8TBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "c1_gemv_over_read": round(gemv_us / read_us, 4),
+        "read_512KB_per_workgroup_by_workgroups": per_wg,
     }, M
 
 
