@@ -414,22 +414,29 @@ struct TileRows {
   int64_t token;  // row of x
 };
 
-SIMSD_DEV bool decode_tile(const MoeArgs& a, int t, int r, TileRows& tr) {
-  if (t < a.num_tiles) {
-    const int e = a.tile_expert[t];
-    if (e < 0 || e >= a.E) return false;
-    const int s = a.slots[(int64_t)t * kTile + r];
+SIMSD_DEV bool decode_tile(const int32_t* tile_expert, const int32_t* slots, int num_tiles, int E, int k, int T,
+                           int t, int r, TileRows& tr) {
+  if (t < num_tiles) {
+    const int e = tile_expert[t];
+    if (e < 0 || e >= E) return false;
+    const int s = slots[(int64_t)t * kTile + r];
     tr.e = e;
     tr.slot = s;
-    tr.token = s >= 0 ? s / a.k : -1;
+    tr.token = s >= 0 ? s / k : -1;
   } else {
-    const int64_t tok = (int64_t)(t - a.num_tiles) * kTile + r;
+    const int64_t tok = (int64_t)(t - num_tiles) * kTile + r;
     tr.e = -1;
-    tr.slot = tok < a.T ? tok : -1;
+    tr.slot = tok < T ? tok : -1;
     tr.token = tr.slot;
   }
   return true;
 }
+
+// The MoE kernels take the tile table and two pointers and two strides their
+// first loads depend on as leading scalar arguments, which the build preloads
+// into SGPRs; the rest of MoeArgs is read where it is used.
+#define SIMSD_MOE_HOT const int32_t *__restrict__ tile_expert, const int32_t *__restrict__ slots, int num_tiles, \
+    int E, int k, int T, const char *__restrict__ p0, const char *__restrict__ p1, int i0, int i1, MoeArgs a
 
 SIMSD_DEV float silu_f32(float v) { return v / (1.f + expf(-v)); }
 
@@ -444,20 +451,21 @@ SIMSD_DEV float silu_f32(float v) { return v / (1.f + expf(-v)); }
 #define SIMSD_MOE_DN_U 4   // 256-byte k chunks per load batch in down
 #endif
 
+// p0, p1: w_gate, w_up; i0, i1: their expert strides (elements)
 template <int DT, bool FAST>
-__global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256) void moe_gate_up_kernel(SIMSD_MOE_HOT) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int KS = 4;
   __shared__ __attribute__((aligned(16))) char gu_tile[KS][FAST ? 32 * kLdsRow : 16];
   const int lane = threadIdx.x & 63, wk = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int t = blockIdx.x;
-  const int64_t i0 = (int64_t)blockIdx.y * 16;
+  const int64_t c0i = (int64_t)blockIdx.y * 16;   // first intermediate column
   TileRows tr;
-  if (!decode_tile(a, t, r, tr)) return;
+  if (!decode_tile(tile_expert, slots, num_tiles, E, k, T, t, r, tr)) return;
   const bool shared = tr.e < 0;
   const int64_t II = shared ? a.Is : a.I;
-  if (i0 >= II) return;
+  if (c0i >= II) return;
   const char* wbase[2];
   int64_t a_sn[2], a_sk[2];
   if (shared) {
@@ -467,8 +475,8 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     a_sk[0] = a.shg_h * ES;
     a_sk[1] = a.shu_h * ES;
   } else {
-    wbase[0] = a.wg + (int64_t)tr.e * a.sge * ES;
-    wbase[1] = a.wu + (int64_t)tr.e * a.sue * ES;
+    wbase[0] = p0 + (int64_t)tr.e * i0 * ES;
+    wbase[1] = p1 + (int64_t)tr.e * i1 * ES;
     a_sn[0] = a.sgi; a_sn[1] = a.sui;
     a_sk[0] = a.sgh * ES;
     a_sk[1] = a.suh * ES;
@@ -488,10 +496,10 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     for (int b = 0; b < 2; ++b) {
       a_snb[b] = (uint32_t)(a_sn[b] * ES);
       ra[b] = make_rsrc(wbase[b], (uint32_t)(II - 1) * a_snb[b] + Kb);
-      a_row0[b] = (uint32_t)i0 * a_snb[b];
+      a_row0[b] = (uint32_t)c0i * a_snb[b];
     }
     const uint32_t sxt_b = (uint32_t)(a.sxt * ES);
-    const rsrc_t rB = make_rsrc(a.x, (uint32_t)(a.T - 1) * sxt_b + Kb);
+    const rsrc_t rB = make_rsrc(a.x, (uint32_t)(T - 1) * sxt_b + Kb);
     const uint32_t boff[1] = {tr.token >= 0 ? (uint32_t)tr.token * sxt_b : 0u};
     const bool bok[1] = {tr.token >= 0};
     const int chunks = (int)((Kb + kStep4Bytes - 1) / kStep4Bytes);
@@ -499,7 +507,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
     const int c0 = wk * per, c1 = min(chunks, c0 + per);
     accum_lds<DT, 2, 1, SIMSD_MOE_GU_U>(ra, a_row0, a_snb, rB, boff, bok, c0, c1, Kb, gu_tile[wk], acc);
   } else {
-    const int64_t i_row = min(i0 + r, II - 1);
+    const int64_t i_row = min(c0i + r, II - 1);
     const char* arow[2] = {wbase[0] + i_row * a_sn[0] * ES, wbase[1] + i_row * a_sn[1] * ES};
     const char* brow[1] = {tr.token >= 0 ? a.x + tr.token * a.sxt * ES : nullptr};
     // both A blocks share one k-stride in the generic gather; use per-block calls
@@ -517,7 +525,7 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
   char* orow = shared ? a.hs + tr.slot * a.Is * ES : a.h + tr.slot * a.I * ES;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int64_t i = i0 + 4 * g + j;
+    const int64_t i = c0i + 4 * g + j;
     if (i < II) {
       const float gv = round_to<DT>(acc[0][0][j]);
       const float uv = round_to<DT>(acc[1][0][j]);
@@ -530,7 +538,9 @@ __global__ __launch_bounds__(256) void moe_gate_up_kernel(MoeArgs a) {
 // down: one workgroup = one tile x 64 output features; each of the 4 waves owns
 // 16 rows of W_down over the whole I.
 template <int DT, bool FAST>
-__global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
+// p0, p1: w_down and the routed h rows; i0: w_down's expert stride, i1 its
+// row stride (elements)
+__global__ __launch_bounds__(256) void moe_down_kernel(SIMSD_MOE_HOT) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   __shared__ __attribute__((aligned(16))) char dn_tile[4][FAST ? 16 * kLdsRow : 16];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -538,20 +548,20 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
   const int t = blockIdx.x;
   const int64_t n0 = (int64_t)blockIdx.y * 64 + wv * 16;
   TileRows tr;
-  if (!decode_tile(a, t, r, tr)) return;
+  if (!decode_tile(tile_expert, slots, num_tiles, E, k, T, t, r, tr)) return;
   const bool shared = tr.e < 0;
   if (n0 >= a.H) return;
   const int64_t II = shared ? a.Is : a.I;
-  const char* wbase = shared ? a.shd : a.wd + (int64_t)tr.e * a.sde * ES;
-  const int64_t a_sn = shared ? a.shd_h : a.sdh;
+  const char* wbase = shared ? a.shd : p0 + (int64_t)tr.e * i0 * ES;
+  const int64_t a_sn = shared ? a.shd_h : (int64_t)i1;
   const int64_t a_sk = (shared ? a.shd_i : a.sdi) * ES;
-  const char* hbase = shared ? a.hs : a.h;   // slot-major (or token-major) h, row length II
+  const char* hbase = shared ? a.hs : p1;   // slot-major (or token-major) h, row length II
   const int steps = (int)((II * ES + kStepBytes - 1) / kStepBytes);
   f32x4_t acc[1][1] = {{f32x4_t{0.f, 0.f, 0.f, 0.f}}};
   if (FAST) {
     const uint32_t Kb = (uint32_t)(II * ES);
     const uint32_t sn_b = (uint32_t)(a_sn * ES);
-    const int64_t h_rows = shared ? a.T : a.T * a.k;
+    const int64_t h_rows = shared ? (int64_t)T : (int64_t)T * k;
     const rsrc_t ra[1] = {make_rsrc(wbase, (uint32_t)(a.H - 1) * sn_b + Kb)};
     const uint32_t a_row0[1] = {(uint32_t)n0 * sn_b};
     const uint32_t a_snb[1] = {sn_b};
@@ -578,26 +588,30 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeArgs a) {
 // then (shared expert) out = dtype(out + ys[t]).  The ids, weights and expert
 // outputs of 8 picks are loaded before any is used (one round trip, not 8);
 // rows of invalid ids are read but not added.
+// p0, p1: the routed expert outputs y and the ids; i0: H (the tile table
+// arguments are unused here)
 template <int DT>
-__global__ __launch_bounds__(256) void moe_combine_kernel(MoeArgs a) {
+__global__ __launch_bounds__(256) void moe_combine_kernel(SIMSD_MOE_HOT) {
   constexpr int J = 8;
   const int64_t t = blockIdx.y;
   const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (h >= a.H) return;
+  const int64_t H = i0;
+  if (h >= H) return;
+  const int64_t* ids = reinterpret_cast<const int64_t*>(p1);
   float acc = 0.f;
-  for (int j0 = 0; j0 < a.k; j0 += J) {
+  for (int j0 = 0; j0 < k; j0 += J) {
     int64_t e[J];
     float wv[J], yv[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const bool in = j0 + j < a.k;
-      e[j] = in ? a.ids[t * a.sidt + (j0 + j) * a.sidk] : -1;
+      const bool in = j0 + j < k;
+      e[j] = in ? ids[t * a.sidt + (j0 + j) * a.sidk] : -1;
       wv[j] = in ? a.topk_w[t * a.swt + (j0 + j) * a.swk] : 0.f;
-      yv[j] = in ? load_elem<DT>(a.y, (t * a.k + j0 + j) * a.H + h) : 0.f;
+      yv[j] = in ? load_elem<DT>(p0, (t * k + j0 + j) * H + h) : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < J; ++j)
-      if (e[j] >= 0 && e[j] < a.E) acc = __fadd_rn(acc, __fmul_rn(yv[j], wv[j]));
+      if (e[j] >= 0 && e[j] < E) acc = __fadd_rn(acc, __fmul_rn(yv[j], wv[j]));
   }
   float o = round_to<DT>(acc);
   if (a.shared_tiles > 0) o = o + load_elem<DT>(a.ys, t * a.H + h);
@@ -629,7 +643,9 @@ struct SmallUnit {
 };
 
 template <int DT, int G, int S, int W, int UM>
-__global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
+// p0, p1: w_down and the routed h rows; i0: w_down's expert stride, i1 its
+// row stride (elements)
+__global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(SIMSD_MOE_HOT) {
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int R = 4 * G;
   __shared__ float y_sh[kSmallSlots + kSmallT][R];   // [slot t*k + j | T*k + token][feature]
@@ -637,8 +653,8 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
   const int i4 = lane & 3, b4 = lane >> 2;
   const int64_t n0 = (int64_t)blockIdx.x * R;
   const int rows = (int)min((int64_t)R, a.H - n0);
-  const int n_units = a.num_tiles + (a.shared_tiles > 0 ? 1 : 0);
-  const int M = (int)(a.T * a.k);
+  const int n_units = num_tiles + (a.shared_tiles > 0 ? 1 : 0);
+  const int M = T * k;
   const uint32_t lane_k = (uint32_t)b4 * kLaneBytes;
 
   // descriptors of this wave's units: expert (-1 shared, -2 none) and the
@@ -651,14 +667,14 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
 #pragma unroll
   for (int i = 0; i < UM; ++i) {
     const int u = wv + i * W;
-    if (u < a.num_tiles) {
-      const int e = a.tile_expert[u];
-      ue[i] = (e >= 0 && e < a.E) ? e : -2;
+    if (u < num_tiles) {
+      const int e = tile_expert[u];
+      ue[i] = (e >= 0 && e < E) ? e : -2;
 #pragma unroll
-      for (int cs = 0; cs < kSets; ++cs) ucol[i][cs] = a.slots[(int64_t)u * kTile + 4 * cs + i4];
+      for (int cs = 0; cs < kSets; ++cs) ucol[i][cs] = slots[(int64_t)u * kTile + 4 * cs + i4];
     } else if (u < n_units) {
       ue[i] = -1;
-      ucol[i][0] = i4 < a.T ? i4 : -1;
+      ucol[i][0] = i4 < T ? i4 : -1;
 #pragma unroll
       for (int cs = 1; cs < kSets; ++cs) ucol[i][cs] = -1;
     } else {
@@ -670,13 +686,13 @@ __global__ __launch_bounds__(64 * W) void moe_down_combine_kernel(MoeArgs a) {
   auto w_rsrc = [&](int e, uint32_t& sn_b, uint32_t& Kb) {
     const bool shared = e < 0;
     Kb = (uint32_t)((shared ? a.Is : a.I) * ES);
-    const int64_t sn = shared ? a.shd_h : a.sdh;
+    const int64_t sn = shared ? a.shd_h : (int64_t)i1;
     sn_b = (uint32_t)(sn * ES);
-    const char* wb = (shared ? a.shd : a.wd + (int64_t)e * a.sde * ES) + n0 * sn * ES;
+    const char* wb = (shared ? a.shd : p0 + (int64_t)e * i0 * ES) + n0 * sn * ES;
     return make_rsrc(wb, (uint32_t)(rows - 1) * sn_b + Kb);
   };
   auto h_rsrc = [&](int e, uint32_t Kb) {
-    return make_rsrc(e < 0 ? a.hs : a.h, (uint32_t)(e < 0 ? a.T : M) * Kb);
+    return make_rsrc(e < 0 ? a.hs : p1, (uint32_t)(e < 0 ? T : M) * Kb);
   };
   auto load_b = [&](const rsrc_t& rH, uint32_t Kb, int col, u32x4_t (&B)[S]) {
 #pragma unroll
@@ -819,26 +835,37 @@ void launch_ffn(const MoeArgs& a, bool fast_gu, bool fast_dn, bool small, void* 
   const int tiles = a.num_tiles + a.shared_tiles;
   const int64_t imax = a.I > a.Is ? a.I : a.Is;
   dim3 g1((unsigned)tiles, (unsigned)((imax + 15) / 16));
-  if (fast_gu) hipLaunchKernelGGL((moe_gate_up_kernel<DT, true>), g1, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((moe_gate_up_kernel<DT, false>), g1, dim3(256), 0, stream, a);
+  const int E = a.E, k = a.k, T = (int)a.T, nt = a.num_tiles;
+  if (fast_gu)
+    hipLaunchKernelGGL((moe_gate_up_kernel<DT, true>), g1, dim3(256), 0, stream, a.tile_expert, a.slots, nt, E, k, T,
+                       a.wg, a.wu, (int)a.sge, (int)a.sue, a);
+  else
+    hipLaunchKernelGGL((moe_gate_up_kernel<DT, false>), g1, dim3(256), 0, stream, a.tile_expert, a.slots, nt, E, k, T,
+                       a.wg, a.wu, (int)a.sge, (int)a.sue, a);
   if constexpr (DT != kF32) {
     if (small) {
       constexpr int R = 4 * kSmallG;
       const dim3 gs((unsigned)((a.H + R - 1) / R));
       if (imax * DTypeInfo<DT>::kSize <= 4 * kStep4Bytes)
         hipLaunchKernelGGL((moe_down_combine_kernel<DT, kSmallG, 4, kSmallW, kSmallUM>), gs, dim3(64 * kSmallW), 0,
-                           stream, a);
+                           stream, a.tile_expert, a.slots, nt, E, k, T, a.wd, a.h, (int)a.sde, (int)a.sdh, a);
       else   // twice the k steps: 4 features per workgroup
         hipLaunchKernelGGL((moe_down_combine_kernel<DT, 1, 8, kSmallW, kSmallUM8>),
-                           dim3((unsigned)((a.H + 3) / 4)), dim3(64 * kSmallW), 0, stream, a);
+                           dim3((unsigned)((a.H + 3) / 4)), dim3(64 * kSmallW), 0, stream, a.tile_expert, a.slots, nt,
+                           E, k, T, a.wd, a.h, (int)a.sde, (int)a.sdh, a);
       return;
     }
   }
   dim3 g2((unsigned)tiles, (unsigned)((a.H + 63) / 64));
-  if (fast_dn) hipLaunchKernelGGL((moe_down_kernel<DT, true>), g2, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((moe_down_kernel<DT, false>), g2, dim3(256), 0, stream, a);
+  if (fast_dn)
+    hipLaunchKernelGGL((moe_down_kernel<DT, true>), g2, dim3(256), 0, stream, a.tile_expert, a.slots, nt, E, k, T, a.wd,
+                       a.h, (int)a.sde, (int)a.sdh, a);
+  else
+    hipLaunchKernelGGL((moe_down_kernel<DT, false>), g2, dim3(256), 0, stream, a.tile_expert, a.slots, nt, E, k, T,
+                       a.wd, a.h, (int)a.sde, (int)a.sdh, a);
   dim3 g3((unsigned)((a.H + 255) / 256), (unsigned)a.T);
-  hipLaunchKernelGGL((moe_combine_kernel<DT>), g3, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((moe_combine_kernel<DT>), g3, dim3(256), 0, stream, a.tile_expert, a.slots, nt, E, k, T, a.y,
+                     reinterpret_cast<const char*>(a.ids), (int)a.H, 0, a);
 }
 
 }  // namespace
@@ -975,6 +1002,9 @@ extern "C" int simsd_moe_grouped_ffn(
     return set_error("moe_grouped_ffn: null pointer");
   const int64_t shared_tiles = has_shared ? (T + kTile - 1) / kTile : 0;
   if (num_tiles + shared_tiles > 0x7fffffff) return set_error("moe_grouped_ffn: too many tiles");
+  auto fits = [](int64_t v) { return v >= -0x7fffffffll && v <= 0x7fffffffll; };
+  if (!fits(T) || !fits(H) || !fits(sge) || !fits(sue) || !fits(sde) || !fits(sdh))
+    return set_error("moe_grouped_ffn: T, H and the expert / row strides must fit 31 bits");   // kernel arguments
   MoeArgs a{};
   a.x = static_cast<const char*>(x); a.sxt = sxt; a.sxh = sxh;
   a.wg = static_cast<const char*>(w_gate); a.sge = sge; a.sgi = sgi; a.sgh = sgh;
