@@ -55,9 +55,9 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           H=2048, I=512, T tokens; cycled over 8 distinct layers.
 Each step is captured once in a HIP graph and replayed; the timed region is
 K replays bracketed by synchronisations and HIP events on the replay stream.
-The default run (c2) also times c1, c3m16, c3m32, c4t4, c4t16, c4t64 and c5
-and adds them under "extras" in the same JSON line (--no-extras skips them);
-progress goes to stderr.
+The default run (c2) also times c1, c3m16, c3m32, c4t4, c4t16, c4t64 and c5,
+each in a child process of its own, and adds them under "extras" in the same
+JSON line (--no-extras skips them); progress goes to stderr.
 
 value = algorithmic bytes per step / time per step (weights read once +
 activations in + outputs out).  The roofline object is for the dominant
@@ -1229,25 +1229,33 @@ _EXTRA_KEYS = ("value", "unit", "ms_per_step", "steps", "config", "roofline", "b
 
 
 def run_extras(args, torch, dev):
+    """Each extra workload in a process of its own, one after another: in the
+    process that has just run the C2 step, fresh allocations of the next
+    workload's weights stream measurably slower (C1 10.8 against 10.0 us per
+    call on one box), an effect of where the allocator places them, not of
+    the kernels."""
+    import subprocess
+
     out = {}
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     for wl in EXTRA_WORKLOADS:
-        sub = argparse.Namespace(**vars(args))
-        sub.workload = wl
+        steps = 10 if wl == "c5" else max(10, args.steps // 2)
+        warmup = 2 if wl == "c5" else max(2, args.warmup // 2)
+        cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--steps", str(steps),
+               "--warmup", str(warmup), "--no-extras"]
         # host-core baselines: the headline's, and C5's (one iteration scaled
         # from one timed layer of each model); the others would add minutes
-        sub.no_cpu_baseline = args.no_cpu_baseline or wl != "c5"
-        sub.steps = 10 if wl == "c5" else max(10, args.steps // 2)
-        sub.warmup = 2 if wl == "c5" else max(2, args.warmup // 2)
-        print(f"bench: extra workload {wl} ({sub.steps} steps)", file=sys.stderr, flush=True)
+        if args.no_cpu_baseline or wl != "c5":
+            cmd.append("--no-cpu-baseline")
+        print(f"bench: extra workload {wl} ({steps} steps, own process)", file=sys.stderr, flush=True)
         t0 = time.perf_counter()
-        if wl == "c5":
-            rec, _ = run_c5(sub, torch, dev)
-        elif wl.startswith("c4"):
-            rec, _ = run_moe(sub, torch, dev)
-        else:
-            rec, _ = run_linear(sub, torch, dev)
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
+        # the child's progress goes straight to this process's stderr
+        proc = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=420)
+        lines = [ln for ln in proc.stdout.splitlines() if ln.startswith("{")]
+        if proc.returncode != 0 or not lines:
+            raise RuntimeError(f"bench: extra workload {wl} failed (exit {proc.returncode})")
+        rec = json.loads(lines[-1])
         rec = {k: rec[k] for k in _EXTRA_KEYS if k in rec}
         rec["wall_s"] = round(time.perf_counter() - t0, 1)
         out[wl] = rec
