@@ -66,7 +66,10 @@ const char* simsd_last_error_string(void);
  * the kernels themselves (67-171).
  *   strides are in elements; any stride works (non-unit K strides and
  *   unaligned rows take a slower element-wise path);
- *   block_n: weight rows per workgroup (4, 8, 16 or 32; 0 = automatic);
+ *   block_n: weight rows per workgroup (4, 8, 16 or 32; 0 = automatic;
+ *            above 8 tokens in bf16/fp16 also 24 -- two 16-row MFMA blocks,
+ *            the second half-filled -- and 64, 96 or 128, the shared-activation
+ *            tiles; 24 acts as 16 and 64-128 as 32 elsewhere);
  *   block_k: k elements of activations a wave holds at once in the M <= 8
  *            bf16/fp16 kernel (256 or 1024; 0 = 256; other kernels ignore it);
  *   split_k: workgroups along K (0 = automatic); with split_k > 1 fp32

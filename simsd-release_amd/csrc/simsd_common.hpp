@@ -362,11 +362,13 @@ SIMSD_DEV void accum_generic(const char* const (&arow)[RB], int64_t a_sk_bytes,
 // lane (g, r) reads 16 bytes at boff[cb] + k + 16 g of its row r (invalid rows
 // and bytes past Kb read zero).  U chunks are loaded per batch, all before the
 // first LDS write.  A wave's LDS accesses complete in order, so the reads see
-// the writes and the next chunk's writes follow the reads: no barrier.
+// the writes and the next chunk's writes follow the reads: no barrier.  Rows at
+// or past VR (a tile of fewer than 16 RB rows) are not loaded: their LDS rows
+// are written with zeros and their outputs are never stored.
 constexpr int kStep4Bytes = 256;            // bytes of one row per 4-row load step
 constexpr int kLdsRow = kStep4Bytes + 16;   // padded LDS row of a 256 B chunk
 
-template <int DT, int RB, int CB, int U>
+template <int DT, int RB, int CB, int U, int VR = 16 * RB>
 SIMSD_DEV void accum_lds(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
                          const uint32_t (&a_sn)[RB], rsrc_t rbx, const uint32_t (&boff)[CB],
                          const bool (&bok)[CB], int c0, int c1, uint32_t Kb, char* tile,
@@ -385,8 +387,11 @@ SIMSD_DEV void accum_lds(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t k = kc + lc * kLaneBytes;
-          W[u][rb][q] = buf_load16<kAuxStream>(
-              ra[rb], live && k < Kb ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob);
+          if (16 * rb + 4 * q < VR)
+            W[u][rb][q] = buf_load16<kAuxStream>(
+                ra[rb], live && k < Kb ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob);
+          else
+            W[u][rb][q] = zero4();
         }
 #pragma unroll
       for (int j = 0; j < 4; ++j)

@@ -477,8 +477,11 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(const char* __restr
 // 9..32 tokens: v_mfma_f32_16x16x32 fed from contiguous weight loads (4 rows x
 // 256 bytes per instruction, the GEMV's access pattern) through a per-wave LDS
 // tile (accum_lds).  Activations are the B operand as in thin_gemm_kernel.
+// OUTR > 0: tiles of OUTR < 16 RB weight rows (24 rows on two 16-row blocks,
+// the second half-filled), so that N = 6144 gives 256 workgroups instead of
+// 192 of 32 rows or 384 of 16.
 
-template <int DT, int RB, int CB, int KS, int U, bool PARTIAL, bool GLU>
+template <int DT, int RB, int CB, int KS, int U, bool PARTIAL, bool GLU, int OUTR = 0>
 __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __restrict__ w, const char* __restrict__ x,
                                                                 const char* __restrict__ w2, uint32_t Kb,
                                                                 uint32_t swn_b, uint32_t sxm_b, uint32_t sw2n_b, int N,
@@ -487,7 +490,9 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __re
   constexpr int NF = RB * CB;
   constexpr int ROWS = 16 * RB;
   static_assert(!GLU || RB == 2, "gated: block 0 = gate rows, block 1 = the same rows of up");
-  constexpr int OUT = GLU ? 16 : ROWS;   // output columns per workgroup
+  static_assert(OUTR == 0 || (!GLU && OUTR % 4 == 0 && OUTR > 16 * (RB - 1) && OUTR < ROWS),
+                "partial tiles: ungated, whole 4-row groups, the last block part-filled");
+  constexpr int OUT = GLU ? 16 : (OUTR > 0 ? OUTR : ROWS);   // output columns per workgroup
   // the waves' LDS tiles, reused for the cross-wave reduction once all waves
   // are past their main loop
   constexpr int kTileRows = ROWS + (SIMSD_LDS_X ? 16 * CB : 0);
@@ -541,7 +546,8 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __re
     accum_lds_ab<DT, RB, CB, U>(ra, a_row0, a_sn, rB, sxm_b, (int)cols_valid, w0, w1, Kb,
                                 smem + wk * kTileRows * kLdsRow, acc);
   else
-    accum_lds<DT, RB, CB, U>(ra, a_row0, a_sn, rB, boff, bok, w0, w1, Kb, smem + wk * kTileRows * kLdsRow, acc);
+    accum_lds<DT, RB, CB, U, GLU ? ROWS : OUT>(ra, a_row0, a_sn, rB, boff, bok, w0, w1, Kb,
+                                               smem + wk * kTileRows * kLdsRow, acc);
 
   __syncthreads();   // every wave done with its tile before the partials overwrite it
   reduce_waves<KS, NF>(reinterpret_cast<f32x4_t(&)[NF]>(acc), wk, lane, reinterpret_cast<float*>(smem));
@@ -556,7 +562,8 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __re
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int64_t n = nb + j;
-          if (n < N) put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
+          if (n < N && (OUTR == 0 || rb * 16 + 4 * g + j < OUT))
+            put_out<DT, PARTIAL, GLU>(a, split_id, m, n, acc[rb][cb][j], acc[RB - 1][cb][j]);
         }
       }
     }
@@ -884,15 +891,17 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
       if (cdiv(N, cand) * pl.tiles_m >= kMinWorkgroups) { rows = cand; break; }
     }
   }
-  if (rows != 4 && rows != 8 && rows != 16 && rows != 32 && rows != 64 && rows != 96 && rows != 128)
-    return set_error("thin_linear: block_n must be 4, 8, 16, 32, 64, 96 or 128 (got %d)", block_n);
+  if (rows != 4 && rows != 8 && rows != 16 && rows != 24 && rows != 32 && rows != 64 && rows != 96 &&
+      rows != 128)
+    return set_error("thin_linear: block_n must be 4, 8, 16, 24, 32, 64, 96 or 128 (got %d)", block_n);
   if (rows > 32 && kind != 2) rows = 32;   // 64, 96, 128: the 9..32-token kernel's shared-activation tiles
+  if (rows == 24 && (kind != 2 || glu)) rows = 16;   // 24: the ungated 9..32-token kernel only
   if (kind == 2 && rows < 16) rows = 16;   // whole 16-row MFMA blocks
   if (glu && kind == 1 && rows < 8) rows = 8;    // gated GEMV: a gate and an up row group
   if (glu && kind == 2 && rows < 64) rows = 32;  // gated LDS kernel: a gate and an up block
   pl.rows = rows;
   pl.rt = rows >= 16 ? 16 : rows;
-  pl.rb = rows >= 16 ? rows / 16 : 1;
+  pl.rb = rows >= 16 ? (rows + 15) / 16 : 1;
   if (kind == 2 && rows > 32) {
     // thin_gemm_xs_kernel: the waves split the rows, 16 or 32 each (gated: 32,
     // a gate and an up block); wave counts that do not divide the rows that
@@ -1059,19 +1068,19 @@ void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 #define SIMSD_LDS_U 4
 #endif
 
-template <int DT, int RB, int CB, int KS, bool GLU>
+template <int DT, int RB, int CB, int KS, bool GLU, int OUTR>
 void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = (RB * CB == 1) ? SIMSD_LDS_U : (SIMSD_LDS_U + 1) / 2;
-  if (pl.split > 1) launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
-  else launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
+  if (pl.split > 1) launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU, OUTR>, pl, args, stream);
+  else launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false, GLU, OUTR>, pl, args, stream);
 }
 
-template <int DT, int RB, int CB, bool GLU = false>
+template <int DT, int RB, int CB, bool GLU = false, int OUTR = 0>
 void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   switch (pl.ks) {
-    case 2: launch_lds<DT, RB, CB, 2, GLU>(pl, args, stream); break;
-    case 8: launch_lds<DT, RB, CB, 8, GLU>(pl, args, stream); break;
-    default: launch_lds<DT, RB, CB, 4, GLU>(pl, args, stream); break;
+    case 2: launch_lds<DT, RB, CB, 2, GLU, OUTR>(pl, args, stream); break;
+    case 8: launch_lds<DT, RB, CB, 8, GLU, OUTR>(pl, args, stream); break;
+    default: launch_lds<DT, RB, CB, 4, GLU, OUTR>(pl, args, stream); break;
   }
 }
 
@@ -1132,9 +1141,16 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
       if (pl.ms == 1) gemv4_rows<DT, 1, false>(pl, args, stream);
       else gemv4_rows<DT, 2, false>(pl, args, stream);
     } else if (pl.kind == 2) {
-      const bool two_rows = pl.rows == 32;   // 16-row blocks x 16-token blocks
-      if (pl.cb == 1) { if (two_rows) lds_ks<DT, 2, 1>(pl, args, stream); else lds_ks<DT, 1, 1>(pl, args, stream); }
-      else { if (two_rows) lds_ks<DT, 2, 2>(pl, args, stream); else lds_ks<DT, 1, 2>(pl, args, stream); }
+      // 16-row blocks x 16-token blocks; 24 rows: two blocks, the second half-filled
+      if (pl.cb == 1) {
+        if (pl.rows == 32) lds_ks<DT, 2, 1>(pl, args, stream);
+        else if (pl.rows == 24) lds_ks<DT, 2, 1, false, 24>(pl, args, stream);
+        else lds_ks<DT, 1, 1>(pl, args, stream);
+      } else {
+        if (pl.rows == 32) lds_ks<DT, 2, 2>(pl, args, stream);
+        else if (pl.rows == 24) lds_ks<DT, 2, 2, false, 24>(pl, args, stream);
+        else lds_ks<DT, 1, 2>(pl, args, stream);
+      }
     }
   }
   if (pl.kind == 0) {

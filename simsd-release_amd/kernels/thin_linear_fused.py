@@ -52,9 +52,10 @@ Config tuples keep the reference's shape ``(BLOCK_M, BLOCK_N, BLOCK_K,
 SPLIT_K[, num_warps, num_stages])`` and describe the MI355X kernels:
 BLOCK_M is the token envelope (``TUNED``: dispatch for M up to 16 or 32) or
 column-block width (heuristic: 4 or 8 for the GEMV, 16 or 32 otherwise),
-BLOCK_N the weight rows per workgroup (4, 8, 16, 32, 64, 96 or 128; other
+BLOCK_N the weight rows per workgroup (4, 8, 16, 24, 32, 64, 96 or 128; other
 values round down to one of these; at least 16 above 8 tokens; 64, 96 and 128
-apply above 8 tokens in bf16/fp16 and act as 32 elsewhere), BLOCK_K the K elements of
+apply above 8 tokens in bf16/fp16 and act as 32 elsewhere; 24 applies to the
+ungated projection above 8 tokens and acts as 16 elsewhere), BLOCK_K the K elements of
 activations a wave holds at once in the GEMV (256 or 1024),
 SPLIT_K the workgroups along K, num_warps the waves per workgroup (2, 4 or 8);
 num_stages is accepted and ignored.
@@ -75,7 +76,7 @@ from . import _native
 TARGET_CTAS = 256              # at least one workgroup on every CU
 MAX_SPLIT_K = 16
 MIN_K_PER_SPLIT = 512          # bf16 elements of every row per split (256 B per wave)
-_ROWS = (4, 8, 16, 32, 64, 96, 128)   # weight rows per workgroup the kernels are built for
+_ROWS = (4, 8, 16, 24, 32, 64, 96, 128)   # weight rows per workgroup the kernels are built for
 
 _DEFAULT_WAVES = 4
 
@@ -146,12 +147,17 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
 # Token ranges inside an entry's envelope where another geometry wins:
 # (K, N) -> (((M_lo, M_hi), 6-tuple), ...), first match taken.  Same sweep as
 # TUNED.  Above 8 tokens these are the shared-activation tiles (64 weight rows
-# per workgroup, waves splitting the rows); at 5-8 tokens the merged qkv with
+# per workgroup, waves splitting the rows) and, for the target's merged qkv,
+# 24-row tiles (256 workgroups for its 6144 rows, where 32-row tiles leave 64
+# CUs idle and 16-row tiles put two workgroups on half of them: 12.33 -> 12.06
+# us at M=16, 16.92 -> 16.33 us at M=32 with 8 waves); at 5-8 tokens the merged qkv with
 # its RMSNorm prologue, where 16 rows per workgroup halve the workgroups that
 # read both column sets' rows for the statistics (7.0-7.1 against 8.0-8.9 us
 # with 8 rows; the plain projection moves by at most 0.4 us either way).
 TUNED_RANGES: dict[tuple[int, int], tuple[tuple[tuple[int, int], tuple[int, int, int, int, int, int]], ...]] = {
     (2048, 4096): (((5, 8), (16, 16, 256, 1, 4, 2)),),      # merged qkv      7.1 us (M=8)
+    (4096, 6144): (((9, 16), (32, 24, 256, 1, 4, 2)),       # merged qkv     12.1 / 16.3 us (M=16 / 32)
+                   ((17, 32), (32, 24, 256, 1, 8, 2))),
     (12288, 4096): (((9, 32), (32, 64, 256, 4, 4, 2)),),    # down_proj   22.0 / 23.3 us (M=16 / 32)
     (4096, 151936): (((17, 32), (32, 64, 256, 1, 4, 2)),),  # lm_head      234 us (M=32)
 }

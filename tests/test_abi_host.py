@@ -121,6 +121,24 @@ def test_workspace_sizes():
     assert lib.simsd_block_attention_workspace_bytes(4, 12, 8, 100) == -1      # 12 q heads over 8 KV heads
 
 
+def test_partial_row_tile_plan():
+    """block_n = 24 keeps 24 rows per workgroup on the ungated 9..32-token
+    kernel (N = 6144: 256 workgroups) and acts as 16 elsewhere."""
+    from kernels import _native
+    from kernels.thin_linear_fused import _rows_for
+    lib = _native.lib()
+    out = (ctypes.c_int * 4)()
+    assert lib.simsd_thin_linear_plan(16, 6144, 4096, 0, 24, 1, 4, out) == 0
+    assert list(out) == [24, 16, 4, 1]
+    assert lib.simsd_thin_linear_plan(32, 6144, 4096, 1, 24, 2, 8, out) == 0   # fp16
+    assert list(out) == [24, 32, 8, 2]
+    assert lib.simsd_thin_linear_plan(4, 6144, 4096, 0, 24, 1, 4, out) == 0    # GEMV
+    assert out[0] == 16
+    assert lib.simsd_thin_linear_plan(16, 6144, 4096, 2, 24, 1, 4, out) == 0   # fp32
+    assert out[0] == 16
+    assert _rows_for(24) == 24 and _rows_for(31) == 24 and _rows_for(23) == 16
+
+
 def test_error_string_round_trip():
     from kernels import _native
     lib = _native.lib()
@@ -145,7 +163,8 @@ def test_tuned_table_envelope():
         assert (K, N) in TUNED
         for (lo, hi), cfg in ranges:
             assert 1 <= lo <= hi <= TUNED[(K, N)][0]
-            assert cfg[1] >= 64 if lo > 8 else hi <= 8     # wide tiles only above 8 tokens
+            # wide or 24-row tiles only above 8 tokens
+            assert cfg[1] in (24, 64, 96, 128) if lo > 8 else hi <= 8
             assert _tuned_for(lo, N, K) == cfg and _tuned_for(hi, N, K) == cfg
             assert _tuned_for(lo - 1, N, K) == TUNED[(K, N)] or any(
                 a <= lo - 1 <= b for (a, b), _ in ranges)

@@ -161,7 +161,7 @@ def test_every_launch_shape(M):
     x, w = rnd(M, 1000, seed=31 + M), rnd(531, 1000, scale=0.02, seed=32)
     with torch.inference_mode():
         ref = F.linear(x, w)
-        for rows in (4, 8, 16, 32, 64, 96, 128):
+        for rows in (4, 8, 16, 24, 32, 64, 96, 128):
             for waves in (2, 4, 8):
                 for split in (1, 3):
                     for block_k in (256, 1024):
@@ -386,6 +386,33 @@ def test_shared_activation_tiles_vs_oracle(M, dtype):
         got = got.float().cpu().numpy()
         assert float(np.abs(got - ref).max()) <= othin.tolerance(amax, dtype), (rows, waves)
         assert othin.max_abs_rel(got, ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M", [9, 16, 17, 32])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_partial_row_tiles_vs_oracle(M, dtype):
+    """24-row tiles (two 16-row MFMA blocks, the second half-filled) against
+    the oracle on the target's merged qkv shape and on dims that leave a
+    partial last tile (531 = 22 x 24 + 3 rows) and a partial last k chunk.
+    Waves split K the same way whatever the rows per workgroup, so every
+    output is the same sum in the same order as with 32-row tiles: bit-equal."""
+    from kernels.thin_linear_fused import thin_linear
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    for K, N in [(4096, 6144), (1000, 531)]:
+        x = rnd(M, K, dtype=tdt, seed=90 + M + K)
+        w = rnd(N, K, dtype=tdt, scale=0.02, seed=91 + N)
+        ref = othin.linear_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), dtype=dtype)
+        amax = float(np.abs(ref).max())
+        for waves in (2, 4, 8):
+            for split in (1, 2):
+                with torch.inference_mode():
+                    got_t = thin_linear(x, w, config=(32, 24, 256, split), num_warps=waves)
+                    full = thin_linear(x, w, config=(32, 32, 256, split), num_warps=waves)
+                assert torch.equal(got_t, full), (K, N, waves, split)
+                got = got_t.float().cpu().numpy()
+                err = float(np.abs(got - ref).max())
+                assert err <= othin.tolerance(amax, dtype), (K, N, waves, split, err)
+                assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
 @pytest.mark.parametrize("M", [3, 5, 13, 17, 31, 33, 64, 96])
