@@ -161,6 +161,8 @@ class SpecRunner:
         n = int(prompt_ids.numel())
         if n % self.bl:
             raise ValueError("prompt length must be a multiple of the block length")
+        if n > min(self.draft.cache.full_len, self.target.cache.full_len):
+            raise ValueError("prompt longer than the KV caches")
         ids = prompt_ids.to(self.dev, torch.int64)
         ar = torch.arange(n, device=self.dev)
         blk = ar // self.bl
@@ -294,6 +296,12 @@ class SpecRunner:
         """One iteration -> (generated tokens, accepted draft tokens).  With
         ``events`` (four torch.cuda.Event), their records bracket the draft,
         verify, acceptance and extend phases on the current stream."""
+        # the verify's scratch rows (and the optimistic drafts') reach
+        # ctx + 2 K bl slots; past the caches the step would write nowhere
+        cap = min(self.draft.cache.full_len, self.target.cache.full_len)
+        if self.ctx + 2 * self.K * self.bl > cap:
+            raise RuntimeError(f"speculative step: context {self.ctx} + {2 * self.K * self.bl} scratch rows "
+                               f"exceeds the KV caches' {cap} slots")
         main = torch.cuda.current_stream()
         if events:
             events[0].record()
