@@ -60,10 +60,12 @@ int simsd_abi_version(void);
 const char* simsd_last_error_string(void);
 
 /* ---- skinny linear ------------------------------------------------------
- * y[m, n] = sum_k x[m, k] * w[n, k]  (+ bias[n]), fp32 accumulation, y in the
- * input dtype.  Replaces the launch of _thin_gemv_kernel (+ _thin_gemv_reduce
- * when SPLIT_K > 1) in thin_linear, kernels/thin_linear_fused.py:321-344, and
- * the kernels themselves (67-171).
+ * y[m, n] = dtype(sum_k x[m, k] * w[n, k])  (+ bias[n] in the dtype), fp32
+ * accumulation, y in the input dtype: the bias goes onto the rounded product,
+ * as the reference's `y += bias` after its kernel (thin_linear_fused.py:343-344).
+ * Replaces the launch of _thin_gemv_kernel (+ _thin_gemv_reduce when
+ * SPLIT_K > 1) in thin_linear, kernels/thin_linear_fused.py:321-344, and the
+ * kernels themselves (67-171).
  *   strides are in elements; any stride works (non-unit K strides and
  *   unaligned rows take a slower element-wise path);
  *   block_n: weight rows per workgroup (4, 8, 16 or 32; 0 = automatic;

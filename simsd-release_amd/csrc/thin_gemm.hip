@@ -137,7 +137,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_kernel(ThinArgs a) {
             if (PARTIAL) {
               a.part[((int64_t)split_id * a.M + m) * a.N + n] = v;
             } else {
-              if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+              if (a.bias != nullptr) v = round_to<DT>(v) + load_elem<DT>(a.bias, n * a.sb);
               if (a.res != nullptr) v = round_to<DT>(v) + load_elem<DT>(a.res, m * a.srm + n * a.srn);
               store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
             }
@@ -178,7 +178,9 @@ SIMSD_DEV void put_out(const ThinArgs& a, int split_id, int64_t m, int64_t n, fl
   } else if (GLU) {
     store_elem<DT>(a.y, m * a.sym + n * a.syn, silu_mul<DT>(v, u));
   } else {
-    if (a.bias != nullptr) v += load_elem<DT>(a.bias, n * a.sb);
+    // bias: the product rounded to the dtype, then the dtype add -- the
+    // reference's y += bias on the kernel's output
+    if (a.bias != nullptr) v = round_to<DT>(v) + load_elem<DT>(a.bias, n * a.sb);
     // residual: the projection rounded to the dtype, then the dtype add
     if (a.res != nullptr) v = round_to<DT>(v) + load_elem<DT>(a.res, m * a.srm + n * a.srn);
     store_elem<DT>(a.y, m * a.sym + n * a.syn, v);
@@ -805,8 +807,8 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const char* __restrict
   }
 }
 
-// Sum the split partials in split order (fixed: bit-reproducible), add bias,
-// round to the output dtype.  One thread per output element.
+// Sum the split partials in split order (fixed: bit-reproducible), round to
+// the output dtype, add bias in the dtype.  One thread per output element.
 template <int DT>
 __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restrict__ part, int split,
                                                           int64_t M, int64_t N,
@@ -828,7 +830,7 @@ __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restric
   }
   float v = 0.f;
   for (int s = 0; s < split; ++s) v += part[(int64_t)s * M * N + e];
-  if (bias != nullptr) v += load_elem<DT>(bias, n * sb);
+  if (bias != nullptr) v = round_to<DT>(v) + load_elem<DT>(bias, n * sb);
   if (res != nullptr) v = round_to<DT>(v) + load_elem<DT>(res, m * srm + n * srn);
   store_elem<DT>(y, m * sym + n * syn, v);
 }

@@ -110,6 +110,47 @@ def test_leading_dims_preserved():
     assert float((got.float() - ref.float()).abs().max()) <= tol(ref)
 
 
+@pytest.mark.parametrize("M", [4, 7, 9, 16, 32])
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_bias_every_tile_kind(M, dtype):
+    """The bias epilogue of every kernel (the GEMV at M <= 8; the 16-, 24- and
+    32-row K-split tiles and the 64- to 128-row shared-activation tiles above),
+    alone and through the split reduce, on a partial last row tile and token
+    block.  The bias goes onto the rounded product, as the reference's
+    ``y += bias`` (kernels/thin_linear_fused.py:343-344): bit-exact against
+    the oracle on small-integer data, whose sums every order gets exactly,
+    with products past the dtype's integer range so that one rounding and two
+    differ; within the reference bound on random data."""
+    from kernels.thin_linear_fused import thin_linear
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    K, N = 1000, 531
+    g = torch.Generator().manual_seed(110 + M)
+    scale = 3.0 if dtype == "bf16" else 15.0            # integer sums past 256 (bf16) / 2048 (fp16)
+    xi = torch.randint(-3, 4, (M, K), generator=g).to(tdt)
+    wi = (torch.randint(-3, 4, (N, K), generator=g) * scale).to(tdt)
+    bi = (torch.randn(N, generator=g) * 3).to(tdt)
+    want = othin.linear_exact(xi.float().numpy(), wi.float().numpy(), bi.float().numpy(), dtype=dtype)
+    once = othin.linear_exact(xi.float().numpy(), wi.float().numpy(), dtype="fp32") + bi.float().numpy()
+    once = torch.from_numpy(once).to(tdt).float().numpy()
+    assert not np.array_equal(want, once)                # the case tells the two roundings apart
+    x = rnd(M, K, dtype=tdt, seed=110 + M)
+    w = rnd(N, K, dtype=tdt, scale=0.02, seed=111)
+    b = rnd(N, dtype=tdt, scale=0.5, seed=112)
+    ref = othin.linear_exact(x.float().cpu().numpy(), w.float().cpu().numpy(), b.float().cpu().numpy(), dtype=dtype)
+    amax = float(np.abs(ref).max())
+    for rows in (4, 8, 16, 24, 32, 64, 96, 128):
+        for split in (1, 3):
+            cfg = (32, rows, 256, split)
+            with torch.inference_mode():
+                got_i = thin_linear(xi.to(DEV), wi.to(DEV), bi.to(DEV), config=cfg).float().cpu().numpy()
+                got_t = thin_linear(x, w, b, config=cfg)
+                assert torch.equal(got_t, thin_linear(x, w, config=cfg) + b)   # the torch add, bit for bit
+                got = got_t.float().cpu().numpy()
+            assert np.array_equal(got_i, want), (rows, split)
+            err = float(np.abs(got - ref).max())
+            assert err <= othin.tolerance(amax, dtype), (rows, split, err)
+
+
 def test_bias_applied():
     from kernels.thin_linear_fused import thin_linear
     x, w = rnd(4, 512, seed=18), rnd(256, 512, scale=0.02, seed=19)
