@@ -61,7 +61,10 @@ def fill_cache(cache, layer, L, seed, dtype=torch.bfloat16):
                                                       (8, 32, 8, 2600, 2624), (5, 10, 5, 63, 96),
                                                       (16, 16, 8, 1024, 1056), (2, 16, 8, 513, 544),
                                                       (16, 16, 8, 1800, 1856), (4, 16, 8, 4500, 4512),
-                                                      (8, 32, 8, 4200, 4224)])
+                                                      (8, 32, 8, 4200, 4224), (9, 32, 8, 700, 736),
+                                                      (16, 32, 8, 1000, 1024), (24, 32, 8, 3000, 3040),
+                                                      (32, 32, 8, 64, 96), (32, 32, 8, 2000, 2048),
+                                                      (33, 32, 8, 900, 928)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_block_attention_vs_oracle(M, Hq, Hkv, L_valid, L_total, masked):
     from kernels.attention_fused import BlockKVCache, block_attention
