@@ -431,8 +431,9 @@ SIMSD_DEV void accum_lds(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
 // LDS rows 16 RB + 16 cb + ... of the wave's tile and read back in the B
 // layout.  Whole cache lines per load instead of 64 bytes of 16 rows, for
 // activations that every workgroup re-reads from L2.  The tile holds
-// 16 (RB + CB) rows.
-template <int DT, int RB, int CB, int U>
+// 16 (RB + CB) rows.  Weight rows at or past VR are not loaded, as in
+// accum_lds.
+template <int DT, int RB, int CB, int U, int VR = 16 * RB>
 SIMSD_DEV void accum_lds_ab(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],
                             const uint32_t (&a_sn)[RB], rsrc_t rbx, uint32_t b_sn, int b_rows, int c0,
                             int c1, uint32_t Kb, char* tile, f32x4_t (&acc)[RB][CB]) {
@@ -450,8 +451,10 @@ SIMSD_DEV void accum_lds_ab(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB]
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          W[u][rb][q] = buf_load16<kAuxStream>(
-              ra[rb], kok ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob);
+          W[u][rb][q] = 16 * rb + 4 * q < VR
+                            ? buf_load16<kAuxStream>(
+                                  ra[rb], kok ? a_row0[rb] + (uint32_t)(4 * q + lr) * a_sn[rb] + k : kOob)
+                            : zero4();
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb)
 #pragma unroll

@@ -545,8 +545,8 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __re
     bok[cb] = cb * 16 + r < cols_valid;
   }
   if (SIMSD_LDS_X)
-    accum_lds_ab<DT, RB, CB, U>(ra, a_row0, a_sn, rB, sxm_b, (int)cols_valid, w0, w1, Kb,
-                                smem + wk * kTileRows * kLdsRow, acc);
+    accum_lds_ab<DT, RB, CB, U, GLU ? ROWS : OUT>(ra, a_row0, a_sn, rB, sxm_b, (int)cols_valid, w0, w1, Kb,
+                                                  smem + wk * kTileRows * kLdsRow, acc);
   else
     accum_lds<DT, RB, CB, U, GLU ? ROWS : OUT>(ra, a_row0, a_sn, rB, boff, bok, w0, w1, Kb,
                                                smem + wk * kTileRows * kLdsRow, acc);

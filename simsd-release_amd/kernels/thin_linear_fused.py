@@ -149,15 +149,14 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
 # TUNED.  Above 8 tokens these are the shared-activation tiles (64 weight rows
 # per workgroup, waves splitting the rows) and, for the target's merged qkv,
 # 24-row tiles (256 workgroups for its 6144 rows, where 32-row tiles leave 64
-# CUs idle and 16-row tiles put two workgroups on half of them: 12.33 -> 12.06
-# us at M=16, 16.92 -> 16.33 us at M=32 with 8 waves); at 5-8 tokens the merged qkv with
+# CUs idle and 16-row tiles put two workgroups on half of them: 12.38 -> 11.62
+# us at M=16, 15.81 -> 15.30 us at M=32); at 5-8 tokens the merged qkv with
 # its RMSNorm prologue, where 16 rows per workgroup halve the workgroups that
 # read both column sets' rows for the statistics (7.0-7.1 against 8.0-8.9 us
 # with 8 rows; the plain projection moves by at most 0.4 us either way).
 TUNED_RANGES: dict[tuple[int, int], tuple[tuple[tuple[int, int], tuple[int, int, int, int, int, int]], ...]] = {
     (2048, 4096): (((5, 8), (16, 16, 256, 1, 4, 2)),),      # merged qkv      7.1 us (M=8)
-    (4096, 6144): (((9, 16), (32, 24, 256, 1, 4, 2)),       # merged qkv     12.1 / 16.3 us (M=16 / 32)
-                   ((17, 32), (32, 24, 256, 1, 8, 2))),
+    (4096, 6144): (((9, 32), (32, 24, 256, 1, 4, 2)),),     # merged qkv     11.6 / 15.3 us (M=16 / 32)
     (12288, 4096): (((9, 32), (32, 64, 256, 4, 4, 2)),),    # down_proj   22.0 / 23.3 us (M=16 / 32)
     (4096, 151936): (((17, 32), (32, 64, 256, 1, 4, 2)),),  # lm_head      234 us (M=32)
 }
