@@ -38,17 +38,6 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           denoise steps, 4 blocks verified per target forward, greedy
           acceptance; value in generated tokens / s.
   copy    a plain 1 GiB device copy: calibrates the PMC byte counters.
-  gemv_valu
-          the M=4 draft set in two designs: the 4x4x4-MFMA GEMV and the VALU
-          form first specified for it (probe), per op, best geometry each.
-  timeline
-          where an M=4 GEMV call's time goes (launch gap, ramp, first data,
-          stream, tail), per C2 op, from the timeline build of the library
-          (python simsd-release_amd/build_lib.py --timeline first).
-  floor   the floors of one launch: an empty kernel, and the fastest pure
-          read of C1's 48 MiB weight in the GEMV's access pattern over a sweep
-          of rows per workgroup x waves, beside the C1 GEMV on the same 24
-          weights.
   c4t4 / c4t16 / c4t64
           MoE step (route top-8 softmax over 256 experts -> align -> grouped
           gate_up + SiLU.mul -> down -> combine, + one shared expert),
@@ -919,218 +908,6 @@ def cpu_baseline_moe(torch, T):
                       f"({med * 1e3:.1f} ms); cpu={cpu_model()}"}
 
 
-def run_floor(args, torch, dev):
-    """The floors of a single launch, in HIP graphs: an empty kernel (what a
-    kernel boundary costs), and a pure read of C1's 48 MiB weight in the
-    GEMV's access pattern (4 rows x 256 B per load, non-temporal) at every
-    rows-per-workgroup x waves geometry, the fastest kept, over 24 distinct
-    weights so the MALL cannot serve repeats; beside it the C1 GEMV on the
-    same weights.  Then the same read on 8..256 workgroups of 512 KB each:
-    the rate one CU sustains."""
-    from kernels import _native
-    from kernels.thin_linear_fused import thin_linear
-
-    lib = _native.lib()
-    N, K, M, n_w = 12288, 2048, 4, 24
-    ws = [(torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_w)]
-    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
-    sink = torch.zeros(N // 4, dtype=torch.int32, device=dev)
-
-    def empty():
-        _native.check(lib.simsd_probe_empty(_native.stream_of(dev)), "probe_empty")
-
-    def reader(w, rows, waves):
-        return lambda: _native.check(lib.simsd_probe_read(w.data_ptr(), N, K * BF16, rows, waves, sink.data_ptr(),
-                                                          sink.numel(), _native.stream_of(dev)), "probe_read")
-
-    with torch.inference_mode():
-        reps = max(10, args.steps)
-        empty_us = graph_us_per_call(torch, [empty] * 112, reps=reps)
-        sweep = {}
-        for rows in (4, 8, 16):
-            for waves in (1, 2, 4, 8):
-                sweep[f"{rows}x{waves}"] = round(graph_us_per_call(
-                    torch, [reader(w, rows, waves) for w in ws], reps=reps), 3)
-        best = min(sweep, key=sweep.get)
-        read_us = sweep[best]
-        gemv_us = graph_us_per_call(torch, [lambda w=w: thin_linear(x, w) for w in ws], reps=reps)
-        # what one CU streams: the same read on a few workgroups (one per CU),
-        # 512 KB each (4 rows x 128 KB, 8 waves), over enough distinct
-        # buffers that the MALL cannot serve repeats
-        per_wg = {}
-        per_wg_bytes, rpw = 512 << 10, 4
-        for wgs in (8, 32, 128, 256):
-            rows = wgs * rpw
-            nb = rows * (per_wg_bytes // rpw)
-            bufs = [torch.empty(nb, dtype=torch.uint8, device=dev) for _ in range(max(2, min(24, (1 << 30) // nb)))]
-            sink_w = torch.zeros(rows, dtype=torch.int32, device=dev)
-
-            def rd(b, rows=rows, sink_w=sink_w):
-                return lambda: _native.check(lib.simsd_probe_read(b.data_ptr(), rows, per_wg_bytes // rpw, rpw, 8,
-                                                                  sink_w.data_ptr(), sink_w.numel(),
-                                                                  _native.stream_of(dev)), "probe_read")
-            us = graph_us_per_call(torch, [rd(b) for b in bufs], reps=reps)
-            per_wg[str(wgs)] = {"us": round(us, 3), "GBps_per_workgroup": round(per_wg_bytes / (us * 1e-6) / 1e9, 1),
-                                "GBps": round(nb / (us * 1e-6) / 1e9, 1)}
-            del bufs
-    wbytes = N * K * BF16
-    gemv_bytes = linear_bytes(M, K, N)
-    return {
-        "metric": "launch floors: empty-kernel us/launch and 48 MiB read GB/s in a HIP graph",
-        "value": round(wbytes / (read_us * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": reps, "warmup": 1, "ms_per_step": round(read_us * 1e-3, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "launch-floors-empty-and-read48MiB", "weights": n_w, "rows": N, "row_bytes": K * BF16,
-                   "best_read_rows_x_waves": best, "parallelism": "single-gpu"},
-        "empty_us_per_launch": round(empty_us, 3),
-        "read_us_per_48MiB": round(read_us, 3),
-        "read_us_by_rows_x_waves": sweep,
-        "read_frac_of_8TBps": round(wbytes / (read_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "c1_gemv_us": round(gemv_us, 3),
-        "c1_gemv_frac_of_8TBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-        "c1_gemv_over_read": round(gemv_us / read_us, 4),
-        "read_512KB_per_workgroup_by_workgroups": per_wg,
-    }, M
-
-
-def run_gemv_valu(args, torch, dev):
-    """The M=4 linear in two designs on the same shapes and weights, in HIP
-    graphs: the product's 4x4x4-MFMA GEMV (thin_linear, tuned configs) and
-    the VALU form the path was first specified with (simsd_probe_gemv_valu:
-    128-bit weight loads, activations staged in LDS, v_dot2_f32_bf16), the
-    latter at its best rows-per-workgroup x waves per op.  Each op: 28
-    distinct weights (the C2 layer count; 24 for the C1 gate_up), so the MALL
-    cannot serve repeats.  value = the VALU form's C2 step in GB/s."""
-    from kernels import _native
-    from kernels.thin_linear_fused import thin_linear
-
-    lib = _native.lib()
-    M = 4
-    ops = [("qkv", 2048, 4096, 28), ("o", 2048, 2048, 28), ("gate_up", 2048, 12288, 28), ("down", 6144, 2048, 28)]
-    per_op = {}
-    step_mfma = step_valu = 0.0
-    step_bytes = 0
-    with torch.inference_mode():
-        reps = max(10, args.steps)
-        for name, K, N, n_w in ops:
-            ws = [(torch.randn(N, K, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_w)]
-            x = torch.randn(M, K, device=dev).to(torch.bfloat16)
-            y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-
-            def valu(w, rows, waves):
-                return lambda: _native.check(lib.simsd_probe_gemv_valu(
-                    x.data_ptr(), K, w.data_ptr(), K, y.data_ptr(), N, M, N, K, rows, waves,
-                    _native.stream_of(dev)), "probe_gemv_valu")
-
-            mfma_us = graph_us_per_call(torch, [lambda w=w: thin_linear(x, w) for w in ws], reps=reps)
-            sweep = {f"{r}x{v}": round(graph_us_per_call(torch, [valu(w, r, v) for w in ws], reps=reps), 3)
-                     for r in (8, 16) for v in (2, 4, 8)}
-            best = min(sweep, key=sweep.get)
-            b = linear_bytes(M, K, N)
-            per_op[name] = {"K": K, "N": N, "mfma_us": round(mfma_us, 3), "valu_us": sweep[best],
-                            "valu_best_rows_x_waves": best, "valu_us_by_rows_x_waves": sweep,
-                            "mfma_frac": round(b / (mfma_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                            "valu_frac": round(b / (sweep[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-            step_mfma += 28 * mfma_us
-            step_valu += 28 * sweep[best]
-            step_bytes += 28 * b
-            del ws
-            torch.cuda.empty_cache()
-    return {
-        "metric": "M=4 linear, VALU vs 4x4x4-MFMA GEMV: C2-step GB/s of the VALU form",
-        "value": round(step_bytes / (step_valu * 1e-6) / 1e9, 2), "unit": "GB/s", "n_gpus": 1,
-        "steps": reps, "warmup": 1, "ms_per_step": round(step_valu * 1e-3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "gemv-valu-vs-mfma-M4-draft-set", "M": M, "parallelism": "single-gpu"},
-        "c2_step_ms_mfma": round(step_mfma * 1e-3, 4), "c2_step_ms_valu": round(step_valu * 1e-3, 4),
-        "per_op": per_op,
-    }, M
-
-
-def run_timeline(args, torch, dev):
-    """Where an M=4 GEMV call's time goes, from the timeline build of the
-    library (build_lib.py --timeline: every wave of thin_gemv4_kernel stamps
-    the 100 MHz clock at entry, after its first chunk, after its last chunk
-    and at its end).  Each C2 op's 28 distinct weights (24 for gate_up) run
-    in one graph, timed first without stamps, then replayed once with them.
-    Per call: the gap from the previous call's last wave end to this call's
-    first wave start, the dispatch ramp (waves' starts), the time to the
-    first chunk's data, the stream (first to last chunk), the tail (last wave
-    end past the median end); medians over the calls.  Writing the stamps
-    happens after the end stamp and lengthens the gap that follows by a
-    constant, which is subtracted (the stamped replay's time per call minus
-    the plain one's)."""
-    import ctypes
-
-    import numpy as np
-    from kernels import _native
-    from kernels.thin_linear_fused import thin_linear
-
-    path = os.path.join(REPO, "simsd-release_amd", "kernels", "libsimsd_timeline.so")
-    if not os.path.exists(path):
-        raise SystemExit("bench.py: the timeline workload needs simsd-release_amd/kernels/libsimsd_timeline.so "
-                         "(python simsd-release_amd/build_lib.py --timeline)")
-    _native.LIB_PATH = path
-    _native.lib()
-    tl = ctypes.CDLL(path)
-    tl.simsd_gemv_timeline_set.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
-    tl.simsd_gemv_timeline_bytes.restype = ctypes.c_int64
-    stamps = torch.zeros(tl.simsd_gemv_timeline_bytes() // 8, dtype=torch.int64, device=dev)
-    M = 4
-    ops = [("qkv", 2048, 4096, 28), ("o", 2048, 2048, 28), ("gate_up", 2048, 12288, 24), ("down", 6144, 2048, 28)]
-    per_op = {}
-    with torch.inference_mode():
-        for name, K, N, L in ops:
-            g = torch.Generator(device=dev).manual_seed(5)
-            ws = [(torch.randn(N, K, device=dev, generator=g) * 0.02).bfloat16() for _ in range(L)]
-            x = torch.randn(M, K, device=dev, generator=g).bfloat16()
-            fns = [lambda w=w: thin_linear(x, w) for w in ws]
-            plain_us = graph_us_per_call(torch, fns, reps=max(10, args.steps))
-            w_list = (ctypes.c_void_p * L)(*[w.data_ptr() for w in ws])
-            _native.check(tl.simsd_gemv_timeline_set(stamps.data_ptr(), w_list, L), "gemv_timeline")
-            stamped_us = graph_us_per_call(torch, fns, reps=1)
-            _native.check(tl.simsd_gemv_timeline_set(None, None, 0), "gemv_timeline")
-            torch.cuda.synchronize()
-            t = stamps.view(64, 1024, 8, 4)[:L].cpu().numpy().astype(np.int64)
-            stamps.zero_()
-            rows = {k: [] for k in ("gap", "ramp_p50", "ramp_max", "first_data", "stream", "tail", "span")}
-            prev_end = None
-            for c in t:
-                used = c[:, :, 0] > 0
-                starts, ends = c[:, :, 0][used], c[:, :, 3][used]
-                t0 = starts.min()
-                ok = used & (c[:, :, 1] > 0)
-                if prev_end is not None:
-                    rows["gap"].append(t0 - prev_end)
-                rows["ramp_p50"].append(np.median(starts) - t0)
-                rows["ramp_max"].append(starts.max() - t0)
-                rows["first_data"].append(np.median((c[:, :, 1] - c[:, :, 0])[ok]))
-                rows["stream"].append(np.median((c[:, :, 2] - c[:, :, 1])[ok]))
-                rows["tail"].append(ends.max() - np.median(ends))
-                rows["span"].append(ends.max() - t0)
-                prev_end = ends.max()
-            med = {k: round(float(np.median(v)) / 100.0, 3) for k, v in rows.items()}   # 100 MHz ticks -> us
-            med["gap"] = round(med["gap"] - (stamped_us - plain_us), 3)
-            per_op[name] = {"K": K, "N": N, "us_per_call": round(plain_us, 3),
-                            "us_per_call_stamped": round(stamped_us, 3),
-                            "workgroups": int(used.any(1).sum()), "waves_per_workgroup": int(used.any(0).sum()),
-                            "gap_us": med["gap"], "dispatch_ramp_p50_us": med["ramp_p50"],
-                            "dispatch_ramp_max_us": med["ramp_max"], "first_data_us": med["first_data"],
-                            "stream_us": med["stream"], "tail_us": med["tail"], "kernel_span_us": med["span"],
-                            "ideal_us_at_8TBps": round(linear_bytes(M, K, N) / 8e6, 3)}
-            del ws
-            torch.cuda.empty_cache()
-    o = per_op["o"]
-    return {
-        "metric": "M=4 GEMV call timeline: launch gap, ramp, first data, stream, tail (us)",
-        "value": o["us_per_call"], "unit": "us per o_proj call", "n_gpus": 1, "steps": max(10, args.steps),
-        "warmup": 1, "ms_per_step": round(o["us_per_call"] * 1e-3, 5), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "gemv-timeline-M4-draft-set", "M": M, "parallelism": "single-gpu"},
-        "per_op": per_op,
-    }, M
-
-
 def run_copy(args, torch, dev):
     """A plain 1 GiB device copy (torch's elementwise copy kernel): the known
     byte count that calibrates the FETCH_SIZE / WRITE_SIZE counters."""
@@ -1163,8 +940,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy",
-                             "floor", "gemv_valu", "timeline"])
+                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
@@ -1183,12 +959,6 @@ def main():
     torch.cuda.set_device(dev)
     if args.workload == "copy":
         print(json.dumps(run_copy(args, torch, dev)), flush=True)
-        return
-    if args.workload in ("floor", "gemv_valu", "timeline"):
-        result, _ = {"floor": run_floor, "gemv_valu": run_gemv_valu, "timeline": run_timeline}[args.workload](
-            args, torch, dev)
-        result["device"] = torch.cuda.get_device_name(dev)
-        print(json.dumps(result), flush=True)
         return
     if args.workload == "c5":
         result, _ = run_c5(args, torch, dev)

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 15
+#define SIMSD_ABI_VERSION 16
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -35,25 +35,6 @@ extern "C" {
 
 #define SIMSD_MOE_MAX_EXPERTS 1024
 #define SIMSD_MOE_MAX_SLOTS 8192
-
-/* ---- measurement probes (no reference counterpart) ----------------------
- * The floors the skinny linear is measured against: an empty launch, and a
- * pure read of a [rows, row_bytes] matrix in thin_gemv4_kernel's access
- * pattern (rows_per_wg 4/8/16 rows per workgroup, waves 1/2/4/8 splitting
- * each row, 4 rows x 256 contiguous bytes per load instruction,
- * non-temporal), folding what it reads into one 4-byte word per workgroup
- * (sink: ceil(rows / rows_per_wg) words). */
-int simsd_probe_empty(void* stream);
-int simsd_probe_read(const void* w, int64_t rows, int64_t row_bytes, int rows_per_wg, int waves,
-                     void* sink, int64_t sink_words, void* stream);
-/* The M <= 4 bf16 linear y[M, N] = x[M, K] . w[N, K]^T in the VALU form the
- * hot path was first specified with (128-bit weight loads of one row x 1 KB,
- * the tokens' rows staged in LDS, v_dot2_f32_bf16, lanes and waves reduced
- * in fixed order), beside simsd_thin_linear's 4x4x4-MFMA GEMV for A/B runs.
- * 1 <= M <= 4, K a multiple of 8 up to 6144, 16-byte aligned rows (strides in
- * elements), rows_per_wg 8 or 16, waves 2, 4 or 8. */
-int simsd_probe_gemv_valu(const void* x, int64_t sxm, const void* w, int64_t swn, void* y, int64_t sym,
-                          int64_t M, int64_t N, int64_t K, int rows_per_wg, int waves, void* stream);
 
 /* ---- housekeeping ---------------------------------------------------- */
 int simsd_abi_version(void);

@@ -153,13 +153,15 @@ def greedy_match_verify(draft_ids, target_argmax):
     return list(draft_ids), len(draft_ids), None
 
 
-def accept_blocks(draft_blocks, target_argmax, block_length):
+def accept_blocks(draft_blocks, target_argmax, block_length, eos_ids=None):
     """K-block greedy acceptance with first-reject truncation,
     speculative_decoding/speculative_decode.py:895-953 (greedy verify,
     partial_block_fill = "draft_argmax"): -> (committed blocks, generated
     tokens, accepted count).  Block k's final ids come from
     greedy_match_verify; a short block is padded with the draft's own tokens
-    from len(final) on; the loop stops after the first rejected block."""
+    from len(final) on; the loop stops after the first rejected block, or
+    after a block whose final ids hold an id of ``eos_ids`` (:944-950)."""
+    eos = set(eos_ids or ())
     committed, generated, n_acc = [], [], 0
     for k in range(len(draft_blocks)):
         final, n, _bonus = greedy_match_verify(draft_blocks[k], target_argmax[k])
@@ -169,6 +171,6 @@ def accept_blocks(draft_blocks, target_argmax, block_length):
             block += list(draft_blocks[k][len(block):block_length])
         committed.append(block)
         generated.extend(final)
-        if n < block_length:
+        if n < block_length or any(t in eos for t in final):
             break
     return committed, generated, n_acc

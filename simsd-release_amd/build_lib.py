@@ -2,9 +2,6 @@
 
     python simsd-release_amd/build_lib.py            # build
     python simsd-release_amd/build_lib.py --verbose  # echo the hipcc line
-    python simsd-release_amd/build_lib.py --timeline # the GEMV timeline build
-                                                     # (kernels/libsimsd_timeline.so,
-                                                     # bench.py --workload timeline)
 
 The library is compiled ahead of time, so nothing JIT-compiles at import or
 inside a captured graph.  All device code is built with packed-fp32 ops
@@ -25,10 +22,11 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(REPO, "include")
 OUT = os.path.join(HERE, "kernels", "libsimsd_kernels.so")
-TIMELINE_OUT = os.path.join(HERE, "kernels", "libsimsd_timeline.so")
 
-SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip", "logits.hip", "attention.hip", "probe.hip"]
-ARCH = os.environ.get("SIMSD_OFFLOAD_ARCH", "gfx950")
+SOURCES = ["capi.cpp", "thin_gemm.hip", "moe.hip", "logits.hip", "attention.hip"]
+# gfx950 only: tiles rely on its 160 KiB of LDS per workgroup and on its
+# instructions (v_permlane32_swap, the 16x16x32 bf16 MFMA)
+ARCH = "gfx950"
 
 
 def hipcc() -> str:
@@ -91,10 +89,5 @@ def build(verbose: bool = False, out: str = OUT, extra=()) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--verbose", action="store_true")
-    ap.add_argument("--timeline", action="store_true",
-                    help="build the GEMV timeline library (stamps in thin_gemv4_kernel) instead")
     args = ap.parse_args()
-    if args.timeline:
-        print(build(verbose=args.verbose, out=TIMELINE_OUT, extra=["-DSIMSD_GEMV_TIMELINE=1"]))
-    else:
-        print(build(verbose=args.verbose))
+    print(build(verbose=args.verbose))

@@ -367,6 +367,9 @@ SIMSD_DEV void accum_generic(const char* const (&arow)[RB], int64_t a_sk_bytes,
 // are written with zeros and their outputs are never stored.
 constexpr int kStep4Bytes = 256;            // bytes of one row per 4-row load step
 constexpr int kLdsRow = kStep4Bytes + 16;   // padded LDS row of a 256 B chunk
+// LDS per workgroup on gfx950 (CDNA4); the library is built for gfx950 only,
+// and some tiles use more than the 64 KiB of earlier CDNA parts.
+constexpr int kLdsBytesGfx950 = 160 * 1024;
 
 template <int DT, int RB, int CB, int U, int VR = 16 * RB>
 SIMSD_DEV void accum_lds(const rsrc_t (&ra)[RB], const uint32_t (&a_row0)[RB],

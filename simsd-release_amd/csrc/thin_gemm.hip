@@ -206,25 +206,6 @@ constexpr int kNormMaxMs = SIMSD_NORM_MAX_MS;
 #define SIMSD_NORM_EARLY 2
 #endif
 
-// Timeline build (SIMSD_GEMV_TIMELINE=1, a separate library: build_lib.py
-// --timeline): every wave of thin_gemv4_kernel takes the 100 MHz clock at
-// entry, after its first chunk's arithmetic, after its last and at its end,
-// and stores the four stamps for calls whose weight pointer is registered
-// (simsd_gemv_timeline_set).  What it measures: the gap between launches, the
-// dispatch ramp, the time to the first data, the stream and the tail.  The
-// product library is built without it.
-#ifndef SIMSD_GEMV_TIMELINE
-#define SIMSD_GEMV_TIMELINE 0
-#endif
-#if SIMSD_GEMV_TIMELINE
-constexpr int kTimelineCalls = 64;
-constexpr int kTimelineWgs = 1024;
-constexpr int kTimelineWaves = 8;
-__device__ unsigned long long* g_timeline;
-__device__ const void* g_timeline_w[kTimelineCalls];
-__device__ int g_timeline_n;
-#endif
-
 // The fields the first loads depend on come as separate scalar arguments
 // ahead of ThinArgs: the build preloads leading scalar kernel arguments into
 // SGPRs (-amdgpu-kernarg-preload-count), so the first weight and activation
@@ -235,10 +216,6 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(const char* __restr
                                                              const char* __restrict__ w2, uint32_t Kb, uint32_t swn_b,
                                                              uint32_t sxm_b, uint32_t sw2n_b, int N, int M, int steps,
                                                              int steps_per_split, ThinArgs a) {
-#if SIMSD_GEMV_TIMELINE
-  const unsigned long long tl0 = __builtin_amdgcn_s_memrealtime();
-  unsigned long long tl1 = 0;
-#endif
   constexpr int ES = DTypeInfo<DT>::kSize;
   constexpr int G = RW / 4;
   static_assert(RW % 4 == 0 && G % GB == 0, "row groups");
@@ -418,17 +395,7 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(const char* __restr
       c0 += CH;
     }
   }
-#if SIMSD_GEMV_TIMELINE
-  if (c0 < w1) {
-    run_chunk(c0, load_b, load_g, load_a);
-    c0 += CH;
-    tl1 = __builtin_amdgcn_s_memrealtime();
-  }
-#endif
   for (; c0 < w1; c0 += CH) run_chunk(c0, load_b, load_g, load_a);
-#if SIMSD_GEMV_TIMELINE
-  const unsigned long long tl2 = __builtin_amdgcn_s_memrealtime();
-#endif
 
   // sum the 16 k-chunk blocks (lane bits 2..5), then the KS waves in wave
   // order through LDS: red[wave][value][col j]
@@ -460,19 +427,6 @@ __global__ __launch_bounds__(64 * KS) void thin_gemv4_kernel(const char* __restr
       put_out<DT, PARTIAL, GLU>(a, split_id, m, n, t, u);
     }
   }
-#if SIMSD_GEMV_TIMELINE
-  const unsigned long long tl3 = __builtin_amdgcn_s_memrealtime();
-  if (g_timeline != nullptr && lane == 0 && blockIdx.x < kTimelineWgs && wk < kTimelineWaves) {
-    int call = -1;
-    for (int q = 0; q < g_timeline_n; ++q)
-      if (g_timeline_w[q] == a.w) call = q;
-    if (call >= 0) {
-      unsigned long long* t =
-          g_timeline + (((int64_t)call * kTimelineWgs + blockIdx.x) * kTimelineWaves + wk) * 4;
-      t[0] = tl0; t[1] = tl1; t[2] = tl2; t[3] = tl3;
-    }
-  }
-#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -596,6 +550,9 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_xs_kernel(const char* __res
   constexpr int kXLoads = U * CB * 4;             // 4-row load instructions per activation batch
   constexpr int kXPer = (kXLoads + KS - 1) / KS;  // ... per wave
   constexpr int kSlot = U * XROWS * kLdsRow;
+  static_assert(2 * kSlot + KS * WROWS * kLdsRow <= kLdsBytesGfx950,
+                "shared-activation tile: LDS beyond gfx950's 160 KiB per workgroup (RB=2, CB=2, KS=4 "
+                "takes 68 KiB, so these tiles need gfx950)");
   __shared__ __attribute__((aligned(16))) char xs[2 * kSlot];
   __shared__ __attribute__((aligned(16))) char wt[KS * WROWS * kLdsRow];
   const int lane = threadIdx.x & 63;
@@ -921,7 +878,7 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
   if (split <= 0) {
     const int64_t wgs = pl.tiles_n * pl.tiles_m;
     split = 1;
-    if (wgs < kMinWorkgroups / 2) {
+    if (wgs > 0 && wgs < kMinWorkgroups / 2) {   // wgs == 0: an empty M or N, nothing to split
       split = (int)cdiv(kMinWorkgroups, wgs);
       const int64_t max_by_k = (K * es) / (kStep4Bytes * (int64_t)pl.ks);
       split = (int)max((int64_t)1, min((int64_t)min(split, kMaxSplit), max_by_k));
@@ -1274,7 +1231,10 @@ extern "C" int simsd_thin_linear_noalloc(const void* x, int64_t sxm, int64_t sxk
                                          int64_t sym, int64_t syn, int64_t M, int64_t N, int64_t K,
                                          int dtype, int block_n, int block_k, int split_k, int num_waves,
                                          void* stream) {
+  if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
+    return set_error("thin_linear_noalloc: unsupported dtype code %d", dtype);
   if (M < 0 || N < 0 || K < 0) return set_error("thin_linear_noalloc: negative size");
+  if (M == 0 || N == 0) return 0;   // as simsd_thin_linear: nothing to compute
   const int64_t need = simsd_thin_linear_workspace_bytes(M, N, K, dtype, block_n, split_k, num_waves);
   if (need < 0) return -1;
   if (need > kNoAllocScratchBytes)
@@ -1421,6 +1381,7 @@ extern "C" int64_t simsd_rmsnorm_linear_workspace_bytes(int64_t M, int64_t N_row
                                                         int block_n, int split_k, int num_waves) {
   const int64_t part = simsd_thin_linear_workspace_bytes(M, N_rows, K, dtype, block_n, split_k, num_waves);
   if (part < 0) return -1;
+  if (M == 0 || N_rows == 0) return 0;   // the entry points return before using a workspace
   return align256(M * K * esize_of(dtype)) + part;
 }
 
@@ -1553,18 +1514,3 @@ extern "C" int simsd_thin_linear_residual(const void* x, int64_t sxm, int64_t sx
   return run_planned(pl, args, dtype, workspace, workspace_bytes, stream, "thin_linear_residual");
 }
 
-#if SIMSD_GEMV_TIMELINE
-// stamps: [call][workgroup][wave][4] u64 (kTimelineCalls x 1024 x 8 x 4), the
-// calls matched by weight pointer against w_list[0..n); p = nullptr stops.
-extern "C" int simsd_gemv_timeline_set(void* stamps, const void* const* w_list, int n) {
-  if (n < 0 || n > kTimelineCalls) return set_error("gemv_timeline: at most %d calls", kTimelineCalls);
-  if (hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), &stamps, sizeof(stamps)) != hipSuccess ||
-      (n > 0 && hipMemcpyToSymbol(HIP_SYMBOL(g_timeline_w), w_list, sizeof(void*) * n) != hipSuccess) ||
-      hipMemcpyToSymbol(HIP_SYMBOL(g_timeline_n), &n, sizeof(n)) != hipSuccess)
-    return set_error("gemv_timeline: setting the stamp buffer failed");
-  return 0;
-}
-extern "C" int64_t simsd_gemv_timeline_bytes(void) {
-  return (int64_t)kTimelineCalls * kTimelineWgs * kTimelineWaves * 4 * 8;
-}
-#endif

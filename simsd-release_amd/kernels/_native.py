@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -36,9 +36,6 @@ SIGNATURES = {
     "simsd_thin_linear_noalloc": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64,
                                          _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
     "simsd_thin_linear_noalloc_max_scratch_bytes": (_i64, []),
-    "simsd_probe_empty": (_i32, [_vp]),
-    "simsd_probe_read": (_i32, [_vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]),
-    "simsd_probe_gemv_valu": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     "simsd_thin_linear_silu_mul": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                           _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                                           _i32, _i32, _i32, _i32, _vp, _i64, _vp]),

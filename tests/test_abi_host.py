@@ -433,5 +433,68 @@ def test_accept_blocks_matches_oracle_host():
         cases.append((d, t))
     for d, t in cases:
         assert accept_blocks(d, t, 4) == over.accept_blocks(d, t, 4)
+        eos = [rng.randint(0, 3)]
+        assert accept_blocks(d, t, 4, eos) == over.accept_blocks(d, t, 4, eos)
     assert accept_blocks([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 2, 9, 4], [5, 6, 7, 8]], 4) == \
         ([[1, 2, 9, 4]], [1, 2, 9], 2)
+
+
+# Hand-worked acceptance (speculative_decode.py:895-953 with mrs.py:111-146
+# greedy_match_verify, partial_block_fill = "draft_argmax"), each worked out
+# by reading the reference loop, not by running either restatement:
+#   (drafts, target argmax, eos ids) -> (committed, generated, accepted)
+ACCEPT_HAND_CASES = [
+    # rejection at position 1 with a tail that differs between draft and
+    # target: the bonus is the target's 9, the block is filled from the
+    # draft's own tail (3, 4), not the target's (8, 7)
+    ([[1, 2, 3, 4]], [[1, 9, 8, 7]], None, ([[1, 9, 3, 4]], [1, 9], 1)),
+    # K = 4, every block accepted: four whole blocks, no bonus token
+    ([[1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12], [13, 14, 15, 16]],
+     [[1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12], [13, 14, 15, 16]], None,
+     ([[1, 2, 3, 4], [5, 6, 7, 8], [9, 10, 11, 12], [13, 14, 15, 16]],
+      [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16], 16)),
+    # rejection at the first position of the first block: one committed
+    # block (the bonus then the draft's tail), later blocks never looked at
+    ([[1, 2, 3, 4], [5, 6, 7, 8]], [[7, 6, 5, 4], [5, 6, 7, 8]], None, ([[7, 2, 3, 4]], [7], 0)),
+    # block 0 accepted, block 1 rejected at its last position, block 2 dropped
+    ([[1, 2, 3, 4], [5, 6, 7, 8], [9, 9, 9, 9]], [[1, 2, 3, 4], [5, 6, 7, 0], [9, 9, 9, 9]], None,
+     ([[1, 2, 3, 4], [5, 6, 7, 0]], [1, 2, 3, 4, 5, 6, 7, 0], 7)),
+    # an accepted block holding an EOS id ends the loop although block 1
+    # would also be accepted
+    ([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 2, 3, 4], [5, 6, 7, 8]], [3], ([[1, 2, 3, 4]], [1, 2, 3, 4], 4)),
+    # the bonus itself is the EOS id: same block count as a plain rejection
+    ([[1, 2, 3, 4], [5, 6, 7, 8]], [[1, 0, 3, 4], [5, 6, 7, 8]], [0], ([[1, 0, 3, 4]], [1, 0], 1)),
+    # EOS ids that no generated token equals change nothing
+    ([[1, 2, 0, 4], [5, 6, 7, 8]], [[1, 2, 0, 4], [5, 6, 7, 8]], [9],
+     ([[1, 2, 0, 4], [5, 6, 7, 8]], [1, 2, 0, 4, 5, 6, 7, 8], 8)),
+    # an EOS id in the draft's fill tail is committed but not generated
+    ([[1, 2, 3, 0], [5, 6, 7, 8]], [[1, 9, 3, 0], [5, 6, 7, 8]], [0], ([[1, 9, 3, 0]], [1, 9], 1)),
+]
+
+
+@pytest.mark.parametrize("drafts,targets,eos,expect", ACCEPT_HAND_CASES)
+def test_accept_blocks_hand_worked(drafts, targets, eos, expect):
+    """Both the runner's acceptance and the oracle's restatement give the
+    hand-worked result."""
+    from oracle import verify as over
+    from speculative.verify import accept_blocks
+    assert accept_blocks(drafts, targets, 4, eos) == expect
+    assert over.accept_blocks(drafts, targets, 4, eos) == expect
+
+
+def test_empty_shapes_return_without_work():
+    """M = 0 or N = 0: the workspace query says 0 bytes and the entry points
+    return 0 before any launch (no device pointer is touched, so null
+    pointers and a null stream are fine here)."""
+    from kernels import _native
+    lib = _native.lib()
+    for M, N in ((0, 4096), (4, 0), (0, 0)):
+        assert lib.simsd_thin_linear_workspace_bytes(M, N, 4096, 0, 0, 0, 0) == 0
+        assert lib.simsd_rmsnorm_linear_workspace_bytes(M, N, 4096, 0, 0, 0, 0) == 0
+        assert lib.simsd_thin_linear(None, 0, 0, None, 0, 0, None, 0, None, 0, 0, M, N, 4096, 0,
+                                     0, 0, 0, 0, None, 0, None) == 0
+        assert lib.simsd_thin_linear_noalloc(None, 0, 0, None, 0, 0, None, 0, None, 0, 0, M, N, 4096, 0,
+                                             0, 0, 0, 0, None) == 0
+    assert lib.simsd_thin_linear_noalloc(None, 0, 0, None, 0, 0, None, 0, None, 0, 0, 0, 4, 4, 7,
+                                         0, 0, 0, 0, None) == -1       # bad dtype code
+    assert b"dtype" in lib.simsd_last_error_string()
