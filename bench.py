@@ -57,7 +57,7 @@ profiles/ for the workload (null if none).  "breakdown" times each op's
 calls alone in a graph of their own.  The CPU baseline is the reference's CPU path -- torch
 F.linear in bf16 (its oracle ref_thin_linear), the stock MoE loop, or (c5)
 the reference's decoder layer forward -- timed on a bounded sample of the
-same workload; in the default run's extras only c5 carries one.
+same workload; every extra of the default run carries its own.
 """
 from __future__ import annotations
 
@@ -180,18 +180,25 @@ def cpu_baseline_linear(torch, workload, M):
         shapes = [("gate_up", 2048, 12288)]
     g = torch.Generator().manual_seed(0)
     sample_layers = 4 if workload != "c1" else 8
-    layers = []
-    for _ in range(sample_layers):
-        layers.append([(torch.randn(M, K, generator=g).to(torch.bfloat16),
-                        (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16))
-                       for _, K, N in shapes])
+
+    def pair(K, N):
+        # uniform weights of the same spread as N(0, 0.02): a CPU GEMM's time
+        # does not depend on the values, and filling gigabytes is faster
+        return (torch.randn(M, K, generator=g).to(torch.bfloat16),
+                torch.empty(N, K, dtype=torch.bfloat16).uniform_(-0.0346, 0.0346, generator=g))
+
+    layers = [[pair(K, N) for _, K, N in shapes] for _ in range(sample_layers)]
     per_layer_bytes = sum(linear_bytes(M, K, N) for _, K, N in shapes)
     step_layers = n_layers if n_layers else 24
+    # the target verify set ends with its lm_head, once per step
+    head = pair(*LM_HEAD_TARGET[1:]) if workload in ("c3m16", "c3m32") else None
 
     def step():
         for i in range(step_layers):
             for x, w in layers[i % sample_layers]:
                 linear_cpu_torch(x, w)
+        if head is not None:
+            linear_cpu_torch(*head)
 
     step()                                  # warmup
     times = []
@@ -201,7 +208,7 @@ def cpu_baseline_linear(torch, workload, M):
         step()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    byts = per_layer_bytes * step_layers
+    byts = per_layer_bytes * step_layers + (linear_bytes(M, *LM_HEAD_TARGET[1:]) if head is not None else 0)
     return {
         "value": round(byts / med / 1e9, 3),
         "unit": "GB/s",
@@ -210,8 +217,9 @@ def cpu_baseline_linear(torch, workload, M):
         "sample": (f"torch CPU F.linear bf16 (the reference oracle ref_thin_linear), M={M}, "
                    f"{sample_layers} distinct layers of {[s[0] for s in shapes]} "
                    f"({sample_layers * per_layer_bytes / 1e6:.0f} MB of weights) cycled to one "
-                   f"{step_layers}-layer step; median of {len(times)} steps "
-                   f"({med * 1e3:.1f} ms/step); cpu={cpu_model()}; os.cpu_count={os.cpu_count()}"),
+                   f"{step_layers}-layer step{' + the lm_head' if head is not None else ''}; median of "
+                   f"{len(times)} steps ({med * 1e3:.1f} ms/step); cpu={cpu_model()}; "
+                   f"os.cpu_count={os.cpu_count()}"),
     }
 
 
@@ -869,43 +877,75 @@ def run_moe(args, torch, dev):
 
 
 def cpu_baseline_moe(torch, T):
-    """The stock per-expert loop (oracle restatement, numpy) on one layer of
-    the workload: only the experts the routing picks are materialised."""
-    import numpy as np
-    from oracle import moe as omoe
+    """The reference's CPU path for one MoE layer, in torch on the host cores
+    in bf16: softmax top-8 routing, then the stock per-expert loop
+    (kernels/workspace/moe_dispatch/build_oracle.py:34-67, the transcription
+    of LLaDA2MoeSparseMoeBlock.moe_infer: histogram, argsort, one F.linear
+    gate / up / SiLU.mul / down per active expert, scatter back, fp32
+    weighting, sum) plus the shared expert.  Bounded sample: one stacked layer
+    of all 256 experts (1.6 GB of bf16 weights, past any host cache) under 8
+    distinct routings and inputs, cycled; GB/s over the same algorithmic
+    bytes as the GPU step ((active experts + 1) x 6 MiB + activations)."""
+    F = torch.nn.functional
+    E, k, H, I, L = 256, 8, 2048, 512, 8
+    g = torch.Generator().manual_seed(0)
+    wg = torch.empty(E, I, H, dtype=torch.bfloat16)
+    wu = torch.empty(E, I, H, dtype=torch.bfloat16)
+    wd = torch.empty(E, H, I, dtype=torch.bfloat16)
+    for t in (wg, wu, wd):                   # uniform, the spread of N(0, 0.02)
+        t.uniform_(-0.0346, 0.0346, generator=g)
+    shared = tuple((torch.randn(*s, generator=g) * 0.02).to(torch.bfloat16) for s in ((I, H), (I, H), (H, I)))
+    layers = []
+    per_expert = (2 * I * H + H * I) * BF16
+    total_bytes = 0
+    for _ in range(L):
+        x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+        logits = torch.randn(T, E, generator=g)
+        layers.append((x, logits))
+        ids = torch.softmax(logits, dim=-1).topk(k, dim=-1).indices
+        total_bytes += (int(torch.unique(ids).numel()) + 1) * per_expert + T * H * BF16 * 2 + T * E * 4 + T * k * 12
 
-    E, k, H, I = 256, 8, 2048, 512
-    rng = np.random.default_rng(0)
-    x = rng.standard_normal((T, H))
-    logits = rng.standard_normal((T, E))
-    ids, w = omoe.route_topk(logits, k, scoring="softmax", renorm=False)
-    act, local = np.unique(ids, return_inverse=True)
-    local = local.reshape(ids.shape)
-    n = act.size
-    wg = rng.standard_normal((n, I, H)) * 0.02
-    wu = rng.standard_normal((n, I, H)) * 0.02
-    wd = rng.standard_normal((n, H, I)) * 0.02
-    times = []
-    t_end = time.perf_counter() + 20.0
-    while len(times) < 3 or (len(times) < 10 and time.perf_counter() < t_end):
-        t0 = time.perf_counter()
-        omoe.dispatch_grouped(x, local, w, wg, wu, wd, dtype="bf16")
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end:
-            break
+    def moe_layer(x, logits):
+        w, ids = torch.softmax(logits, dim=-1).topk(k, dim=-1)
+        cnts = ids.new_zeros((T, E))
+        cnts.scatter_(1, ids, 1)
+        tpe = cnts.sum(dim=0)
+        idxs = ids.view(-1).argsort()
+        sorted_tokens = x[idxs // k]
+        outs, start = [], 0
+        for e in range(E):
+            n = int(tpe[e])
+            if n == 0:
+                continue
+            toks = sorted_tokens[start:start + n]
+            outs.append(F.linear(F.silu(F.linear(toks, wg[e])) * F.linear(toks, wu[e]), wd[e]))
+            start += n
+        o = torch.cat(outs)
+        new_x = torch.empty_like(o)
+        new_x[idxs] = o
+        y = new_x.view(T, k, -1).to(w.dtype).mul_(w.unsqueeze(-1)).sum(1).to(new_x.dtype)
+        sg, su, sd = shared
+        return y + F.linear(F.silu(F.linear(x, sg)) * F.linear(x, su), sd)
+
+    def step():
+        for x, logits in layers:
+            moe_layer(x, logits)
+
+    with torch.inference_mode():
+        step()                                 # warmup
+        times = []
+        t_end = time.perf_counter() + 12.0
+        while len(times) < 20 and (time.perf_counter() < t_end or len(times) < 3):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    byts = n * (2 * I * H + H * I) * BF16
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()
-                     if i.get("user_api") == "blas"] or [1])
-    except Exception:   # threadpoolctl missing: numpy's BLAS pool size unknown
-        cores = os.cpu_count() or 1
-    return {"value": round(byts / med / 1e9, 3), "unit": "GB/s", "cores": cores,
+    return {"value": round(total_bytes / med / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"oracle per-expert loop (numpy, fp64 sums, bf16 rounding points), one "
-                      f"layer T={T} ({n} active experts), median of {len(times)} "
-                      f"({med * 1e3:.1f} ms); cpu={cpu_model()}"}
+            "sample": (f"torch CPU bf16: softmax top-{k} routing + the reference's stock per-expert loop "
+                       f"(build_oracle.py:34-67) + the shared expert, T={T}, one 256-expert layer under "
+                       f"{L} distinct routings cycled; median of {len(times)} passes "
+                       f"({med * 1e3 / L:.2f} ms per layer); cpu={cpu_model()}; os.cpu_count={os.cpu_count()}")}
 
 
 def run_copy(args, torch, dev):
@@ -1014,9 +1054,9 @@ def run_extras(args, torch, dev):
         warmup = 2 if wl == "c5" else max(2, args.warmup // 2)
         cmd = [sys.executable, os.path.abspath(__file__), "--workload", wl, "--steps", str(steps),
                "--warmup", str(warmup), "--no-extras"]
-        # host-core baselines: the headline's, and C5's (one iteration scaled
-        # from one timed layer of each model); the others would add minutes
-        if args.no_cpu_baseline or wl != "c5":
+        # every extra carries its own host-core baseline (~10-20 s of CPU
+        # work each, bounded inside the child)
+        if args.no_cpu_baseline:
             cmd.append("--no-cpu-baseline")
         print(f"bench: extra workload {wl} ({steps} steps, own process)", file=sys.stderr, flush=True)
         t0 = time.perf_counter()

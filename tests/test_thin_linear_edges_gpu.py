@@ -178,3 +178,40 @@ def test_make_bench_fn_indexes_the_pool():
     with torch.inference_mode():
         for i in range(3):
             assert torch.equal(fn(i), thin_linear(x, pool[i]))
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_int64_weight_offsets(M):
+    """A weight past 2^31 elements (kernels/thin_linear_fused.py:311 switches
+    its kernel to 64-bit offsets once N*K, M*K or M*N reaches 2^31): w is
+    [1114112, 2048] bf16, 2.28e9 elements, 4.25 GiB, so its byte offsets pass
+    2^32 from row 1048576 on.  The rows at the start, around the 2^31-element
+    / 2^32-byte boundary and at the end are checked against the oracle; a
+    32-bit offset would wrap the later ones onto the first rows."""
+    from kernels.thin_linear_fused import thin_linear
+    N, K = 1114112, 2048
+    assert N * K >= 2 ** 31 and N * K * 2 > 2 ** 32
+    print(f"int64 offsets: M={M} w[{N}, {K}] bf16", flush=True)
+    w = torch.empty(N, K, device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(1234)
+    for i in range(0, N, 131072):                        # bounded fp32 temporaries
+        n = min(131072, N - i)
+        w[i:i + n] = (torch.randn(n, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    x = rnd(M, K, seed=99)
+    with torch.inference_mode():
+        y = thin_linear(x, w)
+    torch.cuda.synchronize()
+    assert y.shape == (M, N)
+    edge = 2 ** 31 // K                                  # first row past 2^31 elements (and 2^32 bytes)
+    xs = x.double().cpu().numpy()
+    for lo in (0, edge - 64, N - 128):
+        rows = slice(lo, lo + 128)
+        ref = othin.linear_exact(xs, w[rows].double().cpu().numpy())
+        got = y[:, rows].double().cpu().numpy()
+        err = float(np.abs(got - ref).max())
+        assert err <= othin.tolerance(float(np.abs(ref).max()), "bf16"), (lo, err)
+        assert othin.max_abs_rel(got, ref) <= 1e-2, lo
+    # rows whose 32-bit byte offset would wrap onto the first rows differ from them
+    assert not torch.equal(y[:, edge:edge + 128], y[:, :128])
+    del w
+    torch.cuda.empty_cache()
