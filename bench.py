@@ -17,8 +17,10 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           the gated MLP block per layer (28 draft layers at M=4, 36 target
           layers at M=16/32): gate and up projections with SiLU-mul fused
           (thin_linear_silu_mul), then down; also times the unfused sequence.
-  layer4 / layer16 / layer32
-          the linear path of each decoder layer with the fused epilogues:
+  layer4 / layer16 / layer32 / layer36 / layer48
+          the linear path of each decoder layer with the fused epilogues
+          (36 and 48 rows: the verify with one or four committed blocks
+          folded in):
           RMSNorm + qkv, o, RMSNorm + gate/up + SiLU-mul, down (four launches;
           six above 8 tokens, where each norm is a launch of its own),
           against the unfused sequence with the stock PyTorch RMSNorm.
@@ -377,7 +379,7 @@ def run_layer(args, torch, dev):
     from kernels.thin_linear_fused import (thin_linear, thin_rmsnorm_linear,
                                            thin_rmsnorm_linear_silu_mul)
 
-    M = {"layer4": 4, "layer16": 16, "layer32": 32}[args.workload]
+    M = int(args.workload[len("layer"):])
     if M == 4:
         H, QKV, I, L = 2048, 4096, 6144, 28
     else:
@@ -629,16 +631,21 @@ def run_c5(args, torch, dev):
     """C5: random-init SDAR-1.7B draft and SDAR-8B target resident on one GPU,
     a 512-token prompt uniform over the vocabulary, 4-token blocks denoised in
     4 steps, K = 4 blocks verified per target forward (32 rows), greedy
-    acceptance, committed blocks written to the target cache by an extend
-    forward on a second stream (overlapping the next iteration's draft).
-    value = generated tokens / second over the timed iterations."""
+    acceptance; the blocks an acceptance commits are folded into the next
+    verify (their rows ahead of the 32, writing their K/V), so there is no
+    separate extend forward.  value = generated tokens / second over the
+    timed iterations.  The same run times, for comparison, the reference's
+    separate extend forward on a second stream and in line, and the
+    optimistic pipelined mode."""
     import time as _time
 
     from speculative.model import DRAFT_1P7B, TARGET_8B, SynthModel
     from speculative.step import SpecRunner
 
     steps, warm = args.steps, max(2, args.warmup)
-    max_ctx = 512 + 16 * (steps + warm + 2 * max(4, steps // 2)) + 64
+    # every iteration commits at most K x 4 = 16 tokens: the timed ones, the
+    # warmup, and three comparison modes of max(4, steps // 2) + 1 each
+    max_ctx = 512 + 16 * (steps + warm + 3 * (max(4, steps // 2) + 1)) + 64
     t_init = _time.perf_counter()
     draft = SynthModel(DRAFT_1P7B, dev, seed=11, max_ctx=max_ctx, max_rows=64)
     target = SynthModel(TARGET_8B, dev, seed=12, max_ctx=max_ctx, max_rows=64)
@@ -667,22 +674,25 @@ def run_c5(args, torch, dev):
     torch.cuda.synchronize()
     secs = _time.perf_counter() - t0
     it_ms = secs * 1e3 / steps
-    # the same iterations with the extend in line (no second stream), for comparison
-    runner.overlap = False
     n_serial = max(4, steps // 2)
-    t1 = _time.perf_counter()
-    for _ in range(n_serial):
-        runner.step()
-    torch.cuda.synchronize()
-    serial_ms = (_time.perf_counter() - t1) * 1e3 / n_serial
-    # and with the optimistic pipelined mode (next drafts beside the verify)
-    runner.overlap, runner.pipelined = True, True
-    t2 = _time.perf_counter()
-    for _ in range(n_serial):
-        runner.step()
-    runner.finish()
-    torch.cuda.synchronize()
-    pipe_ms = (_time.perf_counter() - t2) * 1e3 / n_serial
+
+    def timed_mode(fold, overlap, pipelined):
+        runner.fold, runner.overlap, runner.pipelined = fold, overlap, pipelined
+        runner.step()                     # captures the mode's graphs (the first switch flushes)
+        runner.finish()
+        torch.cuda.synchronize()
+        t = _time.perf_counter()
+        for _ in range(n_serial):
+            runner.step()
+        runner.finish()
+        torch.cuda.synchronize()
+        return (_time.perf_counter() - t) * 1e3 / n_serial
+
+    # the reference's separate extend forward, on a second stream beside the
+    # next iteration's draft and in line; then the optimistic pipelined mode
+    side_ms = timed_mode(False, True, False)
+    serial_ms = timed_mode(False, False, False)
+    pipe_ms = timed_mode(True, True, True)
 
     def layer_bytes(sh):
         H, D, I = sh.hidden, sh.head_dim, sh.intermediate
@@ -692,9 +702,10 @@ def run_c5(args, torch, dev):
     t_fwd = TARGET_8B.n_layers * layer_bytes(TARGET_8B)
     t_head = 2 * TARGET_8B.vocab * TARGET_8B.hidden
     d_fwds = runner.K * len(runner.schedule)
-    # per iteration: the draft forwards, the verify (layers and lm_head) and
-    # one extend forward of the committed blocks (layers only)
-    it_bytes = d_fwds * d_fwd + (t_fwd + t_head) + t_fwd
+    # per iteration: the draft forwards and the verify (layers, with the
+    # committed blocks folded in, and lm_head); a separate extend forward
+    # would add t_fwd
+    it_bytes = d_fwds * d_fwd + (t_fwd + t_head)
     gbs = it_bytes / (it_ms * 1e-3) / 1e9
     return {
         "metric": METRIC, "value": round(n_tok / secs, 2), "unit": "tok/s", "n_gpus": 1,
@@ -714,7 +725,8 @@ def run_c5(args, torch, dev):
         "phase_ms_per_iteration": {"draft": round(phase[0] / steps, 3), "verify": round(phase[1] / steps, 3),
                                    "accept_host": round(phase[2] / steps, 3),
                                    "extend_issue": round(phase[3] / steps, 3)},
-        "extend_on_second_stream": True,
+        "committed_blocks_folded_into_verify": True,
+        "ms_per_iteration_extend_second_stream": round(side_ms, 3),
         "ms_per_iteration_extend_in_line": round(serial_ms, 3),
         "ms_per_iteration_pipelined": round(pipe_ms, 3),
         "pipelined_optimistic_drafts": dict(runner.stats),
@@ -980,7 +992,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "head4", "head32", "attn4", "attn32", "c5", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "layer36", "layer48", "head4", "head32", "attn4", "attn32", "c5", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
@@ -1034,7 +1046,8 @@ def main():
 EXTRA_WORKLOADS = ("c1", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "c5")
 _EXTRA_KEYS = ("value", "unit", "ms_per_step", "steps", "config", "roofline", "breakdown", "tflops",
                "tokens_per_iteration", "accepted_draft_tokens_per_iteration", "committed_blocks_per_iteration",
-               "phase_ms_per_iteration", "ms_per_iteration_extend_in_line", "ms_per_iteration_pipelined",
+               "phase_ms_per_iteration", "ms_per_iteration_extend_second_stream",
+               "ms_per_iteration_extend_in_line", "ms_per_iteration_pipelined",
                "hbm_bound_ms_per_iteration", "cpu_baseline")
 
 

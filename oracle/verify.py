@@ -117,13 +117,22 @@ def cached_block_mask(ctx_len: int, s0: int, n_cols: int, n_prefix: int, n_free:
     scratch slots of these rows in row order.  The prefix is a committed block
     (accepted data); the free block is the block being denoised (it sees the
     context, the prefix and all of itself); verify blocks follow the
-    multi-block rule.  -> [R, n_cols] bool."""
+    multi-block rule.  -> [R, n_cols] bool.
+
+    The prefix may hold several committed blocks (of ``block_length``):
+    every later row sees all of them, and among themselves they are
+    block-causal, as the reference's runner flushes committed blocks into the
+    cache one block at a time (speculative_decoding/cache_aware.py:2324-2336,
+    each flush one _extend_cache_graph call of a full block, 1202-1259: a
+    block sees the context before it and all of itself)."""
     K = len(step_maps)
     R = n_prefix + n_free + 2 * K * block_length
     out = np.zeros((R, n_cols), dtype=bool)
     out[:, :ctx_len] = True
-    # prefix: seen by every row, and bidirectional among itself
-    out[:, s0:s0 + n_prefix] = True
+    # prefix: seen by every later row; block-causal among itself
+    out[n_prefix:, s0:s0 + n_prefix] = True
+    pb = np.arange(n_prefix) // block_length
+    out[:n_prefix, s0:s0 + n_prefix] = pb[None, :] <= pb[:, None]
     # free block: its rows see themselves
     out[n_prefix:n_prefix + n_free, s0 + n_prefix:s0 + n_prefix + n_free] = True
     if K:

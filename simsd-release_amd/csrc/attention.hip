@@ -873,7 +873,10 @@ __global__ __launch_bounds__(256) void block_mask_kernel(uint8_t* __restrict__ m
   } else if (col >= s0) {
     const int64_t u = col - s0;
     if (u < n_prefix) {
-      vis = true;
+      // committed blocks: every later row sees them all; among themselves
+      // block-causal, as when they are flushed into the cache one block at a
+      // time (a row sees its own block and the ones before it)
+      vis = row >= n_prefix || u / bl <= row / bl;
     } else if (u < n_prefix + n_free) {
       vis = row >= n_prefix && row < n_prefix + n_free;
     } else if (u < n_prefix + n_free + nv && row >= n_prefix + n_free) {

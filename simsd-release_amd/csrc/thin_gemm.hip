@@ -454,6 +454,8 @@ __global__ __launch_bounds__(64 * KS) void thin_gemm_lds_kernel(const char* __re
   constexpr int kTileRows = ROWS + (SIMSD_LDS_X ? 16 * CB : 0);
   constexpr int kTileBytes = KS * kTileRows * kLdsRow;
   constexpr int kRedBytes = (KS > 1 ? (KS - 1) * NF * 4 * 64 : 1) * 4;
+  static_assert(kTileBytes <= kLdsBytesGfx950 && kRedBytes <= kLdsBytesGfx950,
+                "LDS tiles beyond gfx950's 160 KiB per workgroup");
   __shared__ __attribute__((aligned(16))) char smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
   const int lane = threadIdx.x & 63;
   const int wk = threadIdx.x >> 6;
@@ -837,7 +839,11 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
   pl.glu = glu;
   // GEMV activations held per chunk: 256 (2 load steps) or 1024 (8) k elements
   pl.ch = block_k >= 512 ? 8 : 2;
-  pl.cb = M <= 16 ? 1 : 2;
+  // MFMA column blocks of 16 tokens: one up to 16, two up to 32; the 16-bit
+  // LDS-staged kernels also take three (33..48 tokens in one pass over the
+  // weight: the target's verify rows with a committed prefix folded in);
+  // more tokens go in 32-token tiles
+  pl.cb = M <= 16 ? 1 : ((kind == 2 && M > 32 && M <= 48) ? 3 : 2);
   pl.ms = M <= 4 ? 1 : 2;
   pl.tiles_m = kind == 1 ? cdiv(M, 4 * pl.ms) : cdiv(M, 16 * pl.cb);
   pl.ks = num_waves <= 0 ? 4 : num_waves;
@@ -872,6 +878,9 @@ int plan_geometry(ThinPlan& pl, int kind, int64_t M, int64_t N, int64_t K, int d
       pl.ks = rows / 32;
     }
   }
+  // 48 tokens on two 16-row blocks: 8 waves' LDS tiles would pass gfx950's
+  // 160 KiB, so such plans take 4 waves
+  if (pl.kind == 2 && pl.cb == 3 && pl.rb == 2 && pl.ks == 8) pl.ks = 4;
   pl.tiles_n = cdiv(N, rows);
   pl.steps = (int)cdiv(K * es, kind == 0 ? kStepBytes : kStep4Bytes);
   int split = split_k;
@@ -1036,9 +1045,16 @@ void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 
 template <int DT, int RB, int CB, bool GLU = false, int OUTR = 0>
 void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
+  // 8 waves of 32-row x 48-token tiles do not fit the LDS; their plans take 4
+  constexpr bool kEightFit = !(RB == 2 && CB == 3);
   switch (pl.ks) {
     case 2: launch_lds<DT, RB, CB, 2, GLU, OUTR>(pl, args, stream); break;
-    case 8: launch_lds<DT, RB, CB, 8, GLU, OUTR>(pl, args, stream); break;
+    case 8:
+      if constexpr (kEightFit) {
+        launch_lds<DT, RB, CB, 8, GLU, OUTR>(pl, args, stream);
+        break;
+      }
+      [[fallthrough]];
     default: launch_lds<DT, RB, CB, 4, GLU, OUTR>(pl, args, stream); break;
   }
 }
@@ -1074,10 +1090,12 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
     if (pl.kind == 3) {
       if (pl.glu) {
         if (pl.cb == 1) xs_shape<DT, 1, true>(pl, args, stream);
-        else xs_shape<DT, 2, true>(pl, args, stream);
+        else if (pl.cb == 2) xs_shape<DT, 2, true>(pl, args, stream);
+        else xs_shape<DT, 3, true>(pl, args, stream);
       } else {
         if (pl.cb == 1) xs_shape<DT, 1, false>(pl, args, stream);
-        else xs_shape<DT, 2, false>(pl, args, stream);
+        else if (pl.cb == 2) xs_shape<DT, 2, false>(pl, args, stream);
+        else xs_shape<DT, 3, false>(pl, args, stream);
       }
     } else if (pl.norm) {   // RMSNorm prologue: GEMV plans only
       if (pl.glu) {
@@ -1093,8 +1111,10 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
         else gemv4_rows<DT, 2, true>(pl, args, stream);
       } else if (pl.cb == 1) {
         lds_ks<DT, 2, 1, true>(pl, args, stream);
-      } else {
+      } else if (pl.cb == 2) {
         lds_ks<DT, 2, 2, true>(pl, args, stream);
+      } else {
+        lds_ks<DT, 2, 3, true>(pl, args, stream);
       }
     } else if (pl.kind == 1) {
       if (pl.ms == 1) gemv4_rows<DT, 1, false>(pl, args, stream);
@@ -1105,10 +1125,14 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
         if (pl.rows == 32) lds_ks<DT, 2, 1>(pl, args, stream);
         else if (pl.rows == 24) lds_ks<DT, 2, 1, false, 24>(pl, args, stream);
         else lds_ks<DT, 1, 1>(pl, args, stream);
-      } else {
+      } else if (pl.cb == 2) {
         if (pl.rows == 32) lds_ks<DT, 2, 2>(pl, args, stream);
         else if (pl.rows == 24) lds_ks<DT, 2, 2, false, 24>(pl, args, stream);
         else lds_ks<DT, 1, 2>(pl, args, stream);
+      } else {
+        if (pl.rows == 32) lds_ks<DT, 2, 3>(pl, args, stream);
+        else if (pl.rows == 24) lds_ks<DT, 2, 3, false, 24>(pl, args, stream);
+        else lds_ks<DT, 1, 3>(pl, args, stream);
       }
     }
   }

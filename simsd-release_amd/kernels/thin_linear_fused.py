@@ -50,8 +50,8 @@ second launch sums them in split order.
 
 Config tuples keep the reference's shape ``(BLOCK_M, BLOCK_N, BLOCK_K,
 SPLIT_K[, num_warps, num_stages])`` and describe the MI355X kernels:
-BLOCK_M is the token envelope (``TUNED``: dispatch for M up to 16 or 32) or
-column-block width (heuristic: 4 or 8 for the GEMV, 16 or 32 otherwise),
+BLOCK_M is the token envelope (``TUNED``: dispatch for M up to 16 or 64) or
+column-block width (heuristic: 4 or 8 for the GEMV, 16, 32 or 48 otherwise),
 BLOCK_N the weight rows per workgroup (4, 8, 16, 24, 32, 64, 96 or 128; other
 values round down to one of these; at least 16 above 8 tokens; 64, 96 and 128
 apply above 8 tokens in bf16/fp16 and act as 32 elsewhere; 24 applies to the
@@ -134,14 +134,16 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
     (2048, 151936): (16, 16, 256, 1, 4, 2),   # lm_head
     (2048, 4096): (16, 8, 256, 1, 4, 2),      # merged qkv          5.2 us
     (2048, 12288): (16, 16, 256, 1, 2, 2),    # merged gate+up     10.0 us
-    # 8B-class target, verify rows M <= 32 (hidden 4096, 32 q / 8 kv, inter 12288)
-    (4096, 12288): (32, 32, 256, 1, 4, 2),    # gate_proj / up_proj
-    (4096, 4096): (32, 16, 256, 1, 8, 2),     # q_proj, o_proj      8.7 / 11.2 us (M=16 / 32)
-    (4096, 1024): (32, 16, 256, 4, 4, 2),     # k_proj, v_proj
-    (4096, 6144): (32, 32, 256, 1, 4, 2),     # merged qkv         12.3 / 15.7 us
-    (4096, 24576): (32, 32, 256, 1, 4, 2),    # merged gate+up     33.4 / 39.3 us
-    (12288, 4096): (32, 16, 256, 1, 8, 2),    # down_proj          21.5 / 25.8 us
-    (4096, 151936): (32, 32, 256, 1, 4, 2),   # lm_head
+    # 8B-class target, verify rows M <= 64 (hidden 4096, 32 q / 8 kv, inter
+    # 12288): K blocks of (4 data + 4 mask) rows, plus up to K committed
+    # blocks folded in ahead of them (<= 48 rows at K = 4)
+    (4096, 12288): (64, 32, 256, 1, 4, 2),    # gate_proj / up_proj
+    (4096, 4096): (64, 16, 256, 1, 8, 2),     # q_proj, o_proj      8.7 / 11.2 us (M=16 / 32)
+    (4096, 1024): (64, 16, 256, 4, 4, 2),     # k_proj, v_proj
+    (4096, 6144): (64, 32, 256, 1, 4, 2),     # merged qkv         12.3 / 15.7 us
+    (4096, 24576): (64, 32, 256, 1, 4, 2),    # merged gate+up     33.4 / 39.3 us
+    (12288, 4096): (64, 16, 256, 1, 8, 2),    # down_proj          21.5 / 25.8 us
+    (4096, 151936): (64, 32, 256, 1, 4, 2),   # lm_head
 }
 
 # Token ranges inside an entry's envelope where another geometry wins:
@@ -176,7 +178,8 @@ def _tuned_for(M: int, N: int, K: int):
     An entry covers every M whose rounded-up block ``max(16, next_pow2(M))``
     fits its BLOCK_M: draft entries (BLOCK_M=16) stop at M=16, exactly the
     reference's rule (kernels/thin_linear_fused.py:232-242); target entries
-    (BLOCK_M=32) extend to the 32-row multi-block verify.  Inside the
+    (BLOCK_M=64) extend to the multi-block verify with committed blocks folded
+    in (32 rows plus up to 16).  Inside the
     envelope, the first ``TUNED_RANGES`` entry whose token range holds M
     takes over.
     """
@@ -199,8 +202,8 @@ def _heuristic_config(M: int, N: int, K: int, itemsize: int = 2) -> tuple[int, i
     """
     if itemsize == 2 and M <= 8:        # 4x4x4 GEMV: 4 tokens per column set
         BLOCK_M, BLOCK_K = (4 if M <= 4 else 8), 256
-    else:                               # 16x16 MFMA tiles
-        BLOCK_M = 16 if M <= 16 else 32
+    else:                               # 16x16 MFMA tiles: 1, 2 or (16-bit, 33..48 tokens) 3 column blocks
+        BLOCK_M = 16 if M <= 16 else (48 if itemsize == 2 and 32 < M <= 48 else 32)
         BLOCK_K = (256 if BLOCK_M == 16 else 128) * 2 // itemsize
     m_tiles = _cdiv(M, BLOCK_M)
     BLOCK_N = 4

@@ -12,15 +12,23 @@ draft blocks (data, mask), not the whole prompt.  Per iteration:
           forwards, [prefix 4 | block 4] rows; the rest run the block's 4
           rows), each unmasking ceil(remaining / steps left) positions by
           confidence (denoise_select)
-  verify  one target forward of the K x (4 data + 4 mask) rows; mask rows'
-          argmax (softmax_argmax)
+  verify  one target forward of [the blocks the last acceptance committed |
+          K x (4 data + 4 mask)] rows: the committed blocks are folded in
+          ahead of the verify rows and write their K/V to their permanent
+          slots (block-causal among themselves, seen by every verify row), so
+          no separate extend forward streams the target's weights again; the
+          lm_head runs on the mask rows only, whose argmax is all the
+          acceptance reads (softmax_argmax)
   accept  greedy match per block with first-reject truncation; a rejected
           block is committed padded with the draft's own tokens
           (partial_block_fill = "draft_argmax")
-  extend  one target forward of the committed block(s), storing their K/V,
-          on a second HIP stream: it overlaps the next iteration's draft
-          blocks, which only need the committed ids; the next verify waits
-          for it (an event).  ``overlap=False`` runs it in line.
+
+``fold=False`` keeps the reference's separate extend (cache_aware.py:
+1202-1259, _extend_cache_graph): one target forward of the committed
+block(s) storing their K/V, on a second HIP stream where it overlaps the next
+iteration's draft blocks (which only need the committed ids; the next verify
+waits for it), or in line with ``overlap=False``.  Every mode commits the
+same tokens.
 
 ``pipelined=True`` adds the reference's optimistic execution
 (cache_aware.py:2169-2668, speculative_generate_with_kv_cache_pipelined, there
@@ -84,9 +92,11 @@ def valid_bound(cache_len: int, end: int) -> int:
 
 class _Graphed:
     """A forward captured over static device buffers, one graph per key (the
-    attention's valid-length bound)."""
+    attention's valid-length bound).  ``head_rows``: the rows whose logits
+    the forward computes (all when None)."""
 
-    def __init__(self, rows: int, n_cols: int, device):
+    def __init__(self, rows: int, n_cols: int, device, head_rows: torch.Tensor | None = None):
+        self.head_rows = head_rows
         self.ids = torch.zeros(rows, dtype=torch.int64, device=device)
         self.pos = torch.zeros(rows, dtype=torch.int64, device=device)
         self.slots = torch.zeros(rows, dtype=torch.int64, device=device)
@@ -124,7 +134,7 @@ class SpecRunner:
 
     def __init__(self, draft: SynthModel, target: SynthModel, block_length: int = 4, denoise_steps: int = 4,
                  k_blocks: int = 4, mask_token_id: int = MASK_TOKEN_ID, overlap: bool = True,
-                 pipelined: bool = False):
+                 pipelined: bool = False, fold: bool = True):
         self.draft, self.target = draft, target
         self.bl, self.ds, self.K = block_length, denoise_steps, k_blocks
         self.mask_id = mask_token_id
@@ -133,19 +143,22 @@ class SpecRunner:
         bl, K = block_length, k_blocks
         dcols, tcols = draft.cache.full_len, target.cache.full_len
         self._dg = _Graphed(2 * bl, dcols, self.dev)                  # [prefix | block]
-        self._vg = _Graphed(2 * K * bl, tcols, self.dev)              # K x (data, mask)
+        self._vg = {}          # folded committed blocks c -> [c blocks | K x (data, mask)] graph
         self._eg = {}                                                 # committed blocks -> extend graph
         self._step_map = torch.full((bl,), -1, dtype=torch.int64, device=self.dev)
         self.draft_blocks = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
         self.step_maps = torch.zeros(K, bl, dtype=torch.int64, device=self.dev)
         self.overlap = overlap
         self.pipelined = pipelined
+        self.fold = fold
+        self._pending = []        # committed blocks not yet in the target cache (folded into the next verify)
+        self._verify_graph_now = None
         self.side = torch.cuda.Stream(device=self.dev)      # default priority
         self.draft_stream = torch.cuda.Stream(device=self.dev)
         self._extend_done = None
         self._verify_ready = None
-        self._verify_logits = {}      # bound -> the verify graph's logits output
-        self._verify_bound = None
+        self._verify_logits = {}      # (folded blocks, bound) -> the verify graph's logits output
+        self._verify_key = None
         self._draft_done = None       # optimistic drafts still running on draft_stream
         self._have_next = False       # draft_blocks hold valid drafts for the next iteration
         self.stats = {"optimistic_used": 0, "optimistic_dropped": 0}
@@ -194,10 +207,23 @@ class SpecRunner:
             denoise_select(logits, g.ids[bl:], self.mask_id, n_u, step, self._step_map)
         return None
 
-    def _verify_body(self, bound):
-        g = self._vg
-        logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid)
-        self._verify_logits[bound] = logits
+    def _verify_graph(self, c: int) -> _Graphed:
+        """The verify graph with ``c`` committed blocks folded in: rows
+        [c blocks | K x (bl data, bl mask)], logits of the mask rows only."""
+        g = self._vg.get(c)
+        if g is None:
+            bl, K = self.bl, self.K
+            n0 = c * bl
+            mask_rows = [n0 + 2 * k * bl + bl + j for k in range(K) for j in range(bl)]
+            g = _Graphed(n0 + 2 * K * bl, self.target.cache.full_len, self.dev,
+                         head_rows=torch.tensor(mask_rows, dtype=torch.int64, device=self.dev))
+            self._vg[c] = g
+        return g
+
+    def _verify_body(self, g, key):
+        logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=key[1], valid_len_dev=g.valid,
+                                     head_rows=g.head_rows)
+        self._verify_logits[key] = logits
         ids, _ = softmax_argmax(logits)
         return ids
 
@@ -239,32 +265,63 @@ class SpecRunner:
         if self._extend_done is not None:            # the target cache must hold the last commit
             torch.cuda.current_stream().wait_event(self._extend_done)
             self._extend_done = None
-        g, bl, K = self._vg, self.bl, self.K
-        ids = g.ids.view(K, 2, bl)
+        bl, K = self.bl, self.K
+        c = len(self._pending)
+        g = self._verify_graph(c)
+        n0 = c * bl
+        p0 = self.ctx - n0                           # the folded blocks' permanent slots [p0, ctx)
+        if c:
+            folded = torch.tensor([t for b in self._pending for t in b], dtype=torch.int64)
+            g.ids[:n0].copy_(folded.to(self.dev, non_blocking=True))
+        ids = g.ids[n0:].view(K, 2, bl)
         ids[:, 0].copy_(self.draft_blocks)
         ids[:, 1].fill_(self.mask_id)
+        ar = torch.arange(p0, self.ctx + 2 * K * bl, dtype=torch.int64, device=self.dev)
+        g.slots.copy_(ar)                            # folded blocks, then the verify rows' scratch
+        g.pos[:n0].copy_(ar[:n0])
         pos = torch.arange(self.ctx, self.ctx + K * bl, dtype=torch.int64, device=self.dev).view(K, 1, bl)
-        g.pos.view(K, 2, bl).copy_(pos.expand(K, 2, bl))       # masks share the data positions
-        g.slots.copy_(torch.arange(self.ctx, self.ctx + 2 * K * bl, dtype=torch.int64, device=self.dev))
+        g.pos[n0:].view(K, 2, bl).copy_(pos.expand(K, 2, bl))   # masks share the data positions
         g.valid.fill_(self.ctx + 2 * K * bl)
-        block_mask(self.target.cache.full_len, self.ctx, self.ctx, step_maps=self.step_maps,
+        block_mask(self.target.cache.full_len, p0, p0, n_prefix=n0, step_maps=self.step_maps,
                    block_length=bl, block_size=self.ds, out=g.mask)
         bound = valid_bound(self.target.cache.full_len, self.ctx + 2 * K * bl)
         # the verify's inputs are set: later work may overwrite draft_blocks / step_maps
         self._verify_ready = torch.cuda.Event()
         self._verify_ready.record()
-        self._verify_bound = bound
-        return g.replay(bound, lambda: self._verify_body(bound)).view(K, 2, bl)[:, 1]
+        self._verify_key = (c, bound)
+        self._verify_graph_now = g
+        out = g.replay(bound, lambda: self._verify_body(g, (c, bound)))
+        self._pending = []                           # their K/V are in the target cache now
+        return out.view(K, bl)
 
     @property
     def last_verify_logits(self) -> torch.Tensor:
-        """Logits [K * 2 * bl, V] of the last verify (rows: block k's data,
-        then its mask rows), valid until the next verify replays."""
-        return self._verify_logits[self._verify_bound]
+        """Logits [K * bl, V] of the last verify's mask rows (block k's mask
+        rows at k * bl ..), valid until the same graph replays again."""
+        return self._verify_logits[self._verify_key]
+
+    @property
+    def last_verify_ids(self) -> torch.Tensor:
+        """The last verify's argmax ids at the mask rows, [K, bl]."""
+        g = self._verify_graph_now
+        return g.outs[self._verify_key[1]].view(self.K, self.bl)
+
+    @property
+    def last_verify_drafts(self) -> torch.Tensor:
+        """The drafts the last verify checked, [K, bl] (a view of its inputs)."""
+        g = self._verify_graph_now
+        return g.ids[self._verify_key[0] * self.bl:].view(self.K, 2, self.bl)[:, 0]
+
+    @property
+    def last_verify_graph(self) -> _Graphed:
+        return self._verify_graph_now
 
     @torch.inference_mode()
-    def extend_(self, blocks):
+    def extend_(self, blocks, start: int | None = None):
+        """The committed ``blocks`` through the target, storing their K/V at
+        slots ``start`` .. (default: the committed context's end)."""
         n = len(blocks)
+        start = self.ctx if start is None else start
         g = self._extend_graph(n)
         ids = torch.tensor([t for b in blocks for t in b], dtype=torch.int64)
         main = torch.cuda.current_stream()
@@ -273,13 +330,24 @@ class SpecRunner:
             stream.wait_stream(main)                  # after the verify that wrote its rows
         with torch.cuda.stream(stream):
             g.ids.copy_(ids.to(self.dev, non_blocking=True))
-            g.set_span(self.ctx, self.ctx, n * self.bl)
-            block_mask(self.target.cache.full_len, self.ctx, self.ctx, n_prefix=n * self.bl, out=g.mask)
-            bound = valid_bound(self.target.cache.full_len, self.ctx + n * self.bl)
+            g.set_span(start, start, n * self.bl)
+            block_mask(self.target.cache.full_len, start, start, n_prefix=n * self.bl, block_length=self.bl,
+                       out=g.mask)
+            bound = valid_bound(self.target.cache.full_len, start + n * self.bl)
             g.replay(bound, lambda: self._extend_body(g, bound))
             if self.overlap:
                 self._extend_done = torch.cuda.Event()
                 self._extend_done.record(stream)
+
+    @torch.inference_mode()
+    def flush(self):
+        """Write the committed blocks still waiting to be folded into a verify
+        into the target cache now (an extend), so that it holds the whole
+        committed context."""
+        if self._pending:
+            n = len(self._pending)
+            self.extend_(self._pending, start=self.ctx - n * self.bl)
+            self._pending = []
 
     def finish(self):
         """Wait for work still running on the side streams (an extend, an
@@ -308,6 +376,8 @@ class SpecRunner:
         if self._draft_done is not None:              # optimistic drafts finish before use or redo
             main.wait_event(self._draft_done)
             self._draft_done = None
+        if self._pending and not self.fold:           # switched out of the folding mode
+            self.flush()
         if not self._have_next:
             self.draft_blocks_()
         self._have_next = False
@@ -320,12 +390,12 @@ class SpecRunner:
             K, bl = self.K, self.bl
             with torch.cuda.stream(self.draft_stream):
                 self.draft_stream.wait_event(self._verify_ready)
-                self.draft_blocks_(ctx=self.ctx + K * bl, last_block=self._vg.ids.view(K, 2, bl)[K - 1, 0])
+                self.draft_blocks_(ctx=self.ctx + K * bl, last_block=self.last_verify_drafts[K - 1])
                 self._draft_done = torch.cuda.Event()
                 self._draft_done.record(self.draft_stream)
         if events:
             events[2].record()
-        drafted = self._vg.ids.view(self.K, 2, self.bl)[:, 0]          # the drafts this verify checked
+        drafted = self.last_verify_drafts                              # the drafts this verify checked
         both = torch.stack([drafted, target_ids]).cpu()                # the one host sync
         committed, generated, n_acc = accept_blocks(both[0].tolist(), both[1].tolist(), self.bl)
         if self.pipelined:
@@ -333,7 +403,10 @@ class SpecRunner:
             self.stats["optimistic_used" if self._have_next else "optimistic_dropped"] += 1
         if events:
             events[3].record()
-        self.extend_(committed)
+        if self.fold:
+            self._pending = committed                 # rows of the next verify
+        else:
+            self.extend_(committed)
         self.ctx += self.bl * len(committed)
         self.history.extend(t for b in committed for t in b)
         self.last_block = torch.tensor(committed[-1], dtype=torch.int64, device=self.dev)

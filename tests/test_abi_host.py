@@ -85,7 +85,8 @@ def test_header_links_from_plain_c(tmp_path):
 @pytest.mark.parametrize("M,N,K", [(4, 2048, 2048), (4, 1024, 2048), (4, 12288, 2048),
                                    (4, 2048, 6144), (16, 4096, 4096), (32, 24576, 4096),
                                    (32, 4096, 12288), (4, 151936, 2048), (96, 2048, 2048),
-                                   (1, 1, 1), (7, 33, 1000), (24, 1024, 4096), (9, 100, 64)])
+                                   (1, 1, 1), (7, 33, 1000), (24, 1024, 4096), (9, 100, 64),
+                                   (36, 6144, 4096), (48, 4096, 12288), (40, 100, 64), (49, 4096, 4096)])
 def test_c_plan_equals_python_heuristic(M, N, K):
     from kernels import _native
     from kernels.thin_linear_fused import _heuristic_config
@@ -174,10 +175,12 @@ def test_tuned_table_envelope():
     assert _tuned_for(4, 999, 2048) is None
     assert should_fuse(4, 2048, 2048) and should_fuse(16, 2048, 2048)
     assert not should_fuse(32, 2048, 2048) and not should_fuse(96, 2048, 2048)
-    # target shapes extend to the 32-row verify, not to prefill
+    # target shapes extend to the verify with committed blocks folded in
+    # (up to 48 rows; the envelope is 64), not to prefill
     for K, N in [(4096, 6144), (4096, 4096), (4096, 24576), (12288, 4096), (4096, 151936)]:
         assert should_fuse(4, N, K) and should_fuse(16, N, K) and should_fuse(32, N, K)
-        assert not should_fuse(33, N, K) and not should_fuse(96, N, K)
+        assert should_fuse(36, N, K) and should_fuse(48, N, K) and should_fuse(64, N, K)
+        assert not should_fuse(65, N, K) and not should_fuse(96, N, K)
     assert len(pick_config(4, 2048, 2048)) == 4
     assert pick_config(96, 2048, 2048)[0] == 32
 

@@ -31,7 +31,9 @@ TINY = dict(hidden=256, n_layers=2, n_q_heads=2, n_kv_heads=1, intermediate=512,
                                   (37, 40, 4, 4, 4, 4, []),
                                   (100, 100, 0, 0, 4, 4, [[3, 0, 2, 1], [0, 1, 2, 3], [1, 3, 0, 2], [2, 2, 1, 0]]),
                                   (9, 12, 4, 0, 2, 2, [[1, 0], [0, -1], [-1, -1]]),
-                                  (64, 64, 4, 4, 8, 6, [[5, 4, 3, 2, 1, 0, 0, 1]])])
+                                  (64, 64, 4, 4, 8, 6, [[5, 4, 3, 2, 1, 0, 0, 1]]),
+                                  (20, 20, 12, 0, 4, 4, [[0, 1, 2, 3], [1, 0, 3, 2]]),
+                                  (33, 40, 8, 4, 4, 4, [[2, 2, 0, 1]])])
 def test_block_mask_vs_oracle(case):
     from kernels.attention_fused import block_mask
     ctx, s0, n_prefix, n_free, bl, bs, steps = case
@@ -49,11 +51,16 @@ def _models(seed=3, max_ctx=256):
             shape)
 
 
-def test_cached_verify_equals_full_sequence_forward():
-    """The runner's verify (cached context, K x (data, mask) rows) against one
-    forward of the whole verify sequence with the multi-block mask on a fresh
-    model of the same weights, and bit for bit against an eager forward of the
-    same rows."""
+@pytest.mark.parametrize("extra_blocks", [0, 2])
+def test_cached_verify_equals_full_sequence_forward(extra_blocks):
+    """The runner's verify -- cached context, the blocks the last acceptance
+    committed folded in ahead of the K x (data, mask) rows, logits of the mask
+    rows -- against one forward of the whole verify sequence with the
+    multi-block mask on a fresh model of the same weights, and bit for bit
+    against an eager forward of the same rows.  With ``extra_blocks`` two
+    more committed blocks (fixed ids) join the last acceptance's, so several
+    blocks are folded in at once (block-causal among themselves, as the
+    reference flushes them one at a time)."""
     from kernels.logits_fused import softmax_argmax
     from speculative.model import ModelShape, SynthModel
     from speculative.step import SpecRunner
@@ -65,13 +72,23 @@ def test_cached_verify_equals_full_sequence_forward():
     runner.prefill(prompt)
     for _ in range(2):                                  # grow the context past the prompt
         runner.step()
+    for b in range(extra_blocks):                       # more committed blocks, not yet in the target cache
+        blk = [(97 * b + 13 * j) % (V - 1) for j in range(4)]
+        runner._pending.append(blk)
+        runner.history.extend(blk)
+        runner.ctx += 4
+        runner.last_block = torch.tensor(blk, dtype=torch.int64, device=DEV)
     ctx = runner.ctx
+    n_folded = len(runner._pending)
+    assert n_folded >= 1 + extra_blocks
     runner.draft_blocks_()
     tgt = runner.verify_().clone()
     torch.cuda.synchronize()
-    g = runner._vg
-    logits_v = target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=runner._verify_bound,
-                              valid_len_dev=g.valid)
+    g = runner.last_verify_graph
+    c, bound = runner._verify_key
+    assert c == n_folded and g.ids.numel() == 4 * c + 32
+    logits_v = target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid,
+                              head_rows=g.head_rows)
     # the same sequence in full: prompt + committed blocks + the drafts
     drafts = runner.draft_blocks.cpu().tolist()
     steps = runner.step_maps.cpu().tolist()
@@ -87,7 +104,7 @@ def test_cached_verify_equals_full_sequence_forward():
     ar = torch.arange(n, device=DEV)
     logits = fresh.forward(torch.tensor(ids, device=DEV), torch.tensor(pos, device=DEV), ar, full_mask,
                            valid_len=n)
-    ref = logits[ctx:].float()
+    ref = logits[ctx:].float().view(4, 2, 4, V)[:, 1].reshape(16, V)       # the mask rows
     err = float((logits_v.float() - ref).abs().max())
     # a fresh model's full-sequence forward runs other attention forms and row
     # counts (other reduction orders): equal within the bf16 rounding of 2 x 36
@@ -98,7 +115,7 @@ def test_cached_verify_equals_full_sequence_forward():
     graph_logits = runner.last_verify_logits
     assert torch.equal(graph_logits, logits_v)
     am, _conf = softmax_argmax(logits_v)
-    assert torch.equal(am.view(4, 2, 4)[:, 1], tgt)
+    assert torch.equal(am.view(4, 4), tgt)
 
 
 def check_iteration(runner, gen, n_acc, ctx0, hist0):
@@ -108,14 +125,13 @@ def check_iteration(runner, gen, n_acc, ctx0, hist0):
     greedy acceptance (speculative_decode.py:895-953) of the drafts it
     checked against those ids."""
     K, bl = runner.K, runner.bl
-    logits = runner.last_verify_logits.float().cpu().numpy()
-    V = logits.shape[-1]
-    mask_rows = logits.reshape(K, 2, bl, V)[:, 1].reshape(K * bl, V)
+    mask_rows = runner.last_verify_logits.float().cpu().numpy()       # [K * bl, V]: the mask rows
+    assert mask_rows.shape[0] == K * bl
     ids, _, _ = olog.softmax_argmax(mask_rows)
     ids = ids.reshape(K, bl)
-    graph_ids = runner._vg.outs[runner._verify_bound].view(K, 2, bl)[:, 1].cpu().numpy()
+    graph_ids = runner.last_verify_ids.cpu().numpy()
     assert np.array_equal(graph_ids, ids)
-    drafts = runner._vg.ids.view(K, 2, bl)[:, 0].cpu().tolist()
+    drafts = runner.last_verify_drafts.cpu().tolist()
     committed, generated, acc = over.accept_blocks(drafts, ids.tolist(), bl)
     assert gen == generated and n_acc == acc
     assert runner.ctx - ctx0 == bl * len(committed)
@@ -144,13 +160,14 @@ def test_runner_iterations():
         assert sorted(row) == [0, 1, 2, 3]
 
 
-def _run(pipelined, draft_seed, target_seed, iters=6, prompt_seed=2):
+def _run(pipelined, draft_seed, target_seed, iters=6, prompt_seed=2, fold=True, overlap=True):
     from speculative.model import ModelShape, SynthModel
     from speculative.step import SpecRunner
     shape = ModelShape(**TINY)
     draft = SynthModel(shape, DEV, draft_seed, 256, 64)
     target = SynthModel(shape, DEV, target_seed, 256, 64)
-    runner = SpecRunner(draft, target, mask_token_id=shape.vocab - 1, pipelined=pipelined)
+    runner = SpecRunner(draft, target, mask_token_id=shape.vocab - 1, pipelined=pipelined, fold=fold,
+                        overlap=overlap)
     prompt = torch.randint(0, shape.vocab - 1, (32,), generator=torch.Generator().manual_seed(prompt_seed))
     runner.prefill(prompt)
     out = []
@@ -185,14 +202,31 @@ def test_pipelined_equals_sequential(same_weights):
         assert dropped >= 1, r_pip.stats
 
 
+def test_separate_extend_modes_agree():
+    """The reference's separate extend of the committed blocks (fold=False), in
+    line and on a second stream, commits the same tokens either way, with
+    every iteration equal to the oracle's acceptance; with equal weights it
+    extends four accepted blocks at once (block-causal among themselves)."""
+    for ts in (5, 6):
+        inline, r_in = _run(False, 5, ts, fold=False, overlap=False)
+        side, r_side = _run(False, 5, ts, fold=False, overlap=True)
+        assert inline == side and r_in.history_ids() == r_side.history_ids()
+
+
 def test_speculative_step_at_sdar_shapes():
     """The end-to-end step at its benchmark shapes: random-init SDAR-1.7B
     draft and SDAR-8B target on one GPU, a 512-token prompt, 4-token blocks,
     4 denoise steps, 4 blocks per verify.  Three iterations each with the
-    extend in line, on a second stream, and in the optimistic pipelined mode:
-    every iteration matches the oracle's argmax and acceptance on its own
-    verify logits, commits whole blocks without the mask id, and the three
-    modes commit the same tokens."""
+    committed blocks folded into the next verify (the default), with the
+    reference's separate extend in line and on a second stream, and in the
+    optimistic pipelined mode: every iteration matches the oracle's argmax and
+    acceptance on its own verify logits and commits whole blocks without the
+    mask id.  Modes that run the same kernels on the same rows (folded and
+    pipelined; extend in line and on a second stream) commit the same tokens;
+    the folded and extend forms write the committed blocks' K/V from forwards
+    of different row counts (other reduction orders), so their logits agree
+    within bf16 rounding, not bit for bit, and their tokens are compared per
+    iteration against the oracle instead."""
     from speculative.model import DRAFT_1P7B, TARGET_8B, SynthModel
     from speculative.step import SpecRunner
     from speculative.verify import MASK_TOKEN_ID
@@ -203,9 +237,10 @@ def test_speculative_step_at_sdar_shapes():
     prompt = torch.randint(0, DRAFT_1P7B.vocab - 1, (512,), generator=torch.Generator().manual_seed(5))
     histories = {}
     try:
-        for mode in ("inline", "overlap", "pipelined"):
+        for mode in ("fold", "inline", "overlap", "pipelined"):
             print(f"sdar shapes: mode {mode}", flush=True)
-            runner = SpecRunner(draft, target, overlap=mode != "inline", pipelined=mode == "pipelined")
+            runner = SpecRunner(draft, target, overlap=mode != "inline", pipelined=mode == "pipelined",
+                                fold=mode in ("fold", "pipelined"))
             runner.prefill(prompt)
             for it in range(3):
                 ctx0, hist0 = runner.ctx, runner.history_ids()
@@ -223,4 +258,4 @@ def test_speculative_step_at_sdar_shapes():
         del draft, target
         torch.cuda.empty_cache()
     assert histories["overlap"] == histories["inline"]
-    assert histories["pipelined"] == histories["inline"]
+    assert histories["pipelined"] == histories["fold"]

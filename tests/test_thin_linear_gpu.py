@@ -110,7 +110,7 @@ def test_leading_dims_preserved():
     assert float((got.float() - ref.float()).abs().max()) <= tol(ref)
 
 
-@pytest.mark.parametrize("M", [4, 7, 9, 16, 32])
+@pytest.mark.parametrize("M", [4, 7, 9, 16, 32, 40, 48])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_bias_every_tile_kind(M, dtype):
     """The bias epilogue of every kernel (the GEMV at M <= 8; the 16-, 24- and
@@ -194,7 +194,7 @@ def test_reduction_is_deterministic(split_k):
         assert float((first.float() - ref.float()).abs().max()) <= tol(ref)
 
 
-@pytest.mark.parametrize("M", [1, 4, 7, 9, 16, 24, 32, 40])
+@pytest.mark.parametrize("M", [1, 4, 7, 9, 16, 24, 32, 33, 40, 48, 49])
 def test_every_launch_shape(M):
     """Every rows / waves / split / block_k combination the planner accepts,
     on dims that leave partial tiles and a partial last k chunk."""
@@ -376,12 +376,14 @@ def _oracle_check(M, K, N, seed):
                                    (4, 2048, 4096), (4, 2048, 2048), (4, 6144, 2048),   # C2
                                    (16, 4096, 6144), (16, 4096, 4096), (16, 4096, 24576),
                                    (16, 12288, 4096), (32, 4096, 6144), (32, 4096, 4096),
-                                   (32, 4096, 24576), (32, 12288, 4096)])               # C3
+                                   (32, 4096, 24576), (32, 12288, 4096),                # C3
+                                   (36, 4096, 6144), (40, 4096, 4096), (44, 4096, 24576),
+                                   (48, 12288, 4096)])        # C3 verify with committed blocks folded in
 def test_oracle_baseline_shapes(M, K, N):
     _oracle_check(M, K, N, seed=M * 7 + K + N)
 
 
-@pytest.mark.parametrize("M", [16, 32])
+@pytest.mark.parametrize("M", [16, 32, 48])
 def test_oracle_lm_head_target(M):
     _oracle_check(M, 4096, 151936, seed=99 + M)
 
@@ -389,7 +391,7 @@ def test_oracle_lm_head_target(M):
 XS_TILES = [(64, 2), (64, 4), (96, 4), (128, 4), (128, 8)]   # (rows per workgroup, waves)
 
 
-@pytest.mark.parametrize("M", [9, 16, 17, 32])
+@pytest.mark.parametrize("M", [9, 16, 17, 32, 33, 48])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_shared_activation_tiles_vs_oracle(M, dtype):
     """The 64-, 96- and 128-row tiles (waves split the rows and share each
@@ -414,7 +416,7 @@ def test_shared_activation_tiles_vs_oracle(M, dtype):
             assert err <= othin.tolerance(amax, dtype), (K, N, rows, waves, split, err)
             assert othin.max_abs_rel(got, ref) <= 1e-2
     # gated: the target MLP's gate and up halves (odd I at the other M)
-    K, I = (4096, 12288) if M in (9, 32) else (1000, 531)
+    K, I = (4096, 12288) if M in (9, 32, 48) else (1000, 531)
     x = rnd(M, K, dtype=tdt, seed=80 + M)
     merged = rnd(2 * I, K, dtype=tdt, scale=0.02, seed=81)
     wg, wu = merged[:I], merged[I:]
@@ -429,7 +431,7 @@ def test_shared_activation_tiles_vs_oracle(M, dtype):
         assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("M", [9, 16, 17, 32])
+@pytest.mark.parametrize("M", [9, 16, 17, 32, 36, 48])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_partial_row_tiles_vs_oracle(M, dtype):
     """24-row tiles (two 16-row MFMA blocks, the second half-filled) against
@@ -456,12 +458,12 @@ def test_partial_row_tiles_vs_oracle(M, dtype):
                 assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("M", [3, 5, 13, 17, 31, 33, 64, 96])
+@pytest.mark.parametrize("M", [3, 5, 13, 17, 31, 33, 41, 48, 64, 96])
 def test_oracle_other_row_counts(M):
     _oracle_check(M, 2048, 1536, seed=M)
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 8, 9, 16, 32])
+@pytest.mark.parametrize("M", [1, 3, 4, 8, 9, 16, 32, 40])
 def test_fp16_every_kernel(M):
     """fp16 through the GEMV (M <= 8), the LDS kernel (M > 8) and the strided
     path, against the oracle's exact sum rounded to fp16, within the
@@ -481,7 +483,7 @@ def test_fp16_every_kernel(M):
 
 
 # ──────────────────────────────────────────── gated (SiLU-mul) projection ───
-@pytest.mark.parametrize("M", [1, 4, 8, 9, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 8, 9, 16, 32, 36, 48])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_silu_mul_vs_oracle(M, dtype):
     """thin_linear_silu_mul against the oracle's exact gated projection, on the
@@ -502,7 +504,7 @@ def test_silu_mul_vs_oracle(M, dtype):
         assert othin.max_abs_rel(got, ref) <= 1e-2
 
 
-@pytest.mark.parametrize("M", [4, 16, 32])
+@pytest.mark.parametrize("M", [4, 16, 32, 40])
 def test_silu_mul_every_launch_shape(M):
     from kernels.thin_linear_fused import thin_linear_silu_mul
     x = rnd(M, 1000, seed=60 + M)
@@ -601,7 +603,7 @@ def test_rmsnorm_vs_oracle(dtype):
         assert thin_rmsnorm(x.view(2, 4, 512), w, 1e-5).shape == (2, 4, 512)
 
 
-@pytest.mark.parametrize("M", [1, 4, 6, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 6, 8, 16, 32, 36, 48])
 @pytest.mark.parametrize("dtype", ["bf16", "fp16"])
 def test_rmsnorm_linear_vs_oracle(M, dtype):
     """The fused norm + linear (norm inside the GEMV at M <= 8, a separate
@@ -678,7 +680,7 @@ def test_properties_at_full_size():
             assert torch.equal(thin_linear(x, wt[:, 32:32 + K]), y)           # strided view
 
 
-@pytest.mark.parametrize("M", [1, 4, 6, 8, 16, 32])
+@pytest.mark.parametrize("M", [1, 4, 6, 8, 16, 32, 40, 48])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_linear_residual_vs_oracle(M, dtype):
     """residual + x w^T in one launch: bit-exact on small-integer data (every

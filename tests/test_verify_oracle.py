@@ -71,6 +71,25 @@ def test_cross_blocks_and_context():
     assert not m[:, s0 + 28:].any()
 
 
+def test_several_committed_blocks_are_block_causal():
+    """Three committed blocks folded in ahead of two verify blocks: each sees
+    the context, itself and the blocks before it (the reference flushes
+    committed blocks one at a time); every verify row sees all three."""
+    steps = [[0, 1, 2, 3], [1, 0, 3, 2]]
+    ctx, s0, n_cols = 20, 20, 64
+    m = over.cached_block_mask(ctx, s0, n_cols, 12, 0, steps, 4, 4)
+    assert m.shape == (12 + 16, n_cols)
+    p = m[:12, s0:s0 + 12].astype(int)
+    want = np.kron(np.tril(np.ones((3, 3), int)), np.ones((4, 4), int))
+    assert np.array_equal(p, want)
+    assert m[:, :ctx].all()
+    assert m[12:, s0:s0 + 12].all()
+    assert not m[:12, s0 + 12:].any()
+    # one committed block: all of it, as before
+    one = over.cached_block_mask(ctx, s0, n_cols, 4, 0, steps, 4, 4)
+    assert one[:4, s0:s0 + 4].all()
+
+
 def test_free_block_and_never_drafted():
     m = over.cached_block_mask(5, 8, 20, 4, 4, [], 4, 4)
     assert m[4:8, 8:16].all() and not m[:4, 12:16].any()
