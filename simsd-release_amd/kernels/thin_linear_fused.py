@@ -148,7 +148,9 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
 
 # Token ranges inside an entry's envelope where another geometry wins:
 # (K, N) -> (((M_lo, M_hi), 6-tuple), ...), first match taken.  Same sweep as
-# TUNED.  Above 8 tokens these are the shared-activation tiles (64 weight rows
+# TUNED; 33-48 tokens is the verify with committed blocks folded in (one
+# block at 36 rows), swept over rows x waves x split with 48-token column
+# blocks.  Above 8 tokens these are the shared-activation tiles (64 weight rows
 # per workgroup, waves splitting the rows) and, for the target's merged qkv,
 # 24-row tiles (256 workgroups for its 6144 rows, where 32-row tiles leave 64
 # CUs idle and 16-row tiles put two workgroups on half of them: 12.38 -> 11.62
@@ -158,8 +160,13 @@ TUNED: dict[tuple[int, int], tuple[int, int, int, int, int, int]] = {
 # with 8 rows; the plain projection moves by at most 0.4 us either way).
 TUNED_RANGES: dict[tuple[int, int], tuple[tuple[tuple[int, int], tuple[int, int, int, int, int, int]], ...]] = {
     (2048, 4096): (((5, 8), (16, 16, 256, 1, 4, 2)),),      # merged qkv      7.1 us (M=8)
-    (4096, 6144): (((9, 32), (32, 24, 256, 1, 4, 2)),),     # merged qkv     11.6 / 15.3 us (M=16 / 32)
-    (12288, 4096): (((9, 32), (32, 64, 256, 4, 4, 2)),),    # down_proj   22.0 / 23.3 us (M=16 / 32)
+    (4096, 6144): (((9, 32), (32, 24, 256, 1, 4, 2)),       # merged qkv     11.6 / 15.3 us (M=16 / 32)
+                   ((33, 48), (64, 24, 256, 2, 2, 2))),     #                17.7 / 18.3 us (M=36 / 48)
+    (4096, 4096): (((33, 48), (64, 16, 256, 1, 4, 2)),),    # o_proj         12.7 / 13.1 us (M=36 / 48)
+    (4096, 24576): (((33, 40), (64, 32, 256, 1, 2, 2)),     # gate+up (and the gated MLP) 45.3 us (M=36)
+                    ((41, 48), (64, 96, 256, 1, 8, 2))),    #                46.2 us (M=48)
+    (12288, 4096): (((9, 32), (32, 64, 256, 4, 4, 2)),      # down_proj   22.0 / 23.3 us (M=16 / 32)
+                    ((33, 48), (64, 32, 256, 4, 2, 2))),    #             26.2 / 27.9 us (M=36 / 48)
     (4096, 151936): (((17, 32), (32, 64, 256, 1, 4, 2)),),  # lm_head      234 us (M=32)
 }
 

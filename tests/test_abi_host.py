@@ -158,14 +158,17 @@ def test_tuned_table_envelope():
     assert _tuned_for(4, 2048, 2048) is not None
     assert _tuned_for(16, 2048, 2048) is not None
     assert _tuned_for(96, 2048, 2048) is None
-    # shared-activation entries inside their token range only
-    from kernels.thin_linear_fused import TUNED_RANGES
+    # range entries inside their token range only, never overlapping
+    from kernels.thin_linear_fused import TUNED_RANGES, _ROWS
     for (K, N), ranges in TUNED_RANGES.items():
         assert (K, N) in TUNED
+        spans = sorted(r for r, _ in ranges)
+        assert all(a[1] < b[0] for a, b in zip(spans, spans[1:]))
         for (lo, hi), cfg in ranges:
             assert 1 <= lo <= hi <= TUNED[(K, N)][0]
-            # wide or 24-row tiles only above 8 tokens
-            assert cfg[1] in (24, 64, 96, 128) if lo > 8 else hi <= 8
+            # rows the kernels are built for; at least 16 above 8 tokens
+            # (whole 16-row MFMA blocks), GEMV ranges stay within 8 tokens
+            assert cfg[1] in _ROWS and (cfg[1] >= 16 if lo > 8 else hi <= 8)
             assert _tuned_for(lo, N, K) == cfg and _tuned_for(hi, N, K) == cfg
             assert _tuned_for(lo - 1, N, K) == TUNED[(K, N)] or any(
                 a <= lo - 1 <= b for (a, b), _ in ranges)
