@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 16
+#define SIMSD_ABI_VERSION 17
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -328,6 +328,34 @@ int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void*
                           const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype, void* workspace,
                           int64_t workspace_bytes, void* stream);
 
+/* simsd_qkv_rope_attention: simsd_qkv_rope_cache followed by
+ * simsd_block_attention in one launch, for a forward of M <= 16 rows whose
+ * cache slots are the last M of the valid range, [lv - M, lv) with lv the
+ * (device-lowered) valid length -- the layout of every forward of the
+ * speculative runner.  Replaces, per layer, the q/k norm + RoPE of
+ * sdar/modeling_sdar.py:250-262, the cache write of
+ * adapters/base.py:186-236 (index_copy_) and the SDPA of
+ * adapters/base.py:245-262.  qkv [M, (Hq + 2 Hkv) * D] is the merged
+ * projection output (row stride sqkv); the other arguments are those of the
+ * two calls it replaces (no q_out: the rotated queries stay in registers; no
+ * second slots).  Writes the M rows' K (normed, rotated; rows with a
+ * position outside [0, n_pos) leave their K slot unwritten and attend with
+ * zero K) and V at their slots, and out.  Only the head form is fused: at
+ * most 32 query rows per KV head and L_valid <= 4096 slots, else the call
+ * fails (use the two calls).  16-byte aligned qkv rows, norm weights, cos /
+ * sin rows and K / V tiles.  Workspace: simsd_block_attention_workspace_bytes
+ * with the same arguments, under the same rules.  Deterministic; the q/k
+ * norm's fp32 sum of squares is ordered differently from
+ * simsd_qkv_rope_cache's, so outputs may differ from the two calls' in the
+ * last bit. */
+int simsd_qkv_rope_attention(const void* qkv, int64_t sqkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                             const void* cos, const void* sin, int64_t scs, int64_t n_pos, const int64_t* pos,
+                             void* k_cache, void* v_cache, int64_t kv_head_stride, int64_t L_cap,
+                             const uint8_t* mask, int64_t smask, void* out, int64_t so_m, int64_t so_h, int64_t M,
+                             int64_t Hq, int64_t Hkv, int64_t L_valid, const int64_t* valid_len_dev,
+                             int64_t head_dim, float scale, int dtype, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
 /* simsd_block_mask: the attention mask rows (uint8, 1 = visible; row stride
  * smask, n_cols slots) of a cached forward whose rows are n_prefix rows of a
  * committed block folded in (speculative_decoding/cache_aware.py:1062-1070),
@@ -337,7 +365,10 @@ int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void*
  * s0 in row order.  Verify visibility follows the multi-block rule of
  * sdar/new_attn_multi_block.py:22-183 with step_map [K, bl] (int64, device;
  * -1 = never drafted) and bs denoising steps per block; every row sees the
- * context and the prefix; the free block sees itself.  Replaces the torch
+ * context and the prefix; the free block sees itself.  A prefix of several
+ * committed blocks (n_prefix a multiple of bl) is block-causal among itself,
+ * as the reference flushes them into the cache one block at a time
+ * (cache_aware.py:2324-2336).  Replaces the torch
  * mask construction of cache_aware.py:1149-1180 and the multi-block mask
  * builder. */
 int simsd_block_mask(uint8_t* mask, int64_t smask, int64_t n_cols, int64_t ctx_len, int64_t s0, int n_prefix,

@@ -543,6 +543,165 @@ constexpr int kHeadMaxSplit = SIMSD_HEAD_MAX_SPLIT;   // workgroups per KV head 
 constexpr int kHeadW1 = SIMSD_HEAD_W1;
 constexpr int kHeadW2 = 4;
 
+// LDS of the head form: the waves' states, the merge weights and the split
+// hand-over's flag.
+template <int RBW, int W, int MAXS = kHeadMaxSplit>
+struct HeadShared {
+  static constexpr int ROWS = RBW * 16;
+  static constexpr int OSTR = kHeadDim + 4;   // padded rows: the b128 writes of 16 rows spread over the banks
+  float o[W][ROWS][OSTR];
+  float2 ml[W][ROWS];
+  float wt[W][ROWS];
+  float l[ROWS];
+  float mx[ROWS];
+  float wts[MAXS][ROWS];
+  int last;
+};
+
+// The head form's tail, shared by both head kernels: the W waves' online
+// softmax states merge in LDS (fixed wave order); S = 1 writes the
+// normalised rows; S > 1 writes this workgroup's partial, counts its arrival
+// and the last to arrive merges the S partials in workgroup order.
+template <int DT, int RBW, int W, int MAXS = kHeadMaxSplit>
+SIMSD_DEV void head_finish(HeadShared<RBW, W, MAXS>& sh, const f32x4_t (&acc)[RBW][kDTiles], const float (&m_run)[RBW],
+                           const float (&l_run)[RBW], const AttnArgs& a, int sp, int S, int h, int rows, int M,
+                           int n_rep, char* __restrict__ out, int64_t so_m, int64_t so_h) {
+  constexpr int ROWS = RBW * 16;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  // lane (g, r): acc[rb][dt][j] = O^T[dim dt*16 + 4g + j][row rb*16 + r]
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt)
+      *reinterpret_cast<f32x4_t*>(&sh.o[wv][rb * 16 + r][dt * 16 + 4 * g]) = acc[rb][dt];
+    if (g == 0) sh.ml[wv][rb * 16 + r] = make_float2(m_run[rb], l_run[rb]);
+  }
+  __syncthreads();
+  if (threadIdx.x < ROWS) {
+    const int row = threadIdx.x;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < W; ++v) mx = fmaxf(mx, sh.ml[v][row].x);
+    float l = 0.f;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      const float2 ml = sh.ml[v][row];
+      const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+      sh.wt[v][row] = wt;
+      l += ml.y * wt;
+    }
+    sh.l[row] = l;
+    sh.mx[row] = mx;
+  }
+  __syncthreads();
+  auto put = [&](int row, int d, float o, float l) {
+    const int i = row / M;
+    const int64_t m = row % M;
+    store_elem<DT>(out, m * so_m + (int64_t)(h * n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
+  };
+  if (S == 1) {
+    for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
+      const int row = e / kHeadDim, d = e % kHeadDim;
+      if (row >= rows) break;
+      float o = 0.f;
+#pragma unroll
+      for (int v = 0; v < W; ++v) o += sh.o[v][row][d] * sh.wt[v][row];
+      put(row, d, o, sh.l[row]);
+    }
+    return;
+  }
+  // this workgroup's partial: [h][sp][row][d] and (max, sum) [h][sp][row],
+  // two values per write-through store
+  const int64_t pbase = ((int64_t)h * S + sp) * ROWS;
+  for (int e = threadIdx.x; e < ROWS * kHeadDim / 2; e += 64 * W) {
+    const int row = e / (kHeadDim / 2), d = (e % (kHeadDim / 2)) * 2;
+    if (row >= rows) break;
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int v = 0; v < W; ++v) {
+      o0 += sh.o[v][row][d] * sh.wt[v][row];
+      o1 += sh.o[v][row][d + 1] * sh.wt[v][row];
+    }
+    put_through2(a.o_part + (pbase + row) * kHeadDim + d, o0, o1);
+  }
+  if (threadIdx.x < rows)
+    put_through2(reinterpret_cast<float*>(a.ml_part + pbase + threadIdx.x), sh.mx[threadIdx.x], sh.l[threadIdx.x]);
+  // Every thread's stores precede the barrier; thread 0's arrival follows it
+  // (the workgroup barrier orders them at workgroup scope, the arrival's
+  // release extends that to the agent).
+  __syncthreads();
+  if (threadIdx.x == 0) sh.last = arrive_last(a.arrivals + h, (unsigned)S);
+  __syncthreads();
+  if (!sh.last) return;
+  // this head's partials, workgroup q at [q][row].  The partial rows and the
+  // (max, sum) pairs are all loaded before any is used, so the merge waits
+  // for one round trip: plain 16-byte loads, ordered after the writers'
+  // stores by the arrival's release and the last arriver's acquire (which
+  // also drops this CU's stale cache lines).  Loads are unconditional
+  // (workgroups q >= S re-read the last one's; rows past rows read the
+  // workspace's row padding) so that none waits behind a branch; unused
+  // values are dropped by selects.
+  constexpr int kPer4 = ROWS * kHeadDim / 4 / (64 * W);
+  static_assert(kPer4 >= 1 && ROWS * kHeadDim % (4 * 64 * W) == 0, "whole float4 units per thread");
+  const float4* pO = reinterpret_cast<const float4*>(a.o_part + (int64_t)h * S * ROWS * kHeadDim);
+  const float2* pML = a.ml_part + (int64_t)h * S * ROWS;
+  float4 v4[kPer4][MAXS];
+#pragma unroll
+  for (int i = 0; i < kPer4; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;   // float4 unit: row e / 32, dims 4 (e % 32) ..
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q)
+      v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
+  }
+  if (threadIdx.x < rows) {
+    const int row = threadIdx.x;
+    float pm[MAXS], pl[MAXS];
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q) {
+      const float2 ml = pML[(q < S ? q : S - 1) * ROWS + row];
+      pm[q] = q < S ? ml.x : -INFINITY;
+      pl[q] = q < S ? ml.y : 0.f;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q)
+      if (q < S) mx = fmaxf(mx, pm[q]);
+    float l = 0.f;
+#pragma unroll
+    for (int q = 0; q < MAXS; ++q) {
+      const float wt = (q >= S || pm[q] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[q] - mx);
+      sh.wts[q][row] = wt;
+      l += pl[q] * wt;
+    }
+    sh.l[row] = l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer4; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;
+    const int row = e / (kHeadDim / 4), d = (e % (kHeadDim / 4)) * 4;
+    if (row < rows) {
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll
+      for (int q = 0; q < MAXS; ++q) {
+        const float wt = sh.wts[q][row];
+        o0 += q < S ? v4[i][q].x * wt : 0.f;
+        o1 += q < S ? v4[i][q].y * wt : 0.f;
+        o2 += q < S ? v4[i][q].z * wt : 0.f;
+        o3 += q < S ? v4[i][q].w * wt : 0.f;
+      }
+      const float l = sh.l[row];
+      put(row, d, o0, l);
+      put(row, d + 1, o1, l);
+      put(row, d + 2, o2, l);
+      put(row, d + 3, o3, l);
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The fields the first loads depend on come as leading scalar arguments,
 // which the build preloads into SGPRs; the rest of AttnArgs is read after.
 template <int DT, int RBW, int W>
@@ -551,17 +710,9 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(const char* __restric
                                                            const int64_t* __restrict__ lv_dev, int sq_m, int sq_h,
                                                            int sh, uint32_t head_bytes, int M, int n_rep, AttnArgs a,
                                                            char* __restrict__ out, int64_t so_m, int64_t so_h) {
-  constexpr int ROWS = RBW * 16;
   const int rows = n_rep * M;   // query rows of this KV head's group
   constexpr int kSplitMin = RBW == 1 ? kHeadSplitMinSlots1 : kHeadSplitMinSlots2;
-  constexpr int OSTR = kHeadDim + 4;   // padded rows: the b128 writes of 16 rows spread over the banks
-  __shared__ __attribute__((aligned(16))) float o_sh[W][ROWS][OSTR];
-  __shared__ float2 ml_sh[W][ROWS];
-  __shared__ float wt_sh[W][ROWS];
-  __shared__ float l_sh[ROWS];
-  __shared__ float mx_sh[ROWS];
-  __shared__ float wts_sh[kHeadMaxSplit][ROWS];
-  __shared__ int last_sh;
+  __shared__ __attribute__((aligned(16))) HeadShared<RBW, W> lds;
   constexpr int ES = DTypeInfo<DT>::kSize;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -618,136 +769,341 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(const char* __restric
     attn_step<DT, RBW>(a, qf, row_ok, bB, c, ce, g, m_run, l_run, acc);
     c += kStride;
   }
-  // lane (g, r): acc[rb][dt][j] = O^T[dim dt*16 + 4g + j][row rb*16 + r]
+  head_finish<DT, RBW, W>(lds, acc, m_run, l_run, a, sp, S, h, rows, M, n_rep, out, so_m, so_h);
+}
+
+// ------------------------------------ q/k norm + RoPE + cache write, fused
+// The prologue of qkv_rope_cache_kernel inside the head form, for a forward
+// whose M rows sit at the last M slots of the valid range [lv - M, lv) (the
+// speculative runner's forwards): every wave norms and rotates its own query
+// rows from the projection output as it loads them, and wave 0 of workgroup 0
+// of each KV head norms and rotates the M new keys, writes them and the new
+// values into the cache, and runs them as one extra 32-key step from
+// registers and LDS.  The other steps cover the cached slots [0, lv - M) and
+// are dealt exactly as in attn_head_kernel.  Rounding points as in
+// qkv_rope_cache_kernel (the stock RMSNorm, then
+// dtype(dtype(x * cos) + dtype(rotate_half(x) * sin))); only the order of the
+// norm's fp32 sum of squares differs (per lane over its 32 dims, then across
+// the head's four lanes).
+struct RopeArgs {
+  const char* qn;             // q_norm weight [D] or null
+  const char* kn;             // k_norm weight [D] or null
+  float eps;
+  const char* cos;            // [n_pos, D] rows (stride scs)
+  const char* sin;
+  int64_t scs, n_pos;
+  char* kcw;                  // the K / V tiles, written (the same as a.kc / a.vc)
+  char* vcw;
+  int Hq;
+};
+
+// The sum of one value per lane over the 16 lanes of a DPP row, the same fp32
+// value on every lane: each stage pairs lanes symmetrically (lane xor 1, xor
+// 2, then the half-row and row mirrors), and the add is commutative, so both
+// partners form the same sum.
+SIMSD_DEV float row16_sum(float v) {
+  v += __int_as_float(dpp_quad_xor1(__float_as_int(v)));
+  v += __int_as_float(dpp_quad_xor2(__float_as_int(v)));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));   // row_half_mirror
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));   // row_mirror
+  return v;
+}
+
+// Two values rounded to the dtype (bf16: one v_cvt_pk_bf16_f32, round to
+// nearest even as the element-wise rounding), as packed bits and as floats.
+template <int DT> SIMSD_DEV uint32_t pack_rnd2(float a, float b) { return pack2<DT>(a, b); }
+template <int DT> SIMSD_DEV f32x2_t unpack2(uint32_t u) {
+  return f32x2_t{h16_to_f32<DT>(u), h16_to_f32<DT>(u >> 16)};
+}
+template <int DT> SIMSD_DEV f32x2_t rnd2(float a, float b) { return unpack2<DT>(pack_rnd2<DT>(a, b)); }
+
+// Norm + RoPE of one (token, head) row spread over the 16 lanes of a DPP row:
+// lane j holds dims 8 j .. 8 j + 7 of x, of the norm weight w and of the cos
+// / sin row c, s; the rotate_half partner of dim d < 64 is d + 64, held by
+// lane j + 8, and back (one row rotation by 8).  Rounding points of
+// qkv_rope_cache_kernel: w * dtype(x * r), rounded (the stock RMSNorm, r
+// from the fp32 mean of squares), then dtype(dtype(x * cos) +
+// dtype(rotate_half(x) * sin)); only the order of the fp32 sum of squares
+// differs (per lane, then across the row).
+template <int DT>
+SIMSD_DEV u32x4_t norm_rope16(u32x4_t x, u32x4_t w, bool has_w, u32x4_t c, u32x4_t s, bool pos_ok, bool lower,
+                              float eps) {
+  const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+  f32x2_t xv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xv[i] = unpack2<DT>(xw[i]);
+  uint32_t xn[4] = {xw[0], xw[1], xw[2], xw[3]};
+  if (has_w) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ss += xv[i].x * xv[i].x;
+      ss += xv[i].y * xv[i].y;
+    }
+    ss = row16_sum(ss);
+    const float rr = 1.f / sqrtf(ss / (float)kHeadDim + eps);
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2_t t = rnd2<DT>(xv[i].x * rr, xv[i].y * rr);
+      const f32x2_t wf = unpack2<DT>(ww[i]);
+      xn[i] = pack_rnd2<DT>(wf.x * t.x, wf.y * t.y);
+      xv[i] = unpack2<DT>(xn[i]);
+    }
+  }
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w}, sw[4] = {s.x, s.y, s.z, s.w};
+  uint32_t y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t pf = unpack2<DT>((uint32_t)dpp_row_ror8((int)xn[i]));   // the partner lane's values
+    const f32x2_t cf = unpack2<DT>(cw[i]), sf = unpack2<DT>(sw[i]);
+    const f32x2_t a = rnd2<DT>(xv[i].x * cf.x, xv[i].y * cf.y);
+    const f32x2_t b = lower ? rnd2<DT>(-pf.x * sf.x, -pf.y * sf.y) : rnd2<DT>(pf.x * sf.x, pf.y * sf.y);
+    y[i] = pos_ok ? pack_rnd2<DT>(a.x + b.x, a.y + b.y) : 0u;
+  }
+  return u32x4_t{y[0], y[1], y[2], y[3]};
+}
+
+constexpr int kNewKeysMax = 16;   // new rows of a fused forward (one 16-key tile)
+constexpr int kTileStride = kHeadDim + 8;   // padded LDS rows of the q and K tiles (16-bit elements)
+
+// grid (S_max + 1, Hkv) when S_max > 1 (one more workgroup per KV head: the
+// new keys are one more dealt step), else (1, Hkv); W waves.
+// qkv: the projection output [M, (Hq + 2 Hkv) * D] (row stride sqkv).
+// Prologue: each (token, head) row of the projection output is a task of 16
+// lanes (8 dims each) -- the rows * q rows of this KV head's group, then its
+// M new keys and M new values -- dealt 4 to a wave pass; every workgroup
+// norms and rotates its q rows into LDS, the workgroup that takes the new
+// keys (below) its K into LDS and the cache and its V into LDS (transposed),
+// then one workgroup barrier, and every wave reads its Q^T fragments.
+// Steps: the new keys are step n_old = ceil((lv - M) / 32) in the head form's
+// dealing (steps i < n_old are the cached 32-key steps), so the wave that gets
+// them holds no cached step while the grid has a wave to spare; it writes the
+// new V into the cache and runs the new keys' step from LDS.
+template <int DT, int RBW, int W>
+__global__ __launch_bounds__(64 * W) void attn_head_rope_kernel(const char* __restrict__ qkv, const char* __restrict__ kc,
+                                                                const char* __restrict__ vc,
+                                                                const int64_t* __restrict__ lv_dev,
+                                                                const int64_t* __restrict__ pos, int sqkv, int sh,
+                                                                uint32_t head_bytes, int M, int n_rep, AttnArgs a,
+                                                                RopeArgs ra, char* __restrict__ out, int64_t so_m,
+                                                                int64_t so_h) {
+  constexpr int MAXS = kHeadMaxSplit + 1;
+  constexpr int ROWS = RBW * 16;
+  constexpr int kPasses = (ROWS + 2 * kNewKeysMax + 4 * W - 1) / (4 * W);   // task passes per wave
+  const int rows = n_rep * M;
+  constexpr int kSplitMin = RBW == 1 ? kHeadSplitMinSlots1 : kHeadSplitMinSlots2;
+  __shared__ __attribute__((aligned(16))) HeadShared<RBW, W, MAXS> lds;
+  __shared__ __attribute__((aligned(16))) uint16_t q_t[ROWS][kTileStride];          // rotated q rows
+  __shared__ __attribute__((aligned(16))) uint16_t k_t[kNewKeysMax][kTileStride];   // new K rows
+  __shared__ __attribute__((aligned(16))) uint16_t vt_t[kHeadDim][32];              // new V, [dim][key]
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int sp = (int)blockIdx.x;
+  const int h = blockIdx.y;
+
+  // scalar loads of the rows' positions (uniform addresses, in bounds)
+  int64_t pt[kNewKeysMax];
+#pragma unroll
+  for (int t = 0; t < kNewKeysMax; ++t) pt[t] = pos[t < M ? t : 0];
+
+  // this lane's tasks: task id = (pass * W + wave) * 4 + lane / 16, dims
+  // 8 (lane % 16) ..; ids past the last task re-read task 0 and are dropped
+  const int n_tasks = rows + 2 * M;
+  const int jd = 8 * (lane & 15);
+  int t_kind[kPasses], t_tok[kPasses];   // kind 0: q row, 1: new key, 2: new value, -1: none
+  u32x4_t t_x[kPasses], t_w[kPasses];
+  const char* qn_p = ra.qn != nullptr ? ra.qn : ra.cos;
+  const char* kn_p = ra.kn != nullptr ? ra.kn : ra.cos;
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int t = (p * W + wv) * 4 + (lane >> 4);
+    int kind = -1, tok = 0, head = 0;
+    if (t < rows) {
+      kind = 0; tok = t % M; head = h * n_rep + t / M;
+    } else if (t < rows + M) {
+      kind = 1; tok = t - rows; head = ra.Hq + h;
+    } else if (t < n_tasks) {
+      kind = 2; tok = t - rows - M; head = ra.Hq + a.Hkv + h;
+    }
+    t_kind[p] = kind;
+    t_tok[p] = tok;
+    t_x[p] = *reinterpret_cast<const u32x4_t*>(qkv + ((int64_t)tok * sqkv + (int64_t)head * kHeadDim + jd) * ES);
+    t_w[p] = *reinterpret_cast<const u32x4_t*>((kind == 1 ? kn_p : qn_p) + jd * ES);
+  }
+  // the first cached step's K / V, before the valid length is known
+  int tok_q[RBW];
+  bool row_ok[RBW];
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) {
-#pragma unroll
-    for (int dt = 0; dt < kDTiles; ++dt)
-      *reinterpret_cast<f32x4_t*>(&o_sh[wv][rb * 16 + r][dt * 16 + 4 * g]) = acc[rb][dt];
-    if (g == 0) ml_sh[wv][rb * 16 + r] = make_float2(m_run[rb], l_run[rb]);
+    const int row = rb * 16 + r;
+    row_ok[rb] = row < rows;
+    tok_q[rb] = row_ok[rb] ? row % M : 0;
   }
-  __syncthreads();
-  if (threadIdx.x < ROWS) {
-    const int row = threadIdx.x;
-    float mx = -INFINITY;
-#pragma unroll
-    for (int v = 0; v < W; ++v) mx = fmaxf(mx, ml_sh[v][row].x);
-    float l = 0.f;
-#pragma unroll
-    for (int v = 0; v < W; ++v) {
-      const float2 ml = ml_sh[v][row];
-      const float wt = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
-      wt_sh[v][row] = wt;
-      l += ml.y * wt;
-    }
-    l_sh[row] = l;
-    mx_sh[row] = mx;
+  const WaveKV<RBW> w = wave_kv<DT, RBW>(kc, vc, sh, head_bytes, a, h, tok_q, g, r);
+  StepBuf<RBW> bA, bB;
+  int c = (sp * W + wv) * kKeyStep;
+  attn_load<DT, RBW>(a, w, c, bA);
+  int64_t lv = a.L_valid;
+  if (lv_dev != nullptr) {
+    const int64_t d = *lv_dev;
+    lv = d < 0 ? 0 : (d < lv ? d : lv);
   }
-  __syncthreads();
-  auto put = [&](int row, int d, float o, float l) {
-    const int i = row / (int)M;
-    const int64_t m = row % (int)M;
-    store_elem<DT>(out, m * so_m + (int64_t)(h * n_rep + i) * so_h + d, l > 0.f ? o / l : 0.f);
-  };
-  if (S == 1) {
-    for (int e = threadIdx.x; e < ROWS * kHeadDim; e += 64 * W) {
-      const int row = e / kHeadDim, d = e % kHeadDim;
-      if (row >= rows) break;
-      float o = 0.f;
+  const int ce = (int)lv;
+  const int s0 = ce - M;   // the new rows' slots: [s0, ce)
+  // cos / sin at each task's position
+  u32x4_t t_c[kPasses], t_s[kPasses];
+  bool t_pos_ok[kPasses];
 #pragma unroll
-      for (int v = 0; v < W; ++v) o += o_sh[v][row][d] * wt_sh[v][row];
-      put(row, d, o, l_sh[row]);
-    }
-    return;
+  for (int p = 0; p < kPasses; ++p) {
+    int64_t pp = pt[0];
+#pragma unroll
+    for (int t = 1; t < kNewKeysMax; ++t) pp = t_tok[p] == t ? pt[t] : pp;
+    t_pos_ok[p] = pp >= 0 && pp < ra.n_pos;
+    const int64_t pr = t_pos_ok[p] ? pp : 0;
+    t_c[p] = *reinterpret_cast<const u32x4_t*>(ra.cos + (pr * ra.scs + jd) * ES);
+    t_s[p] = *reinterpret_cast<const u32x4_t*>(ra.sin + (pr * ra.scs + jd) * ES);
   }
-  // this workgroup's partial: [h][sp][row][d] and (max, sum) [h][sp][row],
-  // two values per write-through store
-  const int64_t pbase = ((int64_t)h * S + sp) * ROWS;
-  for (int e = threadIdx.x; e < ROWS * kHeadDim / 2; e += 64 * W) {
-    const int row = e / (kHeadDim / 2), d = (e % (kHeadDim / 2)) * 2;
-    if (row >= rows) break;
-    float o0 = 0.f, o1 = 0.f;
+  // the mask bytes of the new keys (columns s0 + 16 t + 4 g + j), a byte at a
+  // time: s0 has any alignment
+  uint8_t nmb[RBW][2][4];
 #pragma unroll
-    for (int v = 0; v < W; ++v) {
-      o0 += o_sh[v][row][d] * wt_sh[v][row];
-      o1 += o_sh[v][row][d + 1] * wt_sh[v][row];
-    }
-    put_through2(a.o_part + (pbase + row) * kHeadDim + d, o0, o1);
-  }
-  if (threadIdx.x < rows)
-    put_through2(reinterpret_cast<float*>(a.ml_part + pbase + threadIdx.x), mx_sh[threadIdx.x], l_sh[threadIdx.x]);
-  // Every thread's stores precede the barrier; thread 0's arrival follows it
-  // (the workgroup barrier orders them at workgroup scope, the arrival's
-  // release extends that to the agent).
-  __syncthreads();
-  if (threadIdx.x == 0) last_sh = arrive_last(a.arrivals + h, (unsigned)S);
-  __syncthreads();
-  if (!last_sh) return;
-  // this head's partials, workgroup q at [q][row].  The partial rows and the
-  // (max, sum) pairs are all loaded before any is used, so the merge waits
-  // for one round trip: plain 16-byte loads, ordered after the writers'
-  // stores by the arrival's release and the last arriver's acquire (which
-  // also drops this CU's stale cache lines).  Loads are unconditional
-  // (workgroups q >= S re-read the last one's; rows past rows read the
-  // workspace's row padding) so that none waits behind a branch; unused
-  // values are dropped by selects.
-  constexpr int kPer4 = ROWS * kHeadDim / 4 / (64 * W);
-  static_assert(kPer4 >= 1 && ROWS * kHeadDim % (4 * 64 * W) == 0, "whole float4 units per thread");
-  const float4* pO = reinterpret_cast<const float4*>(a.o_part + (int64_t)h * S * ROWS * kHeadDim);
-  const float2* pML = a.ml_part + (int64_t)h * S * ROWS;
-  float4 v4[kPer4][kHeadMaxSplit];
+  for (int rb = 0; rb < RBW; ++rb) {
+    const uint8_t* mr = a.mask != nullptr ? a.mask + (int64_t)tok_q[rb] * a.smask
+                                          : reinterpret_cast<const uint8_t*>(ra.cos);
 #pragma unroll
-  for (int i = 0; i < kPer4; ++i) {
-    const int e = (int)threadIdx.x + i * 64 * W;   // float4 unit: row e / 32, dims 4 (e % 32) ..
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q)
-      v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
-  }
-  if (threadIdx.x < rows) {
-    const int row = threadIdx.x;
-    float pm[kHeadMaxSplit], pl[kHeadMaxSplit];
-#pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q) {
-      const float2 ml = pML[(q < S ? q : S - 1) * ROWS + row];
-      pm[q] = q < S ? ml.x : -INFINITY;
-      pl[q] = q < S ? ml.y : 0.f;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q)
-      if (q < S) mx = fmaxf(mx, pm[q]);
-    float l = 0.f;
-#pragma unroll
-    for (int q = 0; q < kHeadMaxSplit; ++q) {
-      const float wt = (q >= S || pm[q] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[q] - mx);
-      wts_sh[q][row] = wt;
-      l += pl[q] * wt;
-    }
-    l_sh[row] = l;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kPer4; ++i) {
-    const int e = (int)threadIdx.x + i * 64 * W;
-    const int row = e / (kHeadDim / 4), d = (e % (kHeadDim / 4)) * 4;
-    if (row < rows) {
-      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-#pragma unroll
-      for (int q = 0; q < kHeadMaxSplit; ++q) {
-        const float wt = wts_sh[q][row];
-        o0 += q < S ? v4[i][q].x * wt : 0.f;
-        o1 += q < S ? v4[i][q].y * wt : 0.f;
-        o2 += q < S ? v4[i][q].z * wt : 0.f;
-        o3 += q < S ? v4[i][q].w * wt : 0.f;
+      for (int j = 0; j < 4; ++j) {
+        const int k = s0 + 16 * t + 4 * g + j;
+        nmb[rb][t][j] = mr[k >= 0 && k < ce ? k : 0];
       }
-      const float l = l_sh[row];
-      put(row, d, o0, l);
-      put(row, d + 1, o1, l);
-      put(row, d + 2, o2, l);
-      put(row, d + 3, o3, l);
+  }
+  // steps: the cached ones i < n_old, then the new keys as step n_old; step
+  // i goes to workgroup (i / W) % S, wave i % W
+  const int n_old = s0 > 0 ? (s0 + kKeyStep - 1) / kKeyStep : 0;
+  const int S = (gridDim.x == 1 || ce <= kSplitMin)
+                    ? 1
+                    : min((int)gridDim.x, (n_old + 1 + W - 1) / W);
+  if (sp >= S) return;
+  const int new_wg = (n_old / W) % S;
+  const bool owner = new_wg == sp && n_old % W == wv;
+  char* kb = ra.kcw + (int64_t)h * sh * ES;
+  char* vb = ra.vcw + (int64_t)h * sh * ES;
+  // the tasks: q rows in every workgroup, the new keys and values in the one
+  // that runs their step
+  const bool lower = (lane & 15) < 8;   // dims below 64: partner d + 64
+#pragma unroll
+  for (int p = 0; p < kPasses; ++p) {
+    const int kind = t_kind[p], tok = t_tok[p];
+    const int t = (p * W + wv) * 4 + (lane >> 4);
+    if (kind == 0) {
+      const u32x4_t y = norm_rope16<DT>(t_x[p], t_w[p], ra.qn != nullptr, t_c[p], t_s[p], t_pos_ok[p], lower, ra.eps);
+      *reinterpret_cast<u32x4_t*>(&q_t[t][jd]) = y;
+    } else if (kind == 1 && sp == new_wg) {
+      const u32x4_t y = norm_rope16<DT>(t_x[p], t_w[p], ra.kn != nullptr, t_c[p], t_s[p], t_pos_ok[p], lower, ra.eps);
+      *reinterpret_cast<u32x4_t*>(&k_t[tok][jd]) = y;
+      const int64_t slot = (int64_t)s0 + tok;
+      if (t_pos_ok[p] && slot >= 0 && slot < a.L_cap)
+        *reinterpret_cast<u32x4_t*>(kb + k_tile_index(slot, jd) * ES) = y;
+    } else if (kind == 2 && sp == new_wg) {
+      const uint32_t vw[4] = {t_x[p].x, t_x[p].y, t_x[p].z, t_x[p].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt_t[jd + e][tok] = (uint16_t)(vw[e >> 1] >> (16 * (e & 1)));
     }
   }
-  if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  lds_barrier();
+  u32x4_t qf[RBW][kDSteps];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+    for (int ds = 0; ds < kDSteps; ++ds) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&q_t[rb * 16 + r][ds * 32 + 8 * g]);
+      qf[rb][ds] = row_ok[rb] ? v : zero4();
+    }
+
+  float m_run[RBW], l_run[RBW];
+  f32x4_t acc[RBW][kDTiles];
+#pragma unroll
+  for (int rb = 0; rb < RBW; ++rb) {
+    m_run[rb] = -INFINITY;
+    l_run[rb] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) acc[rb][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  if (owner) {
+    const bool key_ok = r < M;   // new key r = token r, lane row r
+    StepBuf<RBW> bn;
+#pragma unroll
+    for (int ds = 0; ds < kDSteps; ++ds) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&k_t[r][ds * 32 + 8 * g]);
+      bn.kf[0][ds] = key_ok ? v : zero4();
+      bn.kf[1][ds] = zero4();
+    }
+    // keys past M hold stale LDS bits: the step zeroes their V and masks their
+    // scores (they sit past ce)
+#pragma unroll
+    for (int dt = 0; dt < kDTiles; ++dt) {
+      const int d = dt * 16 + r;
+      const uint2 lo = *reinterpret_cast<const uint2*>(&vt_t[d][4 * g]);
+      const uint2 hi = *reinterpret_cast<const uint2*>(&vt_t[d][16 + 4 * g]);
+      bn.vf[dt] = u32x4_t{lo.x, lo.y, hi.x, hi.y};
+    }
+    // the new V into the cache: lane l takes dims l and l + 64 and, for each
+    // quad of new keys, their 4 contiguous values in the V tile (slots
+    // s0 + 4 q .. + 3 share a tile row when s0 % 4 == 0, the runner's case;
+    // else one value at a time)
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int d = lane + 64 * half;
+      if ((s0 & 3) == 0) {
+        for (int q4 = 0; q4 < (M + 3) / 4; ++q4) {
+          const int64_t sq4 = (int64_t)s0 + 4 * q4;
+          const int nk = min(4, M - 4 * q4);
+          if (sq4 >= 0 && sq4 + 3 < a.L_cap && nk == 4) {
+            *reinterpret_cast<uint2*>(vb + v_tile_index(sq4, d) * ES) =
+                *reinterpret_cast<const uint2*>(&vt_t[d][4 * q4]);
+          } else {
+            for (int k = 0; k < nk; ++k)
+              if (sq4 + k >= 0 && sq4 + k < a.L_cap)
+                store_elem<DT>(vb, v_tile_index(sq4 + k, d), h16_to_f32<DT>(vt_t[d][4 * q4 + k]));
+          }
+        }
+      } else {
+        for (int k = 0; k < M; ++k)
+          if ((int64_t)s0 + k >= 0 && (int64_t)s0 + k < a.L_cap)
+            store_elem<DT>(vb, v_tile_index((int64_t)s0 + k, d), h16_to_f32<DT>(vt_t[d][k]));
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RBW; ++rb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        uint32_t mw = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k = s0 + 16 * t + 4 * g + j;
+          const bool vis = a.mask == nullptr || nmb[rb][t][j] != 0;
+          mw |= (k >= 0 && k < ce && vis ? 1u : 0u) << (8 * j);
+        }
+        bn.mk[rb][t] = mw;
+      }
+    attn_step<DT, RBW>(a, qf, row_ok, bn, s0, ce, g, m_run, l_run, acc);
+  }
+  // the cached slots [0, s0)
+  const int kStride = S * W * kKeyStep;
+  while (c < s0) {
+    attn_load<DT, RBW>(a, w, c + kStride, bB);
+    attn_step<DT, RBW>(a, qf, row_ok, bA, c, s0, g, m_run, l_run, acc);
+    c += kStride;
+    if (c >= s0) break;
+    attn_load<DT, RBW>(a, w, c + kStride, bA);
+    attn_step<DT, RBW>(a, qf, row_ok, bB, c, s0, g, m_run, l_run, acc);
+    c += kStride;
+  }
+  head_finish<DT, RBW, W, MAXS>(lds, acc, m_run, l_run, a, sp, S, h, rows, M, n_rep, out, so_m, so_h);
 }
 
 constexpr int kMaxChunks = 1024;
@@ -952,7 +1308,9 @@ AttnPlan attn_plan(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
   // workspace: [arrival counters][o partials][(max, sum) partials]; the
   // counters come first in every form so that a workspace shared between
   // calls keeps them at zero
-  const int64_t parts = p.head ? p.split : p.n_chunks;
+  // the head form's partials: split, or split + 1 in the fused launch (its
+  // new keys take one more workgroup), whichever call uses the workspace
+  const int64_t parts = p.head ? (p.split > 1 ? p.split + 1 : 1) : p.n_chunks;
   p.cnt_bytes = up256(Hkv * 4);
   p.o_bytes = up256(Hkv * parts * p.rows_pad * kHeadDim * 4);
   p.ml_bytes = up256(Hkv * parts * p.rows_pad * 8);
@@ -1081,6 +1439,80 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
   if (dtype == kBF16) partial(std::integral_constant<int, kBF16>{});
   else partial(std::integral_constant<int, kF16>{});
   return check_launch("block_attention");
+}
+
+extern "C" int simsd_qkv_rope_attention(const void* qkv, int64_t sqkv, const void* q_norm_w, const void* k_norm_w,
+                                        float eps, const void* cos, const void* sin, int64_t scs, int64_t n_pos,
+                                        const int64_t* pos, void* k_cache, void* v_cache, int64_t kv_head_stride,
+                                        int64_t L_cap, const uint8_t* mask, int64_t smask, void* out, int64_t so_m,
+                                        int64_t so_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid,
+                                        const int64_t* valid_len_dev, int64_t head_dim, float scale, int dtype,
+                                        void* workspace, int64_t workspace_bytes, void* stream) {
+  if (dtype != kBF16 && dtype != kF16) return set_error("qkv_rope_attention: dtype must be bf16 or fp16");
+  if (head_dim != kHeadDim)
+    return set_error("qkv_rope_attention: head_dim must be %d (got %lld)", kHeadDim, (long long)head_dim);
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L_valid < 0 || L_valid > L_cap || n_pos <= 0)
+    return set_error("qkv_rope_attention: bad sizes (M=%lld Hq=%lld Hkv=%lld L_valid=%lld L_cap=%lld)",
+                     (long long)M, (long long)Hq, (long long)Hkv, (long long)L_valid, (long long)L_cap);
+  if (M == 0) return 0;
+  if (M > kNewKeysMax) return set_error("qkv_rope_attention: at most %d rows (got %lld)", kNewKeysMax, (long long)M);
+  if (L_cap % 32 != 0 || kv_head_stride < L_cap * kHeadDim)
+    return set_error("qkv_rope_attention: the cache needs L_cap %% 32 == 0 and a head stride of at least L_cap * %d",
+                     kHeadDim);
+  if (L_cap * kHeadDim * 2 > (int64_t)0xFFFFFFF0) return set_error("qkv_rope_attention: L_cap too large");
+  if (!qkv || !cos || !sin || !pos || !k_cache || !v_cache || !out)
+    return set_error("qkv_rope_attention: null pointer");
+  if (sqkv < (Hq + 2 * Hkv) * kHeadDim || sqkv > 0x7fffffff || kv_head_stride > 0x7fffffff)
+    return set_error("qkv_rope_attention: strides out of range");
+  // 16-byte loads of the projection rows, the norm weights and the cos / sin
+  // rows, 16-byte K tile stores
+  if (!al(qkv, 16) || sqkv % 8 || !al(cos, 16) || !al(sin, 16) || scs % 8 || !al(k_cache, 16) ||
+      !al(v_cache, 16) || kv_head_stride % 8 || (q_norm_w && !al(q_norm_w, 16)) || (k_norm_w && !al(k_norm_w, 16)))
+    return set_error("qkv_rope_attention: operands must be 16-byte aligned");
+  if (mask != nullptr && (smask < (L_valid + 3) / 4 * 4 || smask % 4 != 0 || !al(mask, 4)))
+    return set_error("qkv_rope_attention: mask rows must be 4-byte aligned with at least L_valid rounded up to 4 bytes");
+  const AttnPlan pl = attn_plan(M, Hq, Hkv, L_valid);
+  if (!pl.head) return set_error("qkv_rope_attention: %d rows per KV head over %lld slots need the chunked form "
+                                 "(qkv_rope_cache, then block_attention)", pl.rows, (long long)L_valid);
+  if (pl.bytes > 0 && (workspace == nullptr || workspace_bytes < pl.bytes || !al(workspace, 16)))
+    return set_error("qkv_rope_attention: needs a 16-byte aligned workspace of %lld bytes (got %lld)",
+                     (long long)pl.bytes, (long long)workspace_bytes);
+  AttnArgs a{};
+  a.kc = static_cast<const char*>(k_cache); a.vc = static_cast<const char*>(v_cache);
+  a.sh = kv_head_stride; a.L_cap = L_cap;
+  a.mask = mask; a.smask = smask;
+  a.lv_dev = valid_len_dev;
+  a.M = M; a.n_rep = (int)(Hq / Hkv); a.Hkv = (int)Hkv;
+  a.L_valid = L_valid; a.chunk = pl.chunk; a.wave_chunk = pl.wave_chunk; a.n_chunks = pl.n_chunks;
+  a.scale = scale;
+  a.rows = pl.rows; a.rows_pad = pl.rows_pad;
+  a.arrivals = static_cast<unsigned*>(workspace);
+  a.o_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + pl.cnt_bytes);
+  a.ml_part = reinterpret_cast<float2*>(static_cast<char*>(workspace) + pl.cnt_bytes + pl.o_bytes);
+  RopeArgs ra{};
+  ra.qn = static_cast<const char*>(q_norm_w); ra.kn = static_cast<const char*>(k_norm_w); ra.eps = eps;
+  ra.cos = static_cast<const char*>(cos); ra.sin = static_cast<const char*>(sin); ra.scs = scs; ra.n_pos = n_pos;
+  ra.kcw = static_cast<char*>(k_cache); ra.vcw = static_cast<char*>(v_cache);
+  ra.Hq = (int)Hq;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // one more workgroup per KV head than the plain head form when it splits:
+  // the new keys are one more dealt step
+  const dim3 hgrid((unsigned)(pl.split > 1 ? pl.split + 1 : 1), (unsigned)Hkv);
+  const uint32_t head_bytes = (uint32_t)(L_cap * kHeadDim * 2);
+  const char* x = static_cast<const char*>(qkv);
+  char* o = static_cast<char*>(out);
+  auto go = [&](auto dt_tag) {
+    constexpr int DT = decltype(dt_tag)::value;
+    if (pl.rbw == 2)
+      hipLaunchKernelGGL((attn_head_rope_kernel<DT, 2, kHeadW2>), hgrid, dim3(64 * kHeadW2), 0, st, x, a.kc, a.vc,
+                         a.lv_dev, pos, (int)sqkv, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, ra, o, so_m, so_h);
+    else
+      hipLaunchKernelGGL((attn_head_rope_kernel<DT, 1, kHeadW1>), hgrid, dim3(64 * kHeadW1), 0, st, x, a.kc, a.vc,
+                         a.lv_dev, pos, (int)sqkv, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, ra, o, so_m, so_h);
+  };
+  if (dtype == kBF16) go(std::integral_constant<int, kBF16>{});
+  else go(std::integral_constant<int, kF16>{});
+  return check_launch("qkv_rope_attention");
 }
 
 extern "C" int simsd_block_mask(uint8_t* mask, int64_t smask, int64_t n_cols, int64_t ctx_len, int64_t s0,

@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -64,6 +64,9 @@ SIGNATURES = {
     "simsd_block_attention": (_i32, [_vp, _i64, _i64, _vp, _vp, _i64, _i64,
                                      _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,
                                      _f32, _i32, _vp, _i64, _vp]),
+    "simsd_qkv_rope_attention": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _vp,
+                                        _vp, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i64,
+                                        _i64, _i64, _i64, _vp, _i64, _f32, _i32, _vp, _i64, _vp]),
     "simsd_block_mask": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
     "simsd_moe_route_topk": (_i32, [_vp, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _vp, _vp, _vp]),
     "simsd_moe_num_tiles": (_i32, [_i64, _i64]),

@@ -189,6 +189,100 @@ def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weig
     return q
 
 
+def _mask_u8(mask, M: int, L: int, what: str):
+    """The mask as uint8 rows the kernels read 4 bytes at a time (padded copy
+    when the view's layout does not allow it), or None."""
+    if mask is None:
+        return None
+    if mask.ndim != 2 or mask.shape[0] != M or mask.shape[1] < L:
+        raise ValueError(f"{what}: mask must be [{M}, >= {L}]")
+    m8 = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
+    if m8.dtype != torch.uint8:
+        raise TypeError(f"{what}: mask must be bool or uint8")
+    need = (L + 3) // 4 * 4
+    if m8.stride(1) != 1 or m8.stride(0) % 4 or m8.data_ptr() % 4 or m8.shape[1] < need:
+        pad = torch.zeros((M, max(need, (m8.shape[1] + 3) // 4 * 4)), device=m8.device, dtype=torch.uint8)
+        pad[:, :m8.shape[1]].copy_(m8)
+        m8 = pad
+    return m8
+
+
+# rows of a forward that qkv_rope_attention takes in one launch
+FUSED_MAX_ROWS = 16
+
+
+def fused_attention_ok(M: int, n_q_heads: int, n_kv_heads: int, valid_len: int) -> bool:
+    """Whether qkv_rope_attention runs a forward of these sizes (the head form
+    of the attention: at most 32 query rows per KV head over at most
+    ONE_LAUNCH_SLOTS slots, and at most FUSED_MAX_ROWS rows)."""
+    return (0 < M <= FUSED_MAX_ROWS and n_q_heads % n_kv_heads == 0
+            and (n_q_heads // n_kv_heads) * M <= 32 and valid_len <= ONE_LAUNCH_SLOTS)
+
+
+def qkv_rope_attention(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weight, eps: float,
+                       cos: torch.Tensor, sin: torch.Tensor, position_ids: torch.Tensor, cache: BlockKVCache,
+                       layer: int, mask: torch.Tensor | None = None, valid_len: int | None = None,
+                       valid_len_dev: torch.Tensor | None = None, scale: float | None = None) -> torch.Tensor:
+    """``block_attention(qkv_rope_cache(...))`` in one launch, for a forward
+    whose M rows occupy the last M slots of the valid range: row r writes its
+    K/V at slot valid - M + r (valid = the device-side valid length when
+    ``valid_len_dev`` is given, else ``valid_len``), as every forward of the
+    speculative runner does.  Sizes must pass ``fused_attention_ok``.
+
+    qkv: [M, (Hq + 2 Hkv) * 128] merged projection output; the rest as in
+    qkv_rope_cache and block_attention.  -> [M, Hq * 128].
+    """
+    code = _native.DTYPE_CODES.get(qkv.dtype)
+    if code is None or qkv.dtype == torch.float32:
+        raise TypeError(f"qkv_rope_attention: dtype must be bf16 or fp16, got {qkv.dtype}")
+    M = qkv.shape[0]
+    Hkv, D = cache.n_kv_heads, cache.head_dim
+    if qkv.ndim != 2 or qkv.shape[1] != (n_q_heads + 2 * Hkv) * D or n_q_heads % Hkv != 0:
+        raise ValueError(f"qkv_rope_attention: qkv must be [M, ({n_q_heads} + 2*{Hkv}) * {D}]")
+    L = cache.full_len if valid_len is None else int(valid_len)
+    if not 0 <= L <= cache.full_len:
+        raise ValueError(f"qkv_rope_attention: valid_len {L} outside [0, {cache.full_len}]")
+    if not fused_attention_ok(M, n_q_heads, Hkv, L):
+        raise ValueError(f"qkv_rope_attention: {M} rows x {n_q_heads // Hkv} heads per KV head over {L} slots "
+                         "need the two-launch form (qkv_rope_cache, then block_attention)")
+    if qkv.stride(1) != 1 or qkv.stride(0) % 8 or qkv.data_ptr() % 16:
+        qkv = qkv.contiguous()
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != qkv.dtype or t.ndim != 2 or t.shape[1] != D or t.stride(1) != 1:
+            raise ValueError(f"qkv_rope_attention: {name} must be [n_pos, {D}] in {qkv.dtype}")
+    if cos.shape != sin.shape or cos.stride(0) != sin.stride(0):
+        raise ValueError("qkv_rope_attention: cos and sin differ in shape or stride")
+    if position_ids.dtype != torch.int64 or position_ids.shape != (M,) or (M > 1 and position_ids.stride(0) != 1):
+        raise ValueError("qkv_rope_attention: position_ids must be int64 [M] with unit stride")
+    for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if t is not None and (t.dtype != qkv.dtype or t.shape != (D,) or t.stride(0) != 1 or t.data_ptr() % 16):
+            raise ValueError(f"qkv_rope_attention: {name} must be a 16-byte aligned [{D}] vector in {qkv.dtype}")
+    m8 = _mask_u8(mask, M, L, "qkv_rope_attention")
+    if valid_len_dev is not None and (valid_len_dev.dtype != torch.int64 or valid_len_dev.numel() != 1):
+        raise ValueError("qkv_rope_attention: valid_len_dev must be one int64 on the device")
+    kc, vc = cache.k_tiles[layer], cache.v_tiles[layer]
+    dev = _native.require_device(qkv, cos, sin, position_ids, kc, m8, valid_len_dev, q_norm_weight, k_norm_weight)
+    out = torch.empty((M, n_q_heads * D), device=dev, dtype=qkv.dtype)
+    lib = _native.lib()
+    need = lib.simsd_block_attention_workspace_bytes(M, n_q_heads, Hkv, L)
+    if need < 0:
+        _native.check(-1, "qkv_rope_attention")
+    ws = cache.attention_workspace(need, dev)
+    with _native.device_guard(dev):
+        status = lib.simsd_qkv_rope_attention(
+            qkv.data_ptr(), qkv.stride(0),
+            q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+            k_norm_weight.data_ptr() if k_norm_weight is not None else None, float(eps),
+            cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], position_ids.data_ptr(),
+            kc.data_ptr(), vc.data_ptr(), cache.head_stride, cache.full_len,
+            m8.data_ptr() if m8 is not None else None, m8.stride(0) if m8 is not None else 0,
+            out.data_ptr(), out.stride(0), D, M, n_q_heads, Hkv, L,
+            valid_len_dev.data_ptr() if valid_len_dev is not None else None, D,
+            float(D ** -0.5 if scale is None else scale), code, ws.data_ptr(), ws.numel(), _native.stream_of(dev))
+    _native.check(status, "qkv_rope_attention")
+    return out
+
+
 def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torch.Tensor | None = None,
                     valid_len: int | None = None, scale: float | None = None,
                     valid_len_dev: torch.Tensor | None = None) -> torch.Tensor:
@@ -216,18 +310,7 @@ def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torc
         raise ValueError(f"block_attention: valid_len {L} outside [0, {cache.full_len}]")
     if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
         q = q.contiguous()
-    m8 = None
-    if mask is not None:
-        if mask.ndim != 2 or mask.shape[0] != M or mask.shape[1] < L:
-            raise ValueError(f"block_attention: mask must be [{M}, >= {L}]")
-        m8 = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
-        if m8.dtype != torch.uint8:
-            raise TypeError("block_attention: mask must be bool or uint8")
-        need = (L + 3) // 4 * 4      # the kernel reads 4 mask bytes at a time
-        if m8.stride(1) != 1 or m8.stride(0) % 4 or m8.data_ptr() % 4 or m8.shape[1] < need:
-            pad = torch.zeros((M, max(need, (m8.shape[1] + 3) // 4 * 4)), device=m8.device, dtype=torch.uint8)
-            pad[:, :m8.shape[1]].copy_(m8)
-            m8 = pad
+    m8 = _mask_u8(mask, M, L, "block_attention")
     kc, vc = cache.k_tiles[layer], cache.v_tiles[layer]
     if valid_len_dev is not None and (valid_len_dev.dtype != torch.int64 or valid_len_dev.numel() != 1):
         raise ValueError("block_attention: valid_len_dev must be one int64 on the device")

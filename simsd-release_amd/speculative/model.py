@@ -8,6 +8,8 @@ of the real shapes (no checkpoint is available offline).  Each layer runs as
     qkv = rmsnorm + merged q/k/v projection       (thin_rmsnorm_linear)
     q   = q/k norm + RoPE + K/V cache write        (qkv_rope_cache)
     a   = attention over the static cache          (block_attention)
+          (the two in one launch, qkv_rope_attention, for the runner's
+          forwards of up to 16 rows at the end of the valid range)
     h  += o_proj(a)                                (thin_linear_residual)
     g   = rmsnorm + gate/up projection + SiLU.mul  (thin_rmsnorm_linear_silu_mul)
     h  += down_proj(g)                             (thin_linear_residual)
@@ -23,7 +25,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from kernels.attention_fused import BlockKVCache, block_attention, default_inv_freq, qkv_rope_cache, rope_tables
+from kernels.attention_fused import (BlockKVCache, block_attention, default_inv_freq, fused_attention_ok,
+                                     qkv_rope_attention, qkv_rope_cache, rope_tables)
 from kernels.thin_linear_fused import thin_linear_residual, thin_rmsnorm_linear, thin_rmsnorm_linear_silu_mul
 
 
@@ -86,17 +89,30 @@ class SynthModel:
                                          self.cache.full_len + 64, dtype)
 
     @torch.inference_mode()
-    def forward(self, ids, pos, slots, mask, valid_len=None, valid_len_dev=None, head_rows=None, head=True):
+    def forward(self, ids, pos, slots, mask, valid_len=None, valid_len_dev=None, head_rows=None, head=True,
+                rows_at_end=False):
         """ids/pos/slots: int64 [M]; mask [M, >= valid] (bool); returns the
-        logits of ``head_rows`` (a slice; all rows when None) or, with
-        ``head=False``, nothing (the forward only writes the cache)."""
+        logits of ``head_rows`` (a slice or an index tensor; all rows when
+        None) or, with ``head=False``, nothing (the forward only writes the
+        cache).  ``rows_at_end``: the caller guarantees slots[r] = valid - M + r
+        (valid: the device-side valid length when ``valid_len_dev`` is given,
+        else valid_len), which lets small forwards take the fused attention
+        launch."""
         s = self.shape
         I = s.intermediate
+        M = int(ids.shape[0])
+        L_attn = self.cache.full_len if valid_len is None else int(valid_len)
+        fused = rows_at_end and fused_attention_ok(M, s.n_q_heads, s.n_kv_heads, L_attn)
         h = F.embedding(ids, self.embed)
         for li, L in enumerate(self.layers):
             qkv = thin_rmsnorm_linear(h, L.ln1, s.eps, L.wqkv)
-            q = qkv_rope_cache(qkv, s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin, pos, slots, self.cache, li)
-            a = block_attention(q, self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
+            if fused:
+                a = qkv_rope_attention(qkv, s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin, pos, self.cache, li,
+                                       mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
+            else:
+                q = qkv_rope_cache(qkv, s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin, pos, slots, self.cache,
+                                   li)
+                a = block_attention(q, self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
             h = thin_linear_residual(a, L.wo, h)
             g = thin_rmsnorm_linear_silu_mul(h, L.ln2, s.eps, L.wgu[:I], L.wgu[I:])
             h = thin_linear_residual(g, L.wd, h)

@@ -198,12 +198,13 @@ class SpecRunner:
         g.ids[bl:].fill_(self.mask_id)
         self._step_map.fill_(-1)
         for step, n_u in enumerate(self.schedule):
+            # the rows sit at the last slots of the valid range (set_span)
             if step == 0:
                 logits = self.draft.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound,
-                                            valid_len_dev=g.valid, head_rows=slice(bl, 2 * bl))
+                                            valid_len_dev=g.valid, head_rows=slice(bl, 2 * bl), rows_at_end=True)
             else:
                 logits = self.draft.forward(g.ids[bl:], g.pos[bl:], g.slots[bl:], g.mask[bl:],
-                                            valid_len=bound, valid_len_dev=g.valid)
+                                            valid_len=bound, valid_len_dev=g.valid, rows_at_end=True)
             denoise_select(logits, g.ids[bl:], self.mask_id, n_u, step, self._step_map)
         return None
 
@@ -222,13 +223,14 @@ class SpecRunner:
 
     def _verify_body(self, g, key):
         logits = self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=key[1], valid_len_dev=g.valid,
-                                     head_rows=g.head_rows)
+                                     head_rows=g.head_rows, rows_at_end=True)
         self._verify_logits[key] = logits
         ids, _ = softmax_argmax(logits)
         return ids
 
     def _extend_body(self, g, bound):
-        self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid, head=False)
+        self.target.forward(g.ids, g.pos, g.slots, g.mask, valid_len=bound, valid_len_dev=g.valid, head=False,
+                            rows_at_end=True)
         return None
 
     def _extend_graph(self, n_blocks: int):

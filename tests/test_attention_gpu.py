@@ -372,3 +372,114 @@ def test_errors():
     with pytest.raises(ValueError):
         qkv_rope_cache(qkv[:, :-128], 16, qn, kn, 1e-6, cos, sin, torch.zeros(2, dtype=torch.int64, device=DEV),
                        torch.zeros(2, dtype=torch.int64, device=DEV), cache, 0)
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,ctx", [(4, 16, 8, 1020), (8, 16, 8, 500), (4, 16, 8, 100), (8, 32, 8, 700),
+                                          (16, 16, 8, 2000), (1, 16, 8, 3000), (5, 10, 5, 63), (4, 16, 8, 4088),
+                                          (2, 16, 8, 0), (7, 8, 8, 384)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_qkv_rope_attention_vs_oracle(M, Hq, Hkv, ctx, masked):
+    """The fused launch (q/k norm + RoPE + cache write + attention, the rows at
+    the last M slots of the valid range) against the oracle -- the queries and
+    new keys normed and rotated, attention over the context and the new rows
+    -- within the reference's bf16 bound; the cache's new K within one bf16
+    step of the oracle's and its new V exact; every other slot untouched; the
+    same call as the two-launch pair within the bound.  The device-side valid
+    length sits below the host's bound."""
+    from kernels.attention_fused import (BlockKVCache, block_attention, fused_attention_ok, qkv_rope_attention,
+                                         qkv_rope_cache)
+    print(f"qkv_rope_attention M={M} Hq={Hq} Hkv={Hkv} ctx={ctx} masked={masked}", flush=True)
+    valid = ctx + M
+    host_bound = min(4096, valid + 40)
+    assert fused_attention_ok(M, Hq, Hkv, host_bound)
+    qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 8192, seed=M * 5 + ctx)
+    caches = [BlockKVCache(1, Hkv, (valid + 63) // 32 * 32 + 32, 32, DEV) for _ in range(2)]
+    for c in caches:
+        k_ctx, v_ctx = fill_cache(c, 0, ctx, seed=ctx + 7) if ctx else (None, None)
+    before_k, before_v = caches[0].keys(0).clone(), caches[0].values(0).clone()
+    pos = torch.randperm(8192, device=DEV)[:M]
+    slots = torch.arange(ctx, valid, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(13)
+    full = caches[0].full_len
+    mask = torch.zeros(M, full, dtype=torch.bool, device=DEV)
+    mask[:, :ctx] = True
+    mask[:, ctx:valid] = torch.tril(torch.ones(M, M, dtype=torch.bool, device=DEV))
+    if masked:
+        mask[:, :valid] &= torch.rand(M, valid, generator=g, device=DEV) < 0.7
+        mask[:, ctx] = True
+        if M > 2:
+            mask[1] = False                     # a row with nothing visible -> zeros
+    vdev = torch.tensor([valid], dtype=torch.int64, device=DEV)
+    with torch.inference_mode():
+        out = qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, caches[0], 0, mask, valid_len=host_bound,
+                                 valid_len_dev=vdev).view(M, Hq, D)
+        q2 = qkv_rope_cache(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, slots, caches[1], 0)
+        pair = block_attention(q2, caches[1], 0, mask, valid_len=host_bound, valid_len_dev=vdev).view(M, Hq, D)
+        again = qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, caches[0], 0, mask,
+                                   valid_len=host_bound, valid_len_dev=vdev).view(M, Hq, D)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)                           # deterministic, and idempotent on the cache
+    rq, rk, rv = _oracle_qkv(qkv, Hq, Hkv, qn, kn, cos, sin, pos)
+    kc = caches[0].keys(0).float().cpu().numpy()
+    vc = caches[0].values(0).float().cpu().numpy()
+    # the new K: the norm's statistic is summed in another order than the
+    # oracle's (and than qkv_rope_cache's), so a row's scale may round the
+    # other way; RoPE's sum of two rounded terms can cancel, so the bound is
+    # one bf16 step of the row's largest value, not of each value
+    kn_got = kc[:, ctx:valid].transpose(1, 0, 2)
+    assert np.all(np.abs(kn_got - rk) <= 2.0 ** -7 * np.abs(rk).max(axis=-1, keepdims=True))
+    assert (kn_got != rk).mean() < 0.02
+    assert np.array_equal(vc[:, ctx:valid].transpose(1, 0, 2), rv)
+    others = [i for i in range(full) if not ctx <= i < valid]
+    assert torch.equal(caches[0].keys(0)[:, others], before_k[:, others])
+    assert torch.equal(caches[0].values(0)[:, others], before_v[:, others])
+    k_all = kc[:, :valid]
+    v_all = vc[:, :valid]
+    ref = oatt.attention(rq, k_all, v_all, mask[:, :valid].cpu().numpy(), D ** -0.5)
+    got = out.float().cpu().numpy()
+    err = float(np.abs(got - ref).max())
+    assert err <= bound(ref), f"fused: max err {err:.3e} > {bound(ref):.3e}"
+    assert float(np.abs(pair.float().cpu().numpy() - got).max()) <= bound(ref)
+    if masked and M > 2:
+        assert np.all(got[1] == 0)
+
+
+def test_qkv_rope_attention_graph_replays():
+    """Replays of a captured fused launch over a growing device-side valid
+    length (the runner's use) equal eager calls at each length."""
+    from kernels.attention_fused import BlockKVCache, qkv_rope_attention
+    M, Hq, Hkv, base = 4, 16, 8, 900
+    qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 4096, seed=70)
+    cache = BlockKVCache(1, Hkv, 1024, 32, DEV)
+    fill_cache(cache, 0, 1000, seed=71)
+    ref_cache = BlockKVCache(1, Hkv, 1024, 32, DEV)
+    fill_cache(ref_cache, 0, 1000, seed=71)
+    pos = torch.zeros(M, dtype=torch.int64, device=DEV)
+    vdev = torch.zeros(1, dtype=torch.int64, device=DEV)
+    mask = torch.ones(M, cache.full_len, dtype=torch.bool, device=DEV)
+    with torch.inference_mode():
+        def body():
+            return qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, cache, 0, mask, valid_len=1024,
+                                      valid_len_dev=vdev)
+        pos.copy_(torch.arange(base, base + M, device=DEV))
+        vdev.fill_(base + M)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            body()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = body()
+        for step in range(4):
+            start = base + 8 * step
+            pos.copy_(torch.arange(start, start + M, device=DEV))
+            vdev.fill_(start + M)
+            qkv.copy_(rnd(M, (Hq + 2 * Hkv) * D, scale=2.0, seed=80 + step))
+            g.replay()
+            torch.cuda.synchronize()
+            want = qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, ref_cache, 0, mask, valid_len=1024,
+                                      valid_len_dev=vdev)
+            assert torch.equal(out, want), step
+            assert torch.equal(cache.keys(0), ref_cache.keys(0)) and torch.equal(cache.values(0), ref_cache.values(0))
