@@ -647,13 +647,20 @@ SIMSD_DEV void head_finish(HeadShared<RBW, W, MAXS>& sh, const f32x4_t (&acc)[RB
   static_assert(kPer4 >= 1 && ROWS * kHeadDim % (4 * 64 * W) == 0, "whole float4 units per thread");
   const float4* pO = reinterpret_cast<const float4*>(a.o_part + (int64_t)h * S * ROWS * kHeadDim);
   const float2* pML = a.ml_part + (int64_t)h * S * ROWS;
+  // A pass whose units all lie in the padding rows (rows <= 8 of a 16-row
+  // block: the draft's 4 tokens x 2 query heads) loads nothing: the test is
+  // uniform across the workgroup, and every load the merge uses is issued
+  // before the first wait either way.
   float4 v4[kPer4][MAXS];
+  const int units = rows * (kHeadDim / 4);
 #pragma unroll
   for (int i = 0; i < kPer4; ++i) {
     const int e = (int)threadIdx.x + i * 64 * W;   // float4 unit: row e / 32, dims 4 (e % 32) ..
+    if (i == 0 || i * 64 * W < units) {
 #pragma unroll
-    for (int q = 0; q < MAXS; ++q)
-      v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
+      for (int q = 0; q < MAXS; ++q)
+        v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
+    }
   }
   if (threadIdx.x < rows) {
     const int row = threadIdx.x;
