@@ -229,6 +229,7 @@ template <int RBW>
 struct WaveKV {
   rsrc_t rk, rv, rm;
   uint32_t k_off, v_off, m_off[RBW];
+  int c_oob;   // a step slot whose K and V bytes all lie past the descriptors' range
 };
 
 template <int DT, int RBW>
@@ -241,6 +242,7 @@ SIMSD_DEV WaveKV<RBW> wave_kv(const char* kc, const char* vc, int64_t sh, uint32
   w.rm = make_rsrc(a.mask, a.mask != nullptr ? (uint32_t)(a.M * a.smask) : 0u);
   w.k_off = (uint32_t)(g * 256 + r * 16);
   w.v_off = (uint32_t)(r * 64 + g * 16);
+  w.c_oob = (int)(head_bytes / 256u);
 #pragma unroll
   for (int rb = 0; rb < RBW; ++rb) w.m_off[rb] = (uint32_t)(tok[rb] * a.smask + 4 * g);
   return w;
@@ -258,6 +260,16 @@ struct StepBuf {
   u32x4_t vf[kDTiles];
   uint32_t mk[RBW][2];
 };
+
+// The step to prefetch after the one at c: c_next while it starts before
+// c_end, else a slot past the K/V range, whose loads the buffer range check
+// answers with zeros without a memory request (the step is never computed;
+// a cache larger than the valid length would otherwise stream 16 KB of
+// stale slots per wave at the end of its range).  Uniform across the wave.
+template <int RBW>
+SIMSD_DEV int next_step(const WaveKV<RBW>& w, int c_next, int c_end) {
+  return c_next < c_end ? c_next : w.c_oob;
+}
 
 template <int DT, int RBW>
 SIMSD_DEV void attn_load(const AttnArgs& a, const WaveKV<RBW>& w, int c, StepBuf<RBW>& b) {
@@ -413,10 +425,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     const int ce = (int)c_end;
     attn_load<DT, RBW>(a, w, (int)c_begin, bA);
     for (int c = (int)c_begin;; c += 2 * kKeyStep) {
-      attn_load<DT, RBW>(a, w, c + kKeyStep, bB);
+      attn_load<DT, RBW>(a, w, next_step(w, c + kKeyStep, ce), bB);
       attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
       if (c + kKeyStep >= ce) break;
-      attn_load<DT, RBW>(a, w, c + 2 * kKeyStep, bA);
+      attn_load<DT, RBW>(a, w, next_step(w, c + 2 * kKeyStep, ce), bA);
       attn_step<DT, RBW>(a, qf, row_ok, bB, c + kKeyStep, ce, g, m_run, l_run, acc);
       if (c + 2 * kKeyStep >= ce) break;
     }
@@ -768,11 +780,11 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(const char* __restric
   const int kStride = S * W * kKeyStep;
   // past ce the loads read stale slots or zeros: p = 0 and V zeroed
   while (c < ce) {
-    attn_load<DT, RBW>(a, w, c + kStride, bB);
+    attn_load<DT, RBW>(a, w, next_step(w, c + kStride, ce), bB);
     attn_step<DT, RBW>(a, qf, row_ok, bA, c, ce, g, m_run, l_run, acc);
     c += kStride;
     if (c >= ce) break;
-    attn_load<DT, RBW>(a, w, c + kStride, bA);
+    attn_load<DT, RBW>(a, w, next_step(w, c + kStride, ce), bA);
     attn_step<DT, RBW>(a, qf, row_ok, bB, c, ce, g, m_run, l_run, acc);
     c += kStride;
   }
@@ -1102,11 +1114,11 @@ __global__ __launch_bounds__(64 * W) void attn_head_rope_kernel(const char* __re
   // the cached slots [0, s0)
   const int kStride = S * W * kKeyStep;
   while (c < s0) {
-    attn_load<DT, RBW>(a, w, c + kStride, bB);
+    attn_load<DT, RBW>(a, w, next_step(w, c + kStride, s0), bB);
     attn_step<DT, RBW>(a, qf, row_ok, bA, c, s0, g, m_run, l_run, acc);
     c += kStride;
     if (c >= s0) break;
-    attn_load<DT, RBW>(a, w, c + kStride, bA);
+    attn_load<DT, RBW>(a, w, next_step(w, c + kStride, s0), bA);
     attn_step<DT, RBW>(a, qf, row_ok, bB, c, s0, g, m_run, l_run, acc);
     c += kStride;
   }
@@ -1387,7 +1399,7 @@ extern "C" int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, 
   if (L_cap % 32 != 0 || kv_head_stride < L_cap * kHeadDim)
     return set_error("block_attention: the cache needs L_cap %% 32 == 0 and a head stride of at least L_cap * %d",
                      kHeadDim);
-  if (L_cap * kHeadDim * 2 > (int64_t)0xFFFFFFF0) return set_error("block_attention: L_cap too large");
+  if (L_cap * kHeadDim * 2 > (int64_t)0xFFFF0000) return set_error("block_attention: L_cap too large");   // step offsets past it stay below 2^32
   if (!q || !k_cache || !v_cache || !out) return set_error("block_attention: null pointer");
   if (sq_m < 0 || sq_m > 0x7fffffff || sq_h < 0 || sq_h > 0x7fffffff || kv_head_stride > 0x7fffffff)
     return set_error("block_attention: strides must fit 31 bits");   // 32-bit kernel arguments
@@ -1466,7 +1478,7 @@ extern "C" int simsd_qkv_rope_attention(const void* qkv, int64_t sqkv, const voi
   if (L_cap % 32 != 0 || kv_head_stride < L_cap * kHeadDim)
     return set_error("qkv_rope_attention: the cache needs L_cap %% 32 == 0 and a head stride of at least L_cap * %d",
                      kHeadDim);
-  if (L_cap * kHeadDim * 2 > (int64_t)0xFFFFFFF0) return set_error("qkv_rope_attention: L_cap too large");
+  if (L_cap * kHeadDim * 2 > (int64_t)0xFFFF0000) return set_error("qkv_rope_attention: L_cap too large");
   if (!qkv || !cos || !sin || !pos || !k_cache || !v_cache || !out)
     return set_error("qkv_rope_attention: null pointer");
   if (sqkv < (Hq + 2 * Hkv) * kHeadDim || sqkv > 0x7fffffff || kv_head_stride > 0x7fffffff)
