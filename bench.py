@@ -35,6 +35,12 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           RoPE + cache write, then attention over 1024 slots (28 draft layers,
           4 rows, 16/8 heads; 36 target layers, 32 rows, 32/8 heads), against
           the reference's sequence on its GQA-expanded cache.
+  verify36
+          the target's verify forward as the runner issues it: random-init
+          SDAR-8B shape, 36 rows (one committed block folded in + 4 blocks of
+          4 data and 4 mask rows) over a 1024-slot context, lm_head on the 16
+          mask rows; the projections' split-K partials summed by the launches
+          consuming them, against the reduce-first form.
   c5      the end-to-end speculative step: random-init SDAR-1.7B draft and
           SDAR-8B target on one GPU, 512-token prompt, 4-token blocks, 4
           denoise steps, 4 blocks verified per target forward, greedy
@@ -654,6 +660,64 @@ def run_attn(args, torch, dev):
     return out, M
 
 
+# ─────────────────────────────────────────────── the target's verify forward ───
+def run_verify(args, torch, dev):
+    """The SDAR-8B-shape target's verify forward at 36 rows over a 1024-slot
+    context, one HIP graph per form: each projection's split-K partials handed
+    to the launch that consumes them (reduce + q/k norm + RoPE + cache write,
+    reduce + residual + RMSNorm), and the reduce-first form (a reduce launch,
+    then the norm or the prologue).  Block-causal mask over the 36 rows (blocks
+    of 4) after the context; lm_head on 16 of the rows."""
+    from speculative.model import TARGET_8B, SynthModel
+
+    M, ctx = 36, 1024 - 36
+    model = SynthModel(TARGET_8B, dev, seed=12, max_ctx=1024, max_rows=64)
+    full = model.cache.full_len
+    g = torch.Generator(device=dev).manual_seed(5)
+    for lay in range(TARGET_8B.n_layers):
+        model.cache.k_tiles[lay].normal_(generator=g)
+        model.cache.v_tiles[lay].normal_(generator=g)
+    ids = torch.randint(0, TARGET_8B.vocab - 1, (M,), device=dev, generator=g)
+    pos = torch.arange(ctx, ctx + M, device=dev)
+    blk = torch.arange(M, device=dev) // 4
+    mask = torch.zeros(M, full, dtype=torch.bool, device=dev)
+    mask[:, :ctx] = True
+    mask[:, ctx:ctx + M] = blk[None, :] <= blk[:, None]
+    head_rows = torch.arange(4, M, 2, device=dev)[:16]
+
+    def fwd():
+        return model.forward(ids, pos, pos, mask, valid_len=ctx + M, head_rows=head_rows, rows_at_end=True)
+
+    with torch.inference_mode():
+        fwd()
+        torch.cuda.synchronize()
+        us_parts = graph_us_per_call(torch, [fwd], reps=args.steps)
+        model.reduce_first = True
+        fwd()
+        torch.cuda.synchronize()
+        us_first = graph_us_per_call(torch, [fwd], reps=args.steps)
+        model.reduce_first = False
+    sh = TARGET_8B
+    H, D, I = sh.hidden, sh.head_dim, sh.intermediate
+    layer_w = 2 * (H * (sh.n_q_heads + 2 * sh.n_kv_heads) * D + sh.n_q_heads * D * H + 2 * I * H + H * I)
+    wbytes = sh.n_layers * layer_w + 2 * sh.vocab * H
+    ms = us_parts / 1e3
+    gbs = wbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": 1, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights)",
+        "config": {"workload": "target-verify-forward-SDAR8B-36rows-ctx1024", "M": M, "context_slots": ctx + M,
+                   "weight_bytes_per_step": wbytes, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole forward: weight bytes / forward time"},
+        "reduce_first_ms_per_step": round(us_first / 1e3, 4),
+        "partials_speedup": round(us_first / us_parts, 3),
+    }, M
+
+
 # ───────────────────────────────────────────── end-to-end speculative step ───
 def run_c5(args, torch, dev):
     """C5: random-init SDAR-1.7B draft and SDAR-8B target resident on one GPU,
@@ -1020,7 +1084,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="c2",
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
-                             "mlp32", "layer4", "layer16", "layer32", "layer36", "layer48", "head4", "head32", "attn4", "attn32", "c5", "copy"])
+                             "mlp32", "layer4", "layer16", "layer32", "layer36", "layer48", "head4", "head32",
+                             "attn4", "attn32", "verify36", "c5", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
@@ -1045,9 +1110,9 @@ def main():
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)
         return
-    if args.workload.startswith(("mlp", "layer", "head", "attn")):
+    if args.workload.startswith(("mlp", "layer", "head", "attn", "verify")):
         runner = {"mlp": run_mlp, "layer": run_layer, "head": run_head,
-                  "attn": run_attn}[args.workload.rstrip("0123456789")]
+                  "attn": run_attn, "verify": run_verify}[args.workload.rstrip("0123456789")]
         result, _ = runner(args, torch, dev)
         result["device"] = torch.cuda.get_device_name(dev)
         print(json.dumps(result), flush=True)

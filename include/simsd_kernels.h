@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SIMSD_ABI_VERSION 17
+#define SIMSD_ABI_VERSION 18
 
 /* dtype codes */
 #define SIMSD_DTYPE_BF16 0
@@ -243,6 +243,36 @@ int simsd_thin_linear_residual(const void* x, int64_t sxm, int64_t sxk, const vo
                                int64_t M, int64_t N, int64_t K, int dtype, int block_n, int block_k, int split_k,
                                int num_waves, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* The split-K partials of x @ w^T without their reduce launch: part
+ * [split_k][M][N] fp32 (16-byte aligned, part_bytes >= split_k * M * N * 4),
+ * partial s summing k-chunk s of the plan (split_k 1..16, taken as given;
+ * split_k 1 is the whole K in one partial).  For a consumer that sums them in
+ * a launch it makes anyway -- simsd_reduce_residual_rmsnorm,
+ * simsd_reduce_qkv_rope_cache -- so a projection can split K (every
+ * workgroup reading 1/split of the activation rows) at no extra launch: the
+ * reference's split-K GEMV writes the same staging and sums it in its own
+ * launch, kernels/thin_linear_fused.py:139-171, 313-344.  Other arguments as
+ * simsd_thin_linear (no bias). */
+int simsd_thin_linear_partials(const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn, int64_t swk,
+                               void* part, int64_t part_bytes, int64_t M, int64_t N, int64_t K, int dtype,
+                               int block_n, int block_k, int split_k, int num_waves, void* stream);
+
+/* The decoder layer's residual add and the next RMSNorm on a projection's
+ * partials, one launch: for each row m,
+ *   h[m, :]  = dtype(dtype(sum_s part[s, m, :]) + residual[m, :])
+ *   xn[m, :] = dtype(gamma * dtype(h[m, :] * r)),  r = 1 / sqrt(mean(h^2) + eps)
+ * (the partials summed in split order; the stock RMSNorm of
+ * sdar/run_native_tp2.py:42-47 / SDARRMSNorm, modeling_sdar.py:74-92, on the
+ * new residual stream -- `hidden = residual + proj(...)` followed by the next
+ * norm of the decoder layer, modeling_sdar.py:305-366).  Bit-identical to
+ * simsd_thin_linear_residual's reduce followed by simsd_rmsnorm on the same
+ * partials.  bf16 or fp16; N % 8 == 0, N <= 8192; split 1..8; 16-byte
+ * aligned rows (row strides srm, shm, sxn elements).  h may be residual (in
+ * place). */
+int simsd_reduce_residual_rmsnorm(const void* part, int split, int64_t part_bytes, const void* residual,
+                                  int64_t srm, void* h, int64_t shm, const void* gamma, float eps, void* xn,
+                                  int64_t sxn, int64_t M, int64_t N, int dtype, void* stream);
+
 /* ---- logits epilogue: softmax statistics and the unmasking choice -------
  * For logits rows l[m, 0:V] (bf16, fp16 or fp32; row stride slm elements,
  * unit element stride):
@@ -301,6 +331,19 @@ int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q_norm_w, co
                          const int64_t* slots, const int64_t* slots2, void* k_cache, void* v_cache,
                          int64_t kv_head_stride, int64_t L, void* q_out, int64_t sqo_m, int64_t sqo_h, int64_t M,
                          int64_t Hq, int64_t Hkv, int64_t head_dim, int dtype, void* stream);
+
+/* simsd_qkv_rope_cache with the q/k/v projection given as its split-K
+ * partials (part [split][M][(Hq + 2 Hkv) * D] fp32 from
+ * simsd_thin_linear_partials, split 1..8): each value is the partials' sum
+ * in split order rounded to the dtype -- the reduced projection's value --
+ * then as simsd_qkv_rope_cache.  Bit-identical to the reduce followed by
+ * simsd_qkv_rope_cache, in one launch. */
+int simsd_reduce_qkv_rope_cache(const void* part, int split, int64_t part_bytes, const void* q_norm_w,
+                                const void* k_norm_w, float eps, const void* cos, const void* sin, int64_t scs,
+                                int64_t n_pos, const int64_t* pos, const int64_t* slots, const int64_t* slots2,
+                                void* k_cache, void* v_cache, int64_t kv_head_stride, int64_t L, void* q_out,
+                                int64_t sqo_m, int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                int dtype, void* stream);
 
 /* simsd_block_attention: out[m, hq] = softmax(scale * q[m, hq] . K[h]^T over
  * the visible slots) . V[h] with h = hq / (Hq / Hkv) -- the SDPA call of

@@ -97,7 +97,14 @@ struct QkvArgs {
   char* qo;                   // [M, Hq, D]
   int64_t sqo_m, sqo_h;
   int Hq, Hkv;
+  // in place of qkv: the projection's fp32 split-K partials [split][M][N],
+  // N = (Hq + 2 Hkv) * D, summed here in split order and rounded to the dtype
+  const float* part;
+  int split;
+  int64_t part_mn;
 };
+
+constexpr int kQkvMaxSplit = 8;   // partials the cache-write launch sums
 
 // grid (M, head groups of 8): one wave per (token, head); lane l owns dims l
 // and l + 64, the two halves rotate_half pairs.  All of a wave's loads are
@@ -106,7 +113,7 @@ struct QkvArgs {
 // q_embed = dtype(dtype(q * cos) + dtype(rotate_half(q) * sin)).
 // The fields the first loads depend on come as leading scalar arguments,
 // which the build preloads into SGPRs; the rest of QkvArgs is read after.
-template <int DT>
+template <int DT, bool PART>
 __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(const char* __restrict__ qkv, const int64_t* __restrict__ pos,
                                                              const int64_t* __restrict__ slots, const char* qn,
                                                              const char* kn, int sqkv, int Hq, int Hkv, QkvArgs a) {
@@ -122,11 +129,36 @@ __global__ __launch_bounds__(512) void qkv_rope_cache_kernel(const char* __restr
   const bool s1_ok = s1 >= 0 && s1 < a.L;
   const bool s2_ok = s2 >= 0 && s2 < a.L;
   const int d0 = lane, d1 = lane + 64;
-  const char* src = qkv + (m * sqkv + (int64_t)hh * kHeadDim) * ES;
   const bool is_v = hh >= Hq + Hkv;
   const bool is_q = hh < Hq;
   const char* nwt = is_q ? qn : kn;
-  float x0 = load_elem<DT>(src, d0), x1 = load_elem<DT>(src, d1);
+  float x0, x1;
+  if constexpr (PART) {
+    // the partials of this row and head, all loaded before any is summed
+    // (past the split count the loads re-read partial 0 and are dropped); the
+    // sum starts from 0 above one partial, as thin_reduce_kernel's does, so
+    // the rounded values equal the reduced projection's
+    const float* pr = a.part + m * sqkv + (int64_t)hh * kHeadDim;
+    float p0[kQkvMaxSplit], p1[kQkvMaxSplit];
+#pragma unroll
+    for (int s = 0; s < kQkvMaxSplit; ++s) {
+      const float* ps = pr + (s < a.split ? s : 0) * a.part_mn;
+      p0[s] = ps[d0];
+      p1[s] = ps[d1];
+    }
+    float v0 = a.split > 1 ? 0.f + p0[0] : p0[0], v1 = a.split > 1 ? 0.f + p1[0] : p1[0];
+#pragma unroll
+    for (int s = 1; s < kQkvMaxSplit; ++s) {
+      v0 = s < a.split ? v0 + p0[s] : v0;
+      v1 = s < a.split ? v1 + p1[s] : v1;
+    }
+    x0 = round_to<DT>(v0);
+    x1 = round_to<DT>(v1);
+  } else {
+    const char* src = qkv + (m * sqkv + (int64_t)hh * kHeadDim) * ES;
+    x0 = load_elem<DT>(src, d0);
+    x1 = load_elem<DT>(src, d1);
+  }
   float w0 = 1.f, w1 = 1.f, c0 = 0.f, c1 = 0.f, n0 = 0.f, n1 = 0.f;
   if (!is_v) {
     if (nwt != nullptr) {
@@ -1373,10 +1405,54 @@ extern "C" int simsd_qkv_rope_cache(const void* qkv, int64_t sqkv, const void* q
   const int waves = heads < 8 ? heads : 8;
   const dim3 grid((unsigned)M, (unsigned)((heads + waves - 1) / waves));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  auto kern = dtype == kBF16 ? qkv_rope_cache_kernel<kBF16> : qkv_rope_cache_kernel<kF16>;
+  auto kern = dtype == kBF16 ? qkv_rope_cache_kernel<kBF16, false> : qkv_rope_cache_kernel<kF16, false>;
   hipLaunchKernelGGL(kern, grid, dim3(64 * waves), 0, st, a.qkv, a.pos, a.slots, a.qn, a.kn, (int)a.sqkv, a.Hq,
                      a.Hkv, a);
   return check_launch("qkv_rope_cache");
+}
+
+extern "C" int simsd_reduce_qkv_rope_cache(const void* part, int split, int64_t part_bytes, const void* q_norm_w,
+                                           const void* k_norm_w, float eps, const void* cos, const void* sin,
+                                           int64_t scs, int64_t n_pos, const int64_t* pos, const int64_t* slots,
+                                           const int64_t* slots2, void* k_cache, void* v_cache,
+                                           int64_t kv_head_stride, int64_t L, void* q_out, int64_t sqo_m,
+                                           int64_t sqo_h, int64_t M, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                           int dtype, void* stream) {
+  if (dtype != kBF16 && dtype != kF16) return set_error("reduce_qkv_rope_cache: dtype must be bf16 or fp16");
+  if (head_dim != kHeadDim)
+    return set_error("reduce_qkv_rope_cache: head_dim must be %d (got %lld)", kHeadDim, (long long)head_dim);
+  if (M < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || L <= 0 || n_pos <= 0)
+    return set_error("reduce_qkv_rope_cache: bad sizes");
+  if (split < 1 || split > kQkvMaxSplit)
+    return set_error("reduce_qkv_rope_cache: split must be 1..%d (got %d)", kQkvMaxSplit, split);
+  if (L % 32 != 0 || kv_head_stride < L * kHeadDim)
+    return set_error("reduce_qkv_rope_cache: the cache needs L %% 32 == 0 and a head stride of at least L * %d",
+                     kHeadDim);
+  if (M == 0) return 0;
+  if (M > 0x7fffffff) return set_error("reduce_qkv_rope_cache: too many tokens");
+  const int64_t N = (Hq + 2 * Hkv) * kHeadDim;
+  if (part_bytes < (int64_t)split * M * N * 4)
+    return set_error("reduce_qkv_rope_cache: %d partials of %lld x %lld need %lld bytes (got %lld)", split,
+                     (long long)M, (long long)N, (long long)split * M * N * 4, (long long)part_bytes);
+  if (!part || !cos || !sin || !pos || !slots || !k_cache || !v_cache || !q_out)
+    return set_error("reduce_qkv_rope_cache: null pointer");
+  QkvArgs a{};
+  a.qkv = nullptr; a.sqkv = N;
+  a.part = static_cast<const float*>(part); a.split = split; a.part_mn = M * N;
+  a.qn = static_cast<const char*>(q_norm_w); a.kn = static_cast<const char*>(k_norm_w); a.eps = eps;
+  a.cos = static_cast<const char*>(cos); a.sin = static_cast<const char*>(sin); a.scs = scs; a.n_pos = n_pos;
+  a.pos = pos; a.slots = slots; a.slots2 = slots2;
+  a.kc = static_cast<char*>(k_cache); a.vc = static_cast<char*>(v_cache); a.sh = kv_head_stride; a.L = L;
+  a.qo = static_cast<char*>(q_out); a.sqo_m = sqo_m; a.sqo_h = sqo_h;
+  a.Hq = (int)Hq; a.Hkv = (int)Hkv;
+  const int heads = (int)(Hq + 2 * Hkv);
+  const int waves = heads < 8 ? heads : 8;
+  const dim3 grid((unsigned)M, (unsigned)((heads + waves - 1) / waves));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto kern = dtype == kBF16 ? qkv_rope_cache_kernel<kBF16, true> : qkv_rope_cache_kernel<kF16, true>;
+  hipLaunchKernelGGL(kern, grid, dim3(64 * waves), 0, st, a.qkv, a.pos, a.slots, a.qn, a.kn, (int)a.sqkv, a.Hq,
+                     a.Hkv, a);
+  return check_launch("reduce_qkv_rope_cache");
 }
 
 extern "C" int64_t simsd_block_attention_workspace_bytes(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {

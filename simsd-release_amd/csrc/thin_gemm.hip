@@ -17,6 +17,7 @@
 // (SPLIT > 1) writes fp32 partial tiles and a second launch sums them in split
 // order: deterministic, no atomics, no cross-workgroup synchronisation.
 #include <mutex>
+#include <type_traits>
 
 #include "simsd_common.hpp"
 #include "simsd_kernels.h"
@@ -794,6 +795,88 @@ __global__ __launch_bounds__(256) void thin_reduce_kernel(const float* __restric
   store_elem<DT>(y, m * sym + n * syn, v);
 }
 
+// A projection's split-K partials consumed by the residual add and the next
+// RMSNorm, one workgroup per token row: h = dtype(dtype(sum) + res) (the
+// partials summed in split order, the dtype's residual add), written to the
+// residual stream, then xn = dtype(gamma * dtype(h * r)) with
+// r = 1 / sqrt(sum(h^2) / N + eps) -- what thin_reduce_kernel followed by
+// rmsnorm_vec_kernel compute, with the same element orders, so the results
+// are bit-identical, in one launch.  16-bit rows, N % 8 == 0, N <= R * 2048,
+// P >= split partials (loads past split are answered by the range check and
+// dropped by selects, so none waits behind a branch).  res may alias h: each
+// element is read before the same thread writes it.
+constexpr int kReduceNormMaxSplit = 8;   // partials a consuming norm launch sums
+
+template <int DT, int R, int P>
+__global__ __launch_bounds__(256) void reduce_residual_rmsnorm_kernel(
+    const float* __restrict__ part, int split, uint32_t part_split_bytes, const char* res, int64_t srm, char* h,
+    int64_t shm, const char* __restrict__ gamma, float eps, char* __restrict__ xn, int64_t sxn, int64_t N) {
+  constexpr int ES = DTypeInfo<DT>::kSize;
+  __shared__ float wsum[4];
+  const int64_t m = blockIdx.x;
+  const uint32_t Nb = (uint32_t)(N * ES);
+  const rsrc_t rP = make_rsrc(part + m * N, (uint32_t)(split - 1) * part_split_bytes + (uint32_t)(N * 4));
+  const rsrc_t rR = make_rsrc(res + m * srm * ES, Nb);
+  const rsrc_t rG = make_rsrc(gamma, Nb);
+  u32x4_t pv[R][P][2], rv[R], gv[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t e = (uint32_t)(i * 256 + threadIdx.x) * 8;   // first element of this lane's 8
+    const bool ok = e * ES < Nb;
+#pragma unroll
+    for (int s = 0; s < P; ++s) {
+      const uint32_t o = (uint32_t)s * part_split_bytes + e * 4;
+      pv[i][s][0] = buf_load16<kAuxKeep>(rP, ok && s < split ? o : kOob);
+      pv[i][s][1] = buf_load16<kAuxKeep>(rP, ok && s < split ? o + 16 : kOob);
+    }
+    rv[i] = buf_load16<kAuxKeep>(rR, ok ? e * ES : kOob);
+    gv[i] = buf_load16<kAuxKeep>(rG, ok ? e * ES : kOob);
+  }
+  u32x4_t hv[R];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t rw[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {   // elements 2q, 2q + 1
+      float v[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int el = 2 * q + j;
+        const u32x4_t& c0 = pv[i][0][el >> 2];
+        const uint32_t b0 = (el & 3) == 0 ? c0.x : (el & 3) == 1 ? c0.y : (el & 3) == 2 ? c0.z : c0.w;
+        float t = __uint_as_float(b0);
+        if (split > 1) t = 0.f + t;   // thin_reduce_kernel's sum starts from 0
+#pragma unroll
+        for (int s = 1; s < P; ++s) {
+          const u32x4_t& cs = pv[i][s][el >> 2];
+          const uint32_t bs = (el & 3) == 0 ? cs.x : (el & 3) == 1 ? cs.y : (el & 3) == 2 ? cs.z : cs.w;
+          t = s < split ? t + __uint_as_float(bs) : t;
+        }
+        v[j] = round_to<DT>(round_to<DT>(t) + h16_to_f32<DT>(rw[q] >> (16 * j)));
+      }
+      o[q] = f32_to_h16<DT>(v[0]) | (f32_to_h16<DT>(v[1]) << 16);
+    }
+    hv[i] = u32x4_t{o[0], o[1], o[2], o[3]};
+    acc = sumsq8<DT>(hv[i], acc);
+  }
+  const float t = wave_sum(acc);
+  if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = t;
+  __syncthreads();
+  const float r = 1.f / sqrtf((wsum[0] + wsum[1] + wsum[2] + wsum[3]) / (float)N + eps);
+  char* hr = h + m * shm * ES;
+  char* yr = xn + m * sxn * ES;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * 8 * ES;
+    if (off < Nb) {
+      *reinterpret_cast<u32x4_t*>(hr + off) = hv[i];
+      *reinterpret_cast<u32x4_t*>(yr + off) = rms_scale8<DT>(hv[i], gv[i], r);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ host side
 namespace {
 
@@ -806,6 +889,7 @@ struct ThinPlan {
   bool norm;                 // RMSNorm prologue in the GEMV
   int rows, rt, rb, cb, ms, ks, ch, split;
   bool fast;
+  bool part_out;             // fp32 partials to the caller (even at split 1), no reduce launch
   int64_t tiles_n, tiles_m;
   int steps, steps_per_split;
   int64_t part_bytes;
@@ -950,7 +1034,7 @@ void launch_hot(Kern k, const ThinPlan& pl, const ThinArgs& a, hipStream_t strea
 template <int DT, int RT, int RB, int CB, int KS, bool FAST>
 void launch_gemm(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = (RB * CB == 1) ? SIMSD_THIN_U : SIMSD_THIN_U / 2;
-  if (pl.split > 1) launch<true>(thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, true>, pl, args, stream);
+  if (pl.split > 1 || pl.part_out) launch<true>(thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, true>, pl, args, stream);
   else launch<false>(thin_gemm_kernel<DT, RT, RB, CB, KS, U, FAST, false>, pl, args, stream);
 }
 
@@ -990,7 +1074,7 @@ void launch_gemv4_ch(const ThinPlan& pl, const ThinArgs& args, hipStream_t strea
   constexpr int G = RW / 4;
   constexpr int GB = GLU ? (SIMSD_GEMV_GB_ALL ? G / 2 : (G >= 4 ? 2 : 1))
                          : (SIMSD_GEMV_GB_ALL ? G : (RW >= 8 ? 2 : 1));
-  if (pl.split > 1) launch_hot<DT>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>, pl, args, stream);
+  if (pl.split > 1 || pl.part_out) launch_hot<DT>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, true, GLU, NORM>, pl, args, stream);
   else launch_hot<DT>(thin_gemv4_kernel<DT, RW, MS, KS, CH, GB, false, GLU, NORM>, pl, args, stream);
 }
 
@@ -1039,7 +1123,7 @@ void gemv4_rows(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 template <int DT, int RB, int CB, int KS, bool GLU, int OUTR>
 void launch_lds(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = (RB * CB == 1) ? SIMSD_LDS_U : (SIMSD_LDS_U + 1) / 2;
-  if (pl.split > 1) launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU, OUTR>, pl, args, stream);
+  if (pl.split > 1 || pl.part_out) launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, true, GLU, OUTR>, pl, args, stream);
   else launch_hot<DT>(thin_gemm_lds_kernel<DT, RB, CB, KS, U, false, GLU, OUTR>, pl, args, stream);
 }
 
@@ -1066,7 +1150,7 @@ void lds_ks(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
 template <int DT, int RB, int CB, int KS, bool GLU>
 void launch_xs(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
   constexpr int U = SIMSD_XS_U;
-  if (pl.split > 1) launch_hot<DT>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
+  if (pl.split > 1 || pl.part_out) launch_hot<DT>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, true, GLU>, pl, args, stream);
   else launch_hot<DT>(thin_gemm_xs_kernel<DT, RB, CB, KS, U, false, GLU>, pl, args, stream);
 }
 
@@ -1140,7 +1224,7 @@ void dispatch_dt(const ThinPlan& pl, const ThinArgs& args, hipStream_t stream) {
     if (pl.cb == 1) gemm_rows<DT, 1>(pl, args, stream);
     else gemm_rows<DT, 2>(pl, args, stream);
   }
-  if (pl.split > 1) {
+  if (pl.split > 1 && !pl.part_out) {
     const int64_t total = args.M * args.N;
     hipLaunchKernelGGL((thin_reduce_kernel<DT>), dim3((unsigned)cdiv(total, 256)), dim3(256), 0,
                        stream, args.part, pl.split, args.M, args.N, args.bias, args.sb, args.y,
@@ -1538,3 +1622,93 @@ extern "C" int simsd_thin_linear_residual(const void* x, int64_t sxm, int64_t sx
   return run_planned(pl, args, dtype, workspace, workspace_bytes, stream, "thin_linear_residual");
 }
 
+
+extern "C" int simsd_thin_linear_partials(const void* x, int64_t sxm, int64_t sxk, const void* w, int64_t swn,
+                                          int64_t swk, void* part, int64_t part_bytes, int64_t M, int64_t N,
+                                          int64_t K, int dtype, int block_n, int block_k, int split_k,
+                                          int num_waves, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16 && dtype != kF32)
+    return set_error("thin_linear_partials: unsupported dtype code %d", dtype);
+  if (M < 0 || N < 0 || K < 0) return set_error("thin_linear_partials: negative size");
+  if (split_k < 1 || split_k > kMaxSplit)
+    return set_error("thin_linear_partials: split_k must be 1..%d (got %d)", kMaxSplit, split_k);
+  if (M == 0 || N == 0) return 0;
+  if (K == 0) return set_error("thin_linear_partials: K == 0 must be handled by the caller");
+  if (x == nullptr || w == nullptr || part == nullptr) return set_error("thin_linear_partials: null pointer");
+  if (!aligned16(part)) return set_error("thin_linear_partials: partials must be 16-byte aligned");
+  if (K * (int64_t)esize_of(dtype) > ((int64_t)1 << 31) - 64)
+    return set_error("thin_linear_partials: K=%lld too large", (long long)K);
+  if (part_bytes < (int64_t)split_k * M * N * 4)
+    return set_error("thin_linear_partials: %d partials of %lld x %lld need %lld bytes (got %lld)", split_k,
+                     (long long)M, (long long)N, (long long)split_k * M * N * 4, (long long)part_bytes);
+  ThinPlan pl{};
+  if (make_plan(pl, x, sxm, sxk, w, swn, swk, M, N, K, dtype, block_n, block_k, split_k, num_waves) != 0)
+    return -1;
+  if (pl.split != split_k) return set_error("thin_linear_partials: plan split %d != %d", pl.split, split_k);
+  if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535)
+    return set_error("thin_linear_partials: grid too large (N=%lld, M=%lld)", (long long)N, (long long)M);
+  pl.part_out = true;
+  ThinArgs args{};
+  args.x = static_cast<const char*>(x); args.sxm = sxm; args.sxk = sxk;
+  args.w = static_cast<const char*>(w); args.swn = swn; args.swk = swk;
+  args.part = static_cast<float*>(part);
+  args.M = M; args.N = N; args.K = K;
+  args.steps = pl.steps; args.steps_per_split = pl.steps_per_split;
+  switch (dtype) {
+    case kBF16: dispatch_dt<kBF16>(pl, args, stream); break;
+    case kF16: dispatch_dt<kF16>(pl, args, stream); break;
+    default: dispatch_dt<kF32>(pl, args, stream); break;
+  }
+  return check_launch("thin_linear_partials");
+}
+
+extern "C" int simsd_reduce_residual_rmsnorm(const void* part, int split, int64_t part_bytes, const void* residual,
+                                             int64_t srm, void* h, int64_t shm, const void* gamma, float eps,
+                                             void* xn, int64_t sxn, int64_t M, int64_t N, int dtype, void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (dtype != kBF16 && dtype != kF16) return set_error("reduce_residual_rmsnorm: dtype must be bf16 or fp16");
+  if (M < 0 || N < 0) return set_error("reduce_residual_rmsnorm: negative size");
+  if (split < 1 || split > kReduceNormMaxSplit)
+    return set_error("reduce_residual_rmsnorm: split must be 1..%d (got %d)", kReduceNormMaxSplit, split);
+  if (M == 0 || N == 0) return 0;
+  if (N % 8 != 0 || N > 4 * kNormVecChunk)
+    return set_error("reduce_residual_rmsnorm: N=%lld must be a multiple of 8 and at most %d", (long long)N,
+                     4 * kNormVecChunk);
+  if (!part || !residual || !h || !gamma || !xn) return set_error("reduce_residual_rmsnorm: null pointer");
+  const int64_t es = 2;
+  if (!aligned16(part) || !aligned16(residual) || !aligned16(h) || !aligned16(gamma) || !aligned16(xn) ||
+      (srm * es) % 16 != 0 || (shm * es) % 16 != 0 || (sxn * es) % 16 != 0 || srm < N || shm < N || sxn < N)
+    return set_error("reduce_residual_rmsnorm: 16-byte aligned rows of at least N elements required");
+  const int64_t split_bytes = M * N * 4;
+  if ((int64_t)split * split_bytes > part_bytes)
+    return set_error("reduce_residual_rmsnorm: %d partials of %lld x %lld need %lld bytes (got %lld)", split,
+                     (long long)M, (long long)N, (long long)split * split_bytes, (long long)part_bytes);
+  if ((int64_t)split * split_bytes > (int64_t)0xFFFF0000)
+    return set_error("reduce_residual_rmsnorm: partials past 32-bit offsets");
+  const int R = (int)cdiv(N, kNormVecChunk);
+  const float* pp = static_cast<const float*>(part);
+  const char* rc = static_cast<const char*>(residual);
+  char* hc = static_cast<char*>(h);
+  const char* gc = static_cast<const char*>(gamma);
+  char* yc = static_cast<char*>(xn);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)M), dim3(256), 0, stream, pp, split, (uint32_t)split_bytes, rc, srm,
+                       hc, shm, gc, eps, yc, sxn, N);
+  };
+  auto by_p = [&](auto dt, auto r) {
+    constexpr int DT = decltype(dt)::value, RR = decltype(r)::value;
+    if (split == 1) go(reduce_residual_rmsnorm_kernel<DT, RR, 1>);
+    else if (split == 2) go(reduce_residual_rmsnorm_kernel<DT, RR, 2>);
+    else if (split <= 4) go(reduce_residual_rmsnorm_kernel<DT, RR, 4>);
+    else go(reduce_residual_rmsnorm_kernel<DT, RR, 8>);
+  };
+  auto by_r = [&](auto dt) {
+    if (R == 1) by_p(dt, std::integral_constant<int, 1>{});
+    else if (R == 2) by_p(dt, std::integral_constant<int, 2>{});
+    else by_p(dt, std::integral_constant<int, 4>{});
+  };
+  if (dtype == kBF16) by_r(std::integral_constant<int, kBF16>{});
+  else by_r(std::integral_constant<int, kF16>{});
+  return check_launch("reduce_residual_rmsnorm");
+}

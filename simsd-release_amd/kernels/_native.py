@@ -14,7 +14,7 @@ import torch
 
 LIB_NAME = "libsimsd_kernels.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 SCORE_SOFTMAX = 0
@@ -42,6 +42,10 @@ SIGNATURES = {
     "simsd_thin_linear_residual": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                                           _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _vp, _i64, _vp]),
     "simsd_rmsnorm": (_i32, [_vp, _i64, _vp, _f32, _vp, _i64, _i64, _i64, _i32, _vp]),
+    "simsd_thin_linear_partials": (_i32, [_vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+                                          _i32, _i32, _i32, _i32, _i32, _vp]),
+    "simsd_reduce_residual_rmsnorm": (_i32, [_vp, _i32, _i64, _vp, _i64, _vp, _i64, _vp, _f32, _vp, _i64,
+                                             _i64, _i64, _i32, _vp]),
     "simsd_rmsnorm_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _i32, _i32, _i32, _i32]),
     "simsd_rmsnorm_thin_linear": (_i32, [_vp, _i64, _i64, _vp, _f32, _vp, _i64, _i64, _vp, _i64,
                                          _vp, _i64, _i64, _i64, _i64, _i64, _i32,
@@ -60,6 +64,9 @@ SIGNATURES = {
     "simsd_qkv_rope_cache": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
                                     _vp, _vp, _i64, _i64, _vp, _i64, _i64,
                                     _i64, _i64, _i64, _i64, _i32, _vp]),
+    "simsd_reduce_qkv_rope_cache": (_i32, [_vp, _i32, _i64, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
+                                           _vp, _vp, _i64, _i64, _vp, _i64, _i64,
+                                           _i64, _i64, _i64, _i64, _i32, _vp]),
     "simsd_block_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "simsd_block_attention": (_i32, [_vp, _i64, _i64, _vp, _vp, _i64, _i64,
                                      _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64,

@@ -189,6 +189,59 @@ def qkv_rope_cache(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weig
     return q
 
 
+REDUCE_MAX_SPLIT = 8   # partials the cache-write launch sums
+
+
+def reduce_qkv_rope_cache(part: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_weight, eps: float,
+                          cos: torch.Tensor, sin: torch.Tensor, position_ids: torch.Tensor,
+                          slots: torch.Tensor, cache: BlockKVCache, layer: int,
+                          slots2: torch.Tensor | None = None) -> torch.Tensor:
+    """``qkv_rope_cache`` on the merged projection given as its split-K
+    partials (``thin_linear_fused.thin_linear_partials``: fp32
+    [split, M, (Hq + 2 Hkv) * 128]), summed and rounded in the same launch:
+    the reduce of the projection and the prologue's norm, RoPE and cache
+    write in one.  Bit-identical to ``qkv_rope_cache`` of the reduced
+    projection.  The dtype is the cache's.  -> q [M, Hq, 128]."""
+    kc, vc = cache.k_tiles[layer], cache.v_tiles[layer]
+    code = _native.DTYPE_CODES.get(kc.dtype)
+    if code is None or kc.dtype == torch.float32:
+        raise TypeError(f"reduce_qkv_rope_cache: cache dtype must be bf16 or fp16, got {kc.dtype}")
+    Hkv, D = cache.n_kv_heads, cache.head_dim
+    if part.dtype != torch.float32 or part.ndim != 3 or not part.is_contiguous():
+        raise ValueError("reduce_qkv_rope_cache: partials must be contiguous fp32 [split, M, N]")
+    split, M, N = part.shape
+    if not 1 <= split <= REDUCE_MAX_SPLIT:
+        raise ValueError(f"reduce_qkv_rope_cache: split {split} outside 1..{REDUCE_MAX_SPLIT}")
+    if N != (n_q_heads + 2 * Hkv) * D or n_q_heads % Hkv != 0:
+        raise ValueError(f"reduce_qkv_rope_cache: width {N} != ({n_q_heads} + 2*{Hkv}) * {D}")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != kc.dtype or t.ndim != 2 or t.shape[1] != D or t.stride(1) != 1:
+            raise ValueError(f"reduce_qkv_rope_cache: {name} must be [n_pos, {D}] in {kc.dtype}")
+    if cos.shape != sin.shape or cos.stride(0) != sin.stride(0):
+        raise ValueError("reduce_qkv_rope_cache: cos and sin differ in shape or stride")
+    for name, t in (("position_ids", position_ids), ("slots", slots), ("slots2", slots2)):
+        if t is not None and (t.dtype != torch.int64 or t.shape != (M,) or (M > 1 and t.stride(0) != 1)):
+            raise ValueError(f"reduce_qkv_rope_cache: {name} must be int64 [M] with unit stride")
+    for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
+        if t is not None and (t.dtype != kc.dtype or t.shape != (D,) or t.stride(0) != 1):
+            raise ValueError(f"reduce_qkv_rope_cache: {name} must be [{D}] in {kc.dtype}")
+    dev = _native.require_device(part, cos, sin, position_ids, slots, slots2, kc, q_norm_weight, k_norm_weight)
+    q = torch.empty((M, n_q_heads, D), device=dev, dtype=kc.dtype)
+    if M == 0:
+        return q
+    with _native.device_guard(dev):
+        status = _native.lib().simsd_reduce_qkv_rope_cache(
+            part.data_ptr(), split, part.numel() * 4,
+            q_norm_weight.data_ptr() if q_norm_weight is not None else None,
+            k_norm_weight.data_ptr() if k_norm_weight is not None else None, float(eps),
+            cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], position_ids.data_ptr(),
+            slots.data_ptr(), slots2.data_ptr() if slots2 is not None else None,
+            kc.data_ptr(), vc.data_ptr(), cache.head_stride, cache.full_len,
+            q.data_ptr(), q.stride(0), q.stride(1), M, n_q_heads, Hkv, D, code, _native.stream_of(dev))
+    _native.check(status, "reduce_qkv_rope_cache")
+    return q
+
+
 def _mask_u8(mask, M: int, L: int, what: str):
     """The mask as uint8 rows the kernels read 4 bytes at a time (padded copy
     when the view's layout does not allow it), or None."""

@@ -470,6 +470,83 @@ def thin_linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tenso
     return y
 
 
+REDUCE_MAX_SPLIT = 8   # partials the consuming launches sum
+
+
+def thin_linear_partials(x: torch.Tensor, w: torch.Tensor, config=None, num_warps=None) -> torch.Tensor:
+    """The split-K partials of ``x @ w.T`` without their reduce: fp32
+    [split, M, N], partial s the sum over k-chunk s of the plan (the tuned
+    split, at most 8; 1 is one partial over the whole K).  For the launches
+    that sum them while doing work of their own -- ``reduce_residual_rmsnorm``
+    and ``attention_fused.reduce_qkv_rope_cache`` -- so a projection splits
+    K at no extra launch (the reference's split-K staging,
+    kernels/thin_linear_fused.py:139-171, summed by its own launch)."""
+    if torch.is_grad_enabled() and (x.requires_grad or w.requires_grad):
+        raise RuntimeError("thin_linear_partials is a forward-only inference kernel")
+    if x.dtype != w.dtype:
+        raise TypeError(f"dtype mismatch: x={x.dtype} w={w.dtype}")
+    code = _native.DTYPE_CODES.get(x.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {x.dtype} (bf16, fp16 or fp32)")
+    if x.ndim != 2 or w.ndim != 2 or w.shape[1] != x.shape[1]:
+        raise ValueError(f"shapes: x {tuple(x.shape)}, w {tuple(w.shape)}")
+    M, K = x.shape
+    N = w.shape[0]
+    dev = _native.require_device(x, w)
+    block_n, block_k, split_k, waves = _launch_config(M, N, K, x.element_size(), config, num_warps)
+    split_k = max(1, min(split_k, REDUCE_MAX_SPLIT))
+    part = torch.empty((split_k, M, N), device=dev, dtype=torch.float32)
+    if M == 0 or N == 0:
+        return part
+    if K == 0:
+        return part.zero_()
+    with _native.device_guard(dev):
+        status = _native.lib().simsd_thin_linear_partials(
+            x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), w.stride(0), w.stride(1),
+            part.data_ptr(), part.numel() * 4, M, N, K, code, block_n, block_k, split_k, waves,
+            _native.stream_of(dev))
+    _native.check(status, "thin_linear_partials")
+    return part
+
+
+def reduce_residual_rmsnorm(part: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float,
+                            out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The decoder layer's residual add and the next RMSNorm on a projection
+    given as its partials (``thin_linear_partials``), in one launch:
+    ``h = residual + proj`` (the projection's sum rounded to the dtype, then
+    the dtype add) and ``xn = weight * (h * rsqrt(mean(h^2) + eps)).to(dtype)``
+    (the stock RMSNorm), bit-identical to ``thin_linear_residual`` followed by
+    ``thin_rmsnorm``.  ``out`` (the h buffer) may be ``residual`` itself.
+    bf16/fp16, N % 8 == 0, N <= 8192.  -> (h, xn)."""
+    if part.dtype != torch.float32 or part.ndim != 3 or not part.is_contiguous():
+        raise ValueError("reduce_residual_rmsnorm: partials must be contiguous fp32 [split, M, N]")
+    split, M, N = part.shape
+    code = _native.DTYPE_CODES.get(residual.dtype)
+    if code is None or residual.dtype == torch.float32:
+        raise TypeError(f"reduce_residual_rmsnorm: dtype must be bf16 or fp16, got {residual.dtype}")
+    if residual.shape != (M, N) or residual.stride(1) != 1:
+        raise ValueError(f"reduce_residual_rmsnorm: residual must be [{M}, {N}] with unit column stride")
+    if weight.shape != (N,) or weight.dtype != residual.dtype:
+        raise ValueError(f"reduce_residual_rmsnorm: weight must be [{N}] in {residual.dtype}")
+    if not 1 <= split <= REDUCE_MAX_SPLIT:
+        raise ValueError(f"reduce_residual_rmsnorm: split {split} outside 1..{REDUCE_MAX_SPLIT}")
+    dev = _native.require_device(part, residual, weight, out)
+    h = torch.empty((M, N), device=dev, dtype=residual.dtype) if out is None else out
+    if h.shape != (M, N) or h.dtype != residual.dtype or h.stride(1) != 1:
+        raise ValueError(f"reduce_residual_rmsnorm: out must be [{M}, {N}] in {residual.dtype}")
+    xn = torch.empty((M, N), device=dev, dtype=residual.dtype)
+    if M == 0 or N == 0:
+        return h, xn
+    g = weight.contiguous()
+    with _native.device_guard(dev):
+        status = _native.lib().simsd_reduce_residual_rmsnorm(
+            part.data_ptr(), split, part.numel() * 4, residual.data_ptr(), residual.stride(0),
+            h.data_ptr(), h.stride(0), g.data_ptr(), float(eps), xn.data_ptr(), xn.stride(0), M, N, code,
+            _native.stream_of(dev))
+    _native.check(status, "reduce_residual_rmsnorm")
+    return h, xn
+
+
 def _norm_args(x: torch.Tensor, weight: torch.Tensor):
     if weight.ndim != 1 or weight.shape[0] != x.shape[-1]:
         raise ValueError(f"RMSNorm weight must be [{x.shape[-1]}], got {tuple(weight.shape)}")

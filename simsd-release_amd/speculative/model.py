@@ -14,9 +14,23 @@ of the real shapes (no checkpoint is available offline).  Each layer runs as
     g   = rmsnorm + gate/up projection + SiLU.mul  (thin_rmsnorm_linear_silu_mul)
     h  += down_proj(g)                             (thin_linear_residual)
 
-and the head is rmsnorm + lm_head (thin_rmsnorm_linear).  A forward
-takes its rows' token ids, RoPE positions, cache slots and mask rows, all as
-device tensors, so one captured graph serves every step of a growing context.
+and the head is rmsnorm + lm_head (thin_rmsnorm_linear).  Above 8 rows, where
+each norm would be a launch of its own, the projections hand their split-K
+partials to the launch that consumes them instead of reducing them first:
+
+    xn      = rmsnorm(h)                               (first layer only)
+    q       = qkv partials -> reduce + q/k norm + RoPE + cache write
+                                                       (reduce_qkv_rope_cache)
+    a       = attention                                (block_attention)
+    h, xn   = o partials -> reduce + residual + rmsnorm (reduce_residual_rmsnorm)
+    g       = gate/up + SiLU.mul                       (thin_linear_silu_mul)
+    h, xn   = down partials -> reduce + residual + the next layer's (or the
+              final) rmsnorm                           (reduce_residual_rmsnorm)
+
+with the same values as the form above (each reduce sums the same partials
+in the same order), in 8 launches a layer instead of 11.  A forward takes its
+rows' token ids, RoPE positions, cache slots and mask rows, all as device
+tensors, so one captured graph serves every step of a growing context.
 """
 from __future__ import annotations
 
@@ -26,8 +40,10 @@ import torch
 import torch.nn.functional as F
 
 from kernels.attention_fused import (BlockKVCache, block_attention, default_inv_freq, fused_attention_ok,
-                                     qkv_rope_attention, qkv_rope_cache, rope_tables)
-from kernels.thin_linear_fused import thin_linear_residual, thin_rmsnorm_linear, thin_rmsnorm_linear_silu_mul
+                                     qkv_rope_attention, qkv_rope_cache, reduce_qkv_rope_cache, rope_tables)
+from kernels.thin_linear_fused import (reduce_residual_rmsnorm, thin_linear, thin_linear_partials,
+                                       thin_linear_residual, thin_linear_silu_mul, thin_rmsnorm,
+                                       thin_rmsnorm_linear, thin_rmsnorm_linear_silu_mul)
 
 
 @dataclass(frozen=True)
@@ -104,6 +120,8 @@ class SynthModel:
         L_attn = self.cache.full_len if valid_len is None else int(valid_len)
         fused = rows_at_end and fused_attention_ok(M, s.n_q_heads, s.n_kv_heads, L_attn)
         h = F.embedding(ids, self.embed)
+        if self.partials_path(M):
+            return self._forward_partials(h, pos, slots, mask, valid_len, valid_len_dev, head_rows, head, fused)
         for li, L in enumerate(self.layers):
             qkv = thin_rmsnorm_linear(h, L.ln1, s.eps, L.wqkv)
             if fused:
@@ -121,3 +139,32 @@ class SynthModel:
         if head_rows is not None:
             h = h[head_rows]
         return thin_rmsnorm_linear(h, self.lnf, s.eps, self.lm_head)
+
+    def partials_path(self, M: int) -> bool:
+        """Above 8 rows (the norms are launches of their own there) and for
+        16-bit rows the consuming launches can take (hidden % 8 == 0, <= 8192)."""
+        H = self.shape.hidden
+        return M > 8 and self.dtype != torch.float32 and H % 8 == 0 and H <= 8192 and not self.reduce_first
+
+    reduce_first = False   # True: each projection reduced before its consumer at every row count
+
+    def _forward_partials(self, h, pos, slots, mask, valid_len, valid_len_dev, head_rows, head, fused):
+        s = self.shape
+        I = s.intermediate
+        n = len(self.layers)
+        xn = thin_rmsnorm(h, self.layers[0].ln1, s.eps)
+        for li, L in enumerate(self.layers):
+            if fused:
+                a = qkv_rope_attention(thin_linear(xn, L.wqkv), s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin,
+                                       pos, self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
+            else:
+                q = reduce_qkv_rope_cache(thin_linear_partials(xn, L.wqkv), s.n_q_heads, L.qn, L.kn, s.eps,
+                                          self.cos, self.sin, pos, slots, self.cache, li)
+                a = block_attention(q, self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
+            h, xn = reduce_residual_rmsnorm(thin_linear_partials(a, L.wo), h, L.ln2, s.eps, out=h)
+            g = thin_linear_silu_mul(xn, L.wgu[:I], L.wgu[I:])
+            nxt = self.layers[li + 1].ln1 if li + 1 < n else self.lnf
+            h, xn = reduce_residual_rmsnorm(thin_linear_partials(g, L.wd), h, nxt, s.eps, out=h)
+        if not head:
+            return None
+        return thin_linear(xn if head_rows is None else xn[head_rows], self.lm_head)

@@ -14,7 +14,9 @@ mlp, residual add) and SDARMLP (113-119: down(act(gate(x)) * up(x))).
 
 The GPU forward runs the way the runner runs it: a prefix forward writes the
 context's K/V into the cache, then the last rows run as a cached forward that
-reads them.  The oracle runs the whole sequence at once with the
+reads them.  Forwards above 8 rows (every prefix here, and the 36-row case)
+take the form that hands each projection's split-K partials to the launch
+consuming them (speculative/model.py).  The oracle runs the whole sequence at once with the
 block-causal prompt mask (blocks of 4).
 
 Tolerance: max|got - ref| <= 2^-6 * max|ref| + 1e-3 on the logits of the
@@ -105,6 +107,12 @@ CASES = {
     # 248 context slots + 8 rows = 256 slots
     "sdar1p7b_2l": (dict(hidden=2048, n_layers=2, n_q_heads=16, n_kv_heads=8, intermediate=6144, vocab=8192),
                     256, 8),
+    # the same model with 36 cached rows, the folded verify's count: above 8
+    # rows the projections hand their split-K partials to the launches that
+    # consume them (reduce + q/k norm + RoPE + cache write, reduce + residual
+    # + RMSNorm)
+    "sdar1p7b_2l_36rows": (dict(hidden=2048, n_layers=2, n_q_heads=16, n_kv_heads=8, intermediate=6144,
+                                vocab=8192), 256, 36),
 }
 
 
