@@ -472,6 +472,32 @@ def thin_linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tenso
 
 REDUCE_MAX_SPLIT = 8   # partials the consuming launches sum
 
+# Geometries of thin_linear_partials where they differ from TUNED's:
+# (K, N) -> (((M_lo, M_hi), 6-tuple), ...).  The partials pay no reduce
+# launch of their own, so a split along K costs only the consumer's extra
+# partial reads.  Swept on one MI355X over rows x waves x split, each point
+# the partials launch plus its consumer (reduce + residual + RMSNorm, or
+# reduce + q/k norm + RoPE + cache write) in a graph of 36 distinct weights:
+# o_proj at 36 rows 16.6 -> 15.0 us, qkv at 32 rows 18.1 -> 16.5 us.
+PARTIALS_RANGES: dict[tuple[int, int], tuple[tuple[tuple[int, int], tuple[int, int, int, int, int, int]], ...]] = {
+    (4096, 6144): (((9, 48), (64, 24, 256, 2, 2, 2)),),          # merged qkv  14.0 / 16.5 / 18.8 / 19.5 us
+    (4096, 4096): (((9, 16), (64, 16, 256, 2, 2, 2)),            # o_proj      11.1 us (M=16)
+                   ((17, 32), (64, 64, 256, 4, 4, 2)),           #             12.8 us (M=32)
+                   ((33, 40), (64, 32, 256, 4, 2, 2)),           #             15.0 us (M=36)
+                   ((41, 48), (64, 32, 256, 2, 4, 2))),          #             15.7 us (M=48)
+    (12288, 4096): (((9, 16), (64, 32, 256, 4, 2, 2)),           # down_proj   21.9 us (M=16)
+                    ((17, 32), (64, 64, 256, 4, 4, 2)),          #             23.1 us (M=32)
+                    ((33, 48), (64, 32, 256, 4, 2, 2))),         #             26.8 / 28.5 us (M=36 / 48)
+}
+
+
+def _partials_config(M: int, N: int, K: int):
+    """The PARTIALS_RANGES 6-tuple for this call, or None (then TUNED's)."""
+    for (lo, hi), cfg in PARTIALS_RANGES.get((K, N), ()):
+        if lo <= M <= hi:
+            return cfg
+    return None
+
 
 def thin_linear_partials(x: torch.Tensor, w: torch.Tensor, config=None, num_warps=None) -> torch.Tensor:
     """The split-K partials of ``x @ w.T`` without their reduce: fp32
@@ -493,6 +519,10 @@ def thin_linear_partials(x: torch.Tensor, w: torch.Tensor, config=None, num_warp
     M, K = x.shape
     N = w.shape[0]
     dev = _native.require_device(x, w)
+    if config is None and x.element_size() == 2:
+        cfg = _partials_config(M, N, K)
+        if cfg is not None:
+            config, num_warps = cfg[:4], num_warps or cfg[4]
     block_n, block_k, split_k, waves = _launch_config(M, N, K, x.element_size(), config, num_warps)
     split_k = max(1, min(split_k, REDUCE_MAX_SPLIT))
     part = torch.empty((split_k, M, N), device=dev, dtype=torch.float32)

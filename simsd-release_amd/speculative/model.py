@@ -27,8 +27,10 @@ partials to the launch that consumes them instead of reducing them first:
     h, xn   = down partials -> reduce + residual + the next layer's (or the
               final) rmsnorm                           (reduce_residual_rmsnorm)
 
-with the same values as the form above (each reduce sums the same partials
-in the same order), in 8 launches a layer instead of 11.  A forward takes its
+in 8 launches a layer instead of 11.  Each consuming launch sums the partials
+as the reduce launch would, so with the same splits the values are those of
+the form above; the partials' own geometry table (PARTIALS_RANGES) splits some
+projections differently, which changes only the k-chunking of their sums.  A forward takes its
 rows' token ids, RoPE positions, cache slots and mask rows, all as device
 tensors, so one captured graph serves every step of a growing context.
 """

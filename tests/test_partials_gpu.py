@@ -156,14 +156,20 @@ def test_reduce_qkv_rope_cache_equals_reduce_then_prologue(M, split):
     assert float(caches[0].keys(0)[:, 901].abs().max()) == 0.0 and float(caches[0].keys(0)[:, 900].abs().max()) > 0
 
 
+@pytest.mark.parametrize("tuned", [False, True], ids=["same_splits", "partials_table"])
 @pytest.mark.parametrize("case", ["tiny", "sdar1p7b_2l"])
-def test_decoder_partials_path_equals_reduce_first(case):
+def test_decoder_partials_path_equals_reduce_first(case, tuned, monkeypatch):
     """SynthModel's forward above 8 rows, partials handed to their consumers,
-    against the same model reducing every projection first: equal logits and
-    equal K/V caches, for a long prefix forward, the verify's 36 rows through
-    block attention, and 12 rows at the end of the valid range through the
-    one-launch attention."""
+    against the same model reducing every projection first, for a long prefix
+    forward, the verify's 36 rows through block attention, and 12 rows at the
+    end of the valid range through the one-launch attention.  With the
+    reduce-first form's splits (the partials table emptied) logits and K/V
+    caches are equal; with the partials table's own splits (other k-chunk
+    sums) the logits agree within the composed bf16 bound, 2^-6 max + 1e-3."""
+    import kernels.thin_linear_fused as tlf
     from speculative.model import ModelShape, SynthModel
+    if not tuned:
+        monkeypatch.setattr(tlf, "PARTIALS_RANGES", {})
     dims = {"tiny": dict(hidden=256, n_layers=2, n_q_heads=2, n_kv_heads=1, intermediate=512, vocab=1000),
             "sdar1p7b_2l": dict(hidden=2048, n_layers=2, n_q_heads=16, n_kv_heads=8, intermediate=6144,
                                 vocab=8192)}[case]
@@ -188,8 +194,17 @@ def test_decoder_partials_path_equals_reduce_first(case):
         torch.cuda.synchronize()
         outs.append(o)
     assert models[0].partials_path(36) and not models[1].partials_path(36)
+    if not tuned:
+        for a, b in zip(*outs):
+            assert torch.equal(a, b)
+        for lay in range(shape.n_layers):
+            assert torch.equal(models[0].cache.k_tiles[lay], models[1].cache.k_tiles[lay])
+            assert torch.equal(models[0].cache.v_tiles[lay], models[1].cache.v_tiles[lay])
+        return
     for a, b in zip(*outs):
-        assert torch.equal(a, b)
-    for lay in range(shape.n_layers):
-        assert torch.equal(models[0].cache.k_tiles[lay], models[1].cache.k_tiles[lay])
-        assert torch.equal(models[0].cache.v_tiles[lay], models[1].cache.v_tiles[lay])
+        ref = b.float()
+        bound = 2.0 ** -6 * float(ref.abs().max()) + 1e-3
+        assert float((a.float() - ref).abs().max()) <= bound
+        top2 = ref.topk(2, dim=1).values
+        clear = (top2[:, 0] - top2[:, 1]) > 2 * bound
+        assert torch.equal(a.float().argmax(1)[clear], ref.argmax(1)[clear])
