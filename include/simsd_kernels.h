@@ -386,7 +386,10 @@ int simsd_block_attention(const void* q, int64_t sq_m, int64_t sq_h, const void*
  * zero K) and V at their slots, and out.  Only the head form is fused: at
  * most 32 query rows per KV head and L_valid <= 4096 slots, else the call
  * fails (use the two calls).  16-byte aligned qkv rows, norm weights, cos /
- * sin rows and K / V tiles.  Workspace: simsd_block_attention_workspace_bytes
+ * sin rows and K / V tiles.  pos may be NULL: cos / sin then hold the rows'
+ * own tables, row m's at m * scs (n_pos >= M), gathered once by the caller
+ * for all layers of a forward, so the launch loads them without first
+ * loading the positions.  Workspace: simsd_block_attention_workspace_bytes
  * with the same arguments, under the same rules.  Deterministic; the q/k
  * norm's fp32 sum of squares is ordered differently from
  * simsd_qkv_rope_cache's, so outputs may differ from the two calls' in the

@@ -931,7 +931,10 @@ constexpr int kTileStride = kHeadDim + 8;   // padded LDS rows of the q and K ti
 // dealing (steps i < n_old are the cached 32-key steps), so the wave that gets
 // them holds no cached step while the grid has a wave to spare; it writes the
 // new V into the cache and runs the new keys' step from LDS.
-template <int DT, int RBW, int W>
+// GATHERED: cos / sin hold the rows' own tables (row t at t * scs, gathered
+// once per forward by the caller), so no row waits for its position before
+// its cos / sin loads.
+template <int DT, int RBW, int W, bool GATHERED>
 __global__ __launch_bounds__(64 * W) void attn_head_rope_kernel(const char* __restrict__ qkv, const char* __restrict__ kc,
                                                                 const char* __restrict__ vc,
                                                                 const int64_t* __restrict__ lv_dev,
@@ -955,10 +958,11 @@ __global__ __launch_bounds__(64 * W) void attn_head_rope_kernel(const char* __re
   const int sp = (int)blockIdx.x;
   const int h = blockIdx.y;
 
-  // scalar loads of the rows' positions (uniform addresses, in bounds)
+  // the rows' positions: scalar loads (uniform addresses, in bounds), or the
+  // row index into pre-gathered tables
   int64_t pt[kNewKeysMax];
 #pragma unroll
-  for (int t = 0; t < kNewKeysMax; ++t) pt[t] = pos[t < M ? t : 0];
+  for (int t = 0; t < kNewKeysMax; ++t) pt[t] = GATHERED ? t : pos[t < M ? t : 0];
 
   // this lane's tasks: task id = (pass * W + wave) * 4 + lane / 16, dims
   // 8 (lane % 16) ..; ids past the last task re-read task 0 and are dropped
@@ -1555,8 +1559,11 @@ extern "C" int simsd_qkv_rope_attention(const void* qkv, int64_t sqkv, const voi
     return set_error("qkv_rope_attention: the cache needs L_cap %% 32 == 0 and a head stride of at least L_cap * %d",
                      kHeadDim);
   if (L_cap * kHeadDim * 2 > (int64_t)0xFFFF0000) return set_error("qkv_rope_attention: L_cap too large");
-  if (!qkv || !cos || !sin || !pos || !k_cache || !v_cache || !out)
+  if (!qkv || !cos || !sin || !k_cache || !v_cache || !out)
     return set_error("qkv_rope_attention: null pointer");
+  if (pos == nullptr && n_pos < M)
+    return set_error("qkv_rope_attention: without positions, cos / sin must hold the %lld rows' tables",
+                     (long long)M);
   if (sqkv < (Hq + 2 * Hkv) * kHeadDim || sqkv > 0x7fffffff || kv_head_stride > 0x7fffffff)
     return set_error("qkv_rope_attention: strides out of range");
   // 16-byte loads of the projection rows, the norm weights and the cos / sin
@@ -1596,17 +1603,27 @@ extern "C" int simsd_qkv_rope_attention(const void* qkv, int64_t sqkv, const voi
   const uint32_t head_bytes = (uint32_t)(L_cap * kHeadDim * 2);
   const char* x = static_cast<const char*>(qkv);
   char* o = static_cast<char*>(out);
-  auto go = [&](auto dt_tag) {
+  auto go = [&](auto dt_tag, auto g_tag) {
     constexpr int DT = decltype(dt_tag)::value;
+    constexpr bool G = decltype(g_tag)::value;
     if (pl.rbw == 2)
-      hipLaunchKernelGGL((attn_head_rope_kernel<DT, 2, kHeadW2>), hgrid, dim3(64 * kHeadW2), 0, st, x, a.kc, a.vc,
-                         a.lv_dev, pos, (int)sqkv, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, ra, o, so_m, so_h);
+      hipLaunchKernelGGL((attn_head_rope_kernel<DT, 2, kHeadW2, G>), hgrid, dim3(64 * kHeadW2), 0, st, x, a.kc,
+                         a.vc, a.lv_dev, pos, (int)sqkv, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, ra, o, so_m,
+                         so_h);
     else
-      hipLaunchKernelGGL((attn_head_rope_kernel<DT, 1, kHeadW1>), hgrid, dim3(64 * kHeadW1), 0, st, x, a.kc, a.vc,
-                         a.lv_dev, pos, (int)sqkv, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, ra, o, so_m, so_h);
+      hipLaunchKernelGGL((attn_head_rope_kernel<DT, 1, kHeadW1, G>), hgrid, dim3(64 * kHeadW1), 0, st, x, a.kc,
+                         a.vc, a.lv_dev, pos, (int)sqkv, (int)a.sh, head_bytes, (int)a.M, a.n_rep, a, ra, o, so_m,
+                         so_h);
   };
-  if (dtype == kBF16) go(std::integral_constant<int, kBF16>{});
-  else go(std::integral_constant<int, kF16>{});
+  using gathered = std::integral_constant<bool, true>;
+  using by_pos = std::integral_constant<bool, false>;
+  if (dtype == kBF16) {
+    if (pos == nullptr) go(std::integral_constant<int, kBF16>{}, gathered{});
+    else go(std::integral_constant<int, kBF16>{}, by_pos{});
+  } else {
+    if (pos == nullptr) go(std::integral_constant<int, kF16>{}, gathered{});
+    else go(std::integral_constant<int, kF16>{}, by_pos{});
+  }
   return check_launch("qkv_rope_attention");
 }
 

@@ -283,7 +283,10 @@ def qkv_rope_attention(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_
     speculative runner does.  Sizes must pass ``fused_attention_ok``.
 
     qkv: [M, (Hq + 2 Hkv) * 128] merged projection output; the rest as in
-    qkv_rope_cache and block_attention.  -> [M, Hq * 128].
+    qkv_rope_cache and block_attention.  ``position_ids=None``: cos / sin are
+    the rows' own tables (row m at row m, ``gather_rope_rows``), gathered once
+    for all layers of a forward so that no launch waits for the positions
+    before its cos / sin loads.  -> [M, Hq * 128].
     """
     code = _native.DTYPE_CODES.get(qkv.dtype)
     if code is None or qkv.dtype == torch.float32:
@@ -305,7 +308,10 @@ def qkv_rope_attention(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_
             raise ValueError(f"qkv_rope_attention: {name} must be [n_pos, {D}] in {qkv.dtype}")
     if cos.shape != sin.shape or cos.stride(0) != sin.stride(0):
         raise ValueError("qkv_rope_attention: cos and sin differ in shape or stride")
-    if position_ids.dtype != torch.int64 or position_ids.shape != (M,) or (M > 1 and position_ids.stride(0) != 1):
+    if position_ids is None:
+        if cos.shape[0] < M:
+            raise ValueError(f"qkv_rope_attention: without position_ids, cos / sin must hold the {M} rows' tables")
+    elif position_ids.dtype != torch.int64 or position_ids.shape != (M,) or (M > 1 and position_ids.stride(0) != 1):
         raise ValueError("qkv_rope_attention: position_ids must be int64 [M] with unit stride")
     for name, t in (("q_norm_weight", q_norm_weight), ("k_norm_weight", k_norm_weight)):
         if t is not None and (t.dtype != qkv.dtype or t.shape != (D,) or t.stride(0) != 1 or t.data_ptr() % 16):
@@ -326,7 +332,8 @@ def qkv_rope_attention(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_
             qkv.data_ptr(), qkv.stride(0),
             q_norm_weight.data_ptr() if q_norm_weight is not None else None,
             k_norm_weight.data_ptr() if k_norm_weight is not None else None, float(eps),
-            cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0], position_ids.data_ptr(),
+            cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0],
+            position_ids.data_ptr() if position_ids is not None else None,
             kc.data_ptr(), vc.data_ptr(), cache.head_stride, cache.full_len,
             m8.data_ptr() if m8 is not None else None, m8.stride(0) if m8 is not None else 0,
             out.data_ptr(), out.stride(0), D, M, n_q_heads, Hkv, L,
@@ -334,6 +341,27 @@ def qkv_rope_attention(qkv: torch.Tensor, n_q_heads: int, q_norm_weight, k_norm_
             float(D ** -0.5 if scale is None else scale), code, ws.data_ptr(), ws.numel(), _native.stream_of(dev))
     _native.check(status, "qkv_rope_attention")
     return out
+
+
+def gather_rope_rows(cos: torch.Tensor, sin: torch.Tensor, position_ids: torch.Tensor):
+    """The rows' own cos / sin tables, [M, D] each, for
+    ``qkv_rope_attention(..., position_ids=None)``: one gather when ``cos``
+    and ``sin`` are the two halves of an interleaved [n_pos, 2, D] table
+    (``rope_table_pair``), else two.  Positions must lie in [0, n_pos)."""
+    D, es = cos.shape[1], cos.element_size()
+    if cos.stride(0) == sin.stride(0) == 2 * D and sin.data_ptr() == cos.data_ptr() + D * es:
+        pair = torch.as_strided(cos, (cos.shape[0], 2, D), (2 * D, D, 1))
+        g = pair.index_select(0, position_ids)
+        return g[:, 0], g[:, 1]
+    return cos.index_select(0, position_ids), sin.index_select(0, position_ids)
+
+
+def rope_table_pair(cos: torch.Tensor, sin: torch.Tensor):
+    """cos / sin [n_pos, D] stored interleaved ([n_pos, 2, D]) and returned as
+    the two [n_pos, D] views (row stride 2 D), which every call here takes
+    and ``gather_rope_rows`` gathers in one launch."""
+    pair = torch.stack((cos, sin), dim=1)
+    return pair[:, 0], pair[:, 1]
 
 
 def block_attention(q: torch.Tensor, cache: BlockKVCache, layer: int, mask: torch.Tensor | None = None,

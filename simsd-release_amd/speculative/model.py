@@ -42,7 +42,8 @@ import torch
 import torch.nn.functional as F
 
 from kernels.attention_fused import (BlockKVCache, block_attention, default_inv_freq, fused_attention_ok,
-                                     qkv_rope_attention, qkv_rope_cache, reduce_qkv_rope_cache, rope_tables)
+                                     gather_rope_rows, qkv_rope_attention, qkv_rope_cache, reduce_qkv_rope_cache,
+                                     rope_table_pair, rope_tables)
 from kernels.thin_linear_fused import (reduce_residual_rmsnorm, thin_linear, thin_linear_partials,
                                        thin_linear_residual, thin_linear_silu_mul, thin_rmsnorm,
                                        thin_rmsnorm_linear, thin_rmsnorm_linear_silu_mul)
@@ -103,8 +104,9 @@ class SynthModel:
         self.lnf = norm(H)
         self.lm_head = w(shape.vocab, H)
         self.cache = BlockKVCache(shape.n_layers, shape.n_kv_heads, max_ctx, max_rows, self.device, dtype)
-        self.cos, self.sin = rope_tables(default_inv_freq(D, shape.rope_theta, self.device),
-                                         self.cache.full_len + 64, dtype)
+        # interleaved, so a forward gathers its rows' cos / sin in one launch
+        self.cos, self.sin = rope_table_pair(*rope_tables(default_inv_freq(D, shape.rope_theta, self.device),
+                                                          self.cache.full_len + 64, dtype))
 
     @torch.inference_mode()
     def forward(self, ids, pos, slots, mask, valid_len=None, valid_len_dev=None, head_rows=None, head=True,
@@ -122,12 +124,15 @@ class SynthModel:
         L_attn = self.cache.full_len if valid_len is None else int(valid_len)
         fused = rows_at_end and fused_attention_ok(M, s.n_q_heads, s.n_kv_heads, L_attn)
         h = F.embedding(ids, self.embed)
+        # the one-launch attention takes the rows' cos / sin gathered once for
+        # every layer, not positions it would have to load before them
+        rope = gather_rope_rows(self.cos, self.sin, pos) if fused else None
         if self.partials_path(M):
-            return self._forward_partials(h, pos, slots, mask, valid_len, valid_len_dev, head_rows, head, fused)
+            return self._forward_partials(h, pos, slots, mask, valid_len, valid_len_dev, head_rows, head, rope)
         for li, L in enumerate(self.layers):
             qkv = thin_rmsnorm_linear(h, L.ln1, s.eps, L.wqkv)
             if fused:
-                a = qkv_rope_attention(qkv, s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin, pos, self.cache, li,
+                a = qkv_rope_attention(qkv, s.n_q_heads, L.qn, L.kn, s.eps, *rope, None, self.cache, li,
                                        mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
             else:
                 q = qkv_rope_cache(qkv, s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin, pos, slots, self.cache,
@@ -150,15 +155,15 @@ class SynthModel:
 
     reduce_first = False   # True: each projection reduced before its consumer at every row count
 
-    def _forward_partials(self, h, pos, slots, mask, valid_len, valid_len_dev, head_rows, head, fused):
+    def _forward_partials(self, h, pos, slots, mask, valid_len, valid_len_dev, head_rows, head, rope):
         s = self.shape
         I = s.intermediate
         n = len(self.layers)
         xn = thin_rmsnorm(h, self.layers[0].ln1, s.eps)
         for li, L in enumerate(self.layers):
-            if fused:
-                a = qkv_rope_attention(thin_linear(xn, L.wqkv), s.n_q_heads, L.qn, L.kn, s.eps, self.cos, self.sin,
-                                       pos, self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
+            if rope is not None:
+                a = qkv_rope_attention(thin_linear(xn, L.wqkv), s.n_q_heads, L.qn, L.kn, s.eps, *rope, None,
+                                       self.cache, li, mask, valid_len=valid_len, valid_len_dev=valid_len_dev)
             else:
                 q = reduce_qkv_rope_cache(thin_linear_partials(xn, L.wqkv), s.n_q_heads, L.qn, L.kn, s.eps,
                                           self.cos, self.sin, pos, slots, self.cache, li)

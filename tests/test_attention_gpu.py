@@ -483,3 +483,32 @@ def test_qkv_rope_attention_graph_replays():
                                       valid_len_dev=vdev)
             assert torch.equal(out, want), step
             assert torch.equal(cache.keys(0), ref_cache.keys(0)) and torch.equal(cache.values(0), ref_cache.values(0))
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,L_valid", [(4, 16, 8, 1024), (8, 16, 8, 600), (16, 16, 8, 300),
+                                              (8, 32, 8, 2048), (1, 16, 8, 64)])
+def test_qkv_rope_attention_gathered_tables_equal_positions(M, Hq, Hkv, L_valid):
+    """The rows' cos / sin gathered once (position_ids=None, the decoder's
+    forwards) give exactly the output and cache writes of the position form,
+    from separate tables and from the interleaved pair (one gather)."""
+    from kernels.attention_fused import BlockKVCache, gather_rope_rows, qkv_rope_attention, rope_table_pair
+    print(f"gathered rope rows: M={M} Hq={Hq} Hkv={Hkv} L={L_valid}", flush=True)
+    qkv, qn, kn, cos, sin = _qkv_case(M, Hq, Hkv, 4096, seed=90 + M)
+    pos = torch.arange(L_valid - M, L_valid, device=DEV)
+    pos[0] = 7                                               # positions need not follow the slots
+    mask = torch.ones(M, L_valid + 32, dtype=torch.bool, device=DEV)
+    caches = [BlockKVCache(1, Hkv, L_valid, 32, DEV) for _ in range(3)]
+    for c in caches:
+        fill_cache(c, 0, L_valid - M, seed=91)
+    pc, ps = rope_table_pair(cos, sin)
+    with torch.inference_mode():
+        want = qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, cos, sin, pos, caches[0], 0, mask, valid_len=L_valid)
+        got1 = qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, *gather_rope_rows(cos, sin, pos), None, caches[1], 0,
+                                  mask, valid_len=L_valid)
+        rows = gather_rope_rows(pc, ps, pos)
+        got2 = qkv_rope_attention(qkv, Hq, qn, kn, 1e-6, *rows, None, caches[2], 0, mask, valid_len=L_valid)
+    torch.cuda.synchronize()
+    assert rows[0].stride(0) == 2 * D                        # one gather of the interleaved pair
+    for got, c in ((got1, caches[1]), (got2, caches[2])):
+        assert torch.equal(got, want)
+        assert torch.equal(c.k_tiles[0], caches[0].k_tiles[0]) and torch.equal(c.v_tiles[0], caches[0].v_tiles[0])
