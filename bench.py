@@ -565,7 +565,8 @@ def run_attn(args, torch, dev):
     the GQA-expanded cache, SDPA with the bool mask; SDPA pinned to its
     efficient kernel in bf16) on the same data."""
     from kernels.attention_fused import (BlockKVCache, block_attention, default_inv_freq, fused_attention_ok,
-                                         qkv_rope_attention, qkv_rope_cache, rope_tables)
+                                         gather_rope_rows, qkv_rope_attention, qkv_rope_cache, rope_table_pair,
+                                         rope_tables)
     F = torch.nn.functional
     M, Hq, L_layers = (4, 16, 28) if args.workload == "attn4" else (32, 32, 36)
     Hkv, D, ctx, eps = 8, 128, 1024 - M, 1e-6
@@ -590,9 +591,12 @@ def run_attn(args, torch, dev):
 
     one_launch = fused_attention_ok(M, Hq, Hkv, L)   # the rows sit at the last M valid slots
 
+    pc, ps = rope_table_pair(cos, sin)
+
     def fused():
-        if one_launch:
-            return [qkv_rope_attention(x, Hq, qn, kn, eps, cos, sin, pos, cache, lay, mask, valid_len=L)
+        if one_launch:   # as a decoder forward: the rows' cos / sin gathered once for every layer
+            rows = gather_rope_rows(pc, ps, pos)
+            return [qkv_rope_attention(x, Hq, qn, kn, eps, *rows, None, cache, lay, mask, valid_len=L)
                     for lay, x in enumerate(qkvs)]
         return [block_attention(qkv_rope_cache(x, Hq, qn, kn, eps, cos, sin, pos, slots, cache, lay),
                                 cache, lay, mask, valid_len=L) for lay, x in enumerate(qkvs)]
@@ -649,7 +653,8 @@ def run_attn(args, torch, dev):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": ("qkv_rope_attention per layer (attn_head_rope_kernel: norm + RoPE + cache "
-                                "write + attention in one launch)" if one_launch else
+                                "write + attention in one launch; the rows' cos / sin gathered once for the "
+                                "28 layers, counted in the time)" if one_launch else
                                 "qkv_rope_cache + block attention per layer (attn_partial + attn_combine)")},
         "us_per_layer": round(us_fused / L_layers, 3),
         "unfused_us_per_layer": None if us_unfused is None else round(us_unfused / L_layers, 3),
