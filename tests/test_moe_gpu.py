@@ -274,13 +274,17 @@ SYNTH = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "fp16", "fp32"])
-@pytest.mark.parametrize("case", SYNTH, ids=[c[0] for c in SYNTH])
+# The reference's list runs in fp32 and bf16 (build_oracle.py:117); fp16 is
+# added here for every case but large_mag, whose x * 100 drives
+# h = silu(g) * u past fp16's 65504 (the case targets bf16's range).
+_SYNTH_PARAMS = [pytest.param(c, dt, id=f"{dt}-{c[0]}") for c in SYNTH for dt in ("bf16", "fp16", "fp32")
+                 if not (dt == "fp16" and c[6] > 10)]
+
+
+@pytest.mark.parametrize("case,dtype", _SYNTH_PARAMS)
 def test_dispatch_synthetic_vs_oracle(case, dtype):
     from kernels.moe_dispatch_fused import moe_dispatch
     name, T, k, E, H, I, scale, conc = case
-    if dtype == "fp16" and scale > 10:
-        pytest.skip("x * 100 drives h = silu(g) * u past fp16's 65504 (the case targets bf16's range)")
     x, ids, w, wg, wu, wd = _case(T, k, E, H, I, dtype, scale, conc, seed=zlib.crc32(name.encode()) & 0xFFFF)
     with torch.inference_mode():
         got = moe_dispatch(x, ids, w, wg, wu, wd)
