@@ -528,8 +528,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 constexpr int kHeadMaxSlots = SIMSD_HEAD_MAX_SLOTS;
 // valid lengths up to which one workgroup per KV head takes all the steps
 // (16 and 32 rows): below them the hand-over costs more than the split saves
+// (16 rows, measured with the merge reading only the valid rows of exactly S
+// partials: 400 slots 10.15 -> 8.74 us split, 200 slots 8.09 one workgroup
+// against 8.41 split)
 #ifndef SIMSD_HEAD_SPLIT_MIN_SLOTS1
-#define SIMSD_HEAD_SPLIT_MIN_SLOTS1 512
+#define SIMSD_HEAD_SPLIT_MIN_SLOTS1 256
 #endif
 #ifndef SIMSD_HEAD_SPLIT_MIN_SLOTS2
 #define SIMSD_HEAD_SPLIT_MIN_SLOTS2 384
@@ -601,6 +604,111 @@ struct HeadShared {
   float wts[MAXS][ROWS];
   int last;
 };
+
+// The last arriver's merge of the NS partials of KV head h, in workgroup
+// order.  The partial rows and the (max, sum) pairs are all loaded before any
+// is used, so the merge waits for one round trip: plain 16-byte loads, ordered
+// after the writers' stores by the arrival's release and the last arriver's
+// acquire (which also drops this CU's stale cache lines).  A pass whose units
+// all lie in the padding rows (rows <= 8 of a 16-row block: the draft's 4
+// tokens x 2 query heads) loads nothing (a workgroup-uniform test); rows past
+// rows in a pass that does load read the workspace's row padding and are
+// dropped.
+// Workgroups a KV head's `steps` 32-key steps are dealt to (the caller caps
+// it by the grid): one step a wave up to SIMSD_HEAD_SPW_SWITCH steps, then
+// SIMSD_HEAD_SPW_X2 / 2 steps a wave -- past ~900 slots a partial fewer to
+// merge costs less than a wave's second step.
+#ifndef SIMSD_HEAD_SPW_X2
+#define SIMSD_HEAD_SPW_X2 3
+#endif
+#ifndef SIMSD_HEAD_SPW_SWITCH
+#define SIMSD_HEAD_SPW_SWITCH 28
+#endif
+SIMSD_DEV int head_split(int steps, int W) {
+  if (steps <= SIMSD_HEAD_SPW_SWITCH) return (steps + W - 1) / W;
+  const int per = W * SIMSD_HEAD_SPW_X2;   // twice the steps a workgroup takes
+  return (2 * steps + per - 1) / per;
+}
+
+template <int DT, int RBW, int W, int MAXS, int NS>
+SIMSD_DEV void head_merge(HeadShared<RBW, W, MAXS>& sh, const AttnArgs& a, int h, int rows, int M, int n_rep,
+                          char* __restrict__ out, int64_t so_m, int64_t so_h) {
+  static_assert(NS >= 1 && NS <= MAXS, "partials the shared arrays hold");
+  constexpr int ROWS = RBW * 16;
+  constexpr int kPer4 = ROWS * kHeadDim / 4 / (64 * W);
+  static_assert(kPer4 >= 1 && ROWS * kHeadDim % (4 * 64 * W) == 0, "whole float4 units per thread");
+  const float4* pO = reinterpret_cast<const float4*>(a.o_part + (int64_t)h * NS * ROWS * kHeadDim);
+  const float2* pML = a.ml_part + (int64_t)h * NS * ROWS;
+  float4 v4[kPer4][NS];
+  const int units = rows * (kHeadDim / 4);
+#pragma unroll
+  for (int i = 0; i < kPer4; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;   // float4 unit: row e / 32, dims 4 (e % 32) ..
+    if (i == 0 || i * 64 * W < units) {
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+        v4[i][q] = pO[(q * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
+    }
+  }
+  if (threadIdx.x < rows) {
+    const int row = threadIdx.x;
+    float pm[NS], pl[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const float2 ml = pML[q * ROWS + row];
+      pm[q] = ml.x;
+      pl[q] = ml.y;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) mx = fmaxf(mx, pm[q]);
+    float l = 0.f;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const float wt = pm[q] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[q] - mx);
+      sh.wts[q][row] = wt;
+      l += pl[q] * wt;
+    }
+    sh.l[row] = l;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPer4; ++i) {
+    const int e = (int)threadIdx.x + i * 64 * W;
+    const int row = e / (kHeadDim / 4), d = (e % (kHeadDim / 4)) * 4;
+    if (row < rows) {
+      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll
+      for (int q = 0; q < NS; ++q) {
+        const float wt = sh.wts[q][row];
+        o0 += v4[i][q].x * wt;
+        o1 += v4[i][q].y * wt;
+        o2 += v4[i][q].z * wt;
+        o3 += v4[i][q].w * wt;
+      }
+      const float l = sh.l[row];
+      const int ih = row / M;
+      const int64_t m = row % M;
+      char* orow = out + (m * so_m + (int64_t)(h * n_rep + ih) * so_h + d) * DTypeInfo<DT>::kSize;
+      store_elem<DT>(orow, 0, l > 0.f ? o0 / l : 0.f);
+      store_elem<DT>(orow, 1, l > 0.f ? o1 / l : 0.f);
+      store_elem<DT>(orow, 2, l > 0.f ? o2 / l : 0.f);
+      store_elem<DT>(orow, 3, l > 0.f ? o3 / l : 0.f);
+    }
+  }
+}
+
+// head_merge for NS = S, 2 <= S <= MAXS (S is uniform across the workgroup).
+template <int DT, int RBW, int W, int MAXS, int NS = 2>
+SIMSD_DEV void head_merge_n(int S, HeadShared<RBW, W, MAXS>& sh, const AttnArgs& a, int h, int rows, int M,
+                            int n_rep, char* __restrict__ out, int64_t so_m, int64_t so_h) {
+  if constexpr (NS >= MAXS) {
+    head_merge<DT, RBW, W, MAXS, MAXS>(sh, a, h, rows, M, n_rep, out, so_m, so_h);
+  } else {
+    if (S == NS) head_merge<DT, RBW, W, MAXS, NS>(sh, a, h, rows, M, n_rep, out, so_m, so_h);
+    else head_merge_n<DT, RBW, W, MAXS, NS + 1>(S, sh, a, h, rows, M, n_rep, out, so_m, so_h);
+  }
+}
 
 // The head form's tail, shared by both head kernels: the W waves' online
 // softmax states merge in LDS (fixed wave order); S = 1 writes the
@@ -679,77 +787,9 @@ SIMSD_DEV void head_finish(HeadShared<RBW, W, MAXS>& sh, const f32x4_t (&acc)[RB
   if (threadIdx.x == 0) sh.last = arrive_last(a.arrivals + h, (unsigned)S);
   __syncthreads();
   if (!sh.last) return;
-  // this head's partials, workgroup q at [q][row].  The partial rows and the
-  // (max, sum) pairs are all loaded before any is used, so the merge waits
-  // for one round trip: plain 16-byte loads, ordered after the writers'
-  // stores by the arrival's release and the last arriver's acquire (which
-  // also drops this CU's stale cache lines).  Loads are unconditional
-  // (workgroups q >= S re-read the last one's; rows past rows read the
-  // workspace's row padding) so that none waits behind a branch; unused
-  // values are dropped by selects.
-  constexpr int kPer4 = ROWS * kHeadDim / 4 / (64 * W);
-  static_assert(kPer4 >= 1 && ROWS * kHeadDim % (4 * 64 * W) == 0, "whole float4 units per thread");
-  const float4* pO = reinterpret_cast<const float4*>(a.o_part + (int64_t)h * S * ROWS * kHeadDim);
-  const float2* pML = a.ml_part + (int64_t)h * S * ROWS;
-  // A pass whose units all lie in the padding rows (rows <= 8 of a 16-row
-  // block: the draft's 4 tokens x 2 query heads) loads nothing: the test is
-  // uniform across the workgroup, and every load the merge uses is issued
-  // before the first wait either way.
-  float4 v4[kPer4][MAXS];
-  const int units = rows * (kHeadDim / 4);
-#pragma unroll
-  for (int i = 0; i < kPer4; ++i) {
-    const int e = (int)threadIdx.x + i * 64 * W;   // float4 unit: row e / 32, dims 4 (e % 32) ..
-    if (i == 0 || i * 64 * W < units) {
-#pragma unroll
-      for (int q = 0; q < MAXS; ++q)
-        v4[i][q] = pO[((q < S ? q : S - 1) * ROWS + e / (kHeadDim / 4)) * (kHeadDim / 4) + e % (kHeadDim / 4)];
-    }
-  }
-  if (threadIdx.x < rows) {
-    const int row = threadIdx.x;
-    float pm[MAXS], pl[MAXS];
-#pragma unroll
-    for (int q = 0; q < MAXS; ++q) {
-      const float2 ml = pML[(q < S ? q : S - 1) * ROWS + row];
-      pm[q] = q < S ? ml.x : -INFINITY;
-      pl[q] = q < S ? ml.y : 0.f;
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < MAXS; ++q)
-      if (q < S) mx = fmaxf(mx, pm[q]);
-    float l = 0.f;
-#pragma unroll
-    for (int q = 0; q < MAXS; ++q) {
-      const float wt = (q >= S || pm[q] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[q] - mx);
-      sh.wts[q][row] = wt;
-      l += pl[q] * wt;
-    }
-    sh.l[row] = l;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kPer4; ++i) {
-    const int e = (int)threadIdx.x + i * 64 * W;
-    const int row = e / (kHeadDim / 4), d = (e % (kHeadDim / 4)) * 4;
-    if (row < rows) {
-      float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-#pragma unroll
-      for (int q = 0; q < MAXS; ++q) {
-        const float wt = sh.wts[q][row];
-        o0 += q < S ? v4[i][q].x * wt : 0.f;
-        o1 += q < S ? v4[i][q].y * wt : 0.f;
-        o2 += q < S ? v4[i][q].z * wt : 0.f;
-        o3 += q < S ? v4[i][q].w * wt : 0.f;
-      }
-      const float l = sh.l[row];
-      put(row, d, o0, l);
-      put(row, d + 1, o1, l);
-      put(row, d + 2, o2, l);
-      put(row, d + 3, o3, l);
-    }
-  }
+  // the merge, instantiated for the exact partial count (a chain of uniform
+  // tests on S), so no load re-reads a partial past S
+  head_merge_n<DT, RBW, W, MAXS>(S, sh, a, h, rows, M, n_rep, out, so_m, so_h);
   if (threadIdx.x == 0) __hip_atomic_store(a.arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -807,7 +847,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_kernel(const char* __restric
   // a step per wave, at most the grid's; the others have nothing dealt
   const int S = (gridDim.x == 1 || ce <= kSplitMin)
                     ? 1
-                    : min((int)gridDim.x, (ce + W * kKeyStep - 1) / (W * kKeyStep));
+                    : min((int)gridDim.x, head_split(ce / kKeyStep + (ce % kKeyStep != 0), W));
   if (sp >= S) return;
   const int kStride = S * W * kKeyStep;
   // past ce the loads read stale slots or zeros: p = 0 and V zeroed
@@ -1041,7 +1081,7 @@ __global__ __launch_bounds__(64 * W) void attn_head_rope_kernel(const char* __re
   const int n_old = s0 > 0 ? (s0 + kKeyStep - 1) / kKeyStep : 0;
   const int S = (gridDim.x == 1 || ce <= kSplitMin)
                     ? 1
-                    : min((int)gridDim.x, (n_old + 1 + W - 1) / W);
+                    : min((int)gridDim.x, head_split(n_old + 1, W));
   if (sp >= S) return;
   const int new_wg = (n_old / W) % S;
   const bool owner = new_wg == sp && n_old % W == wv;
