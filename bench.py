@@ -34,7 +34,8 @@ Workloads (synthetic data, bf16, random-init weights of the named shapes):
           attention of the block over the static KV cache per layer: q/k norm +
           RoPE + cache write, then attention over 1024 slots (28 draft layers,
           4 rows, 16/8 heads; 36 target layers, 32 rows, 32/8 heads), against
-          the reference's sequence on its GQA-expanded cache.
+          the reference's sequence on its GQA-expanded cache.  --context sets
+          the valid slots (up to 4096) for a sweep over lengths.
   verify36
           the target's verify forward as the runner issues it: random-init
           SDAR-8B shape, 36 rows (one committed block folded in + 4 blocks of
@@ -569,7 +570,9 @@ def run_attn(args, torch, dev):
                                          rope_tables)
     F = torch.nn.functional
     M, Hq, L_layers = (4, 16, 28) if args.workload == "attn4" else (32, 32, 36)
-    Hkv, D, ctx, eps = 8, 128, 1024 - M, 1e-6
+    Hkv, D, ctx, eps = 8, 128, args.context - M, 1e-6
+    if ctx < 1 or args.context > 4096:
+        raise SystemExit(f"bench.py: --context {args.context} must lie in ({M}, 4096]")
     n_rep = Hq // Hkv
     cache = BlockKVCache(L_layers, Hkv, ctx, M, dev)
     g = torch.Generator(device=dev).manual_seed(90)
@@ -1091,6 +1094,8 @@ def main():
                     choices=["c1", "c2", "c3m16", "c3m32", "c4t4", "c4t16", "c4t64", "mlp4", "mlp16",
                              "mlp32", "layer4", "layer16", "layer32", "layer36", "layer48", "head4", "head32",
                              "attn4", "attn32", "verify36", "c5", "copy"])
+    ap.add_argument("--context", type=int, default=1024,
+                    help="attn4 / attn32: valid cache slots once the new rows are written (default 1024)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
