@@ -5,8 +5,9 @@ oracle on the same inputs and against the reference's own torch sequence.
 Every attention form is covered: up to 32 query rows per KV head over at
 most 4096 slots run as one launch -- one workgroup per KV head up to 256 (16
 rows) or 384 (32 rows) valid slots, else several whose partials the last to
-finish merges -- and the rest as chunked partials and a merge launch; a
-device-side valid length below the host's bound trims either form's work.
+finish merges -- and the rest (the verify's 36 tokens x 4 query heads per KV
+head among them) as chunked partials and a merge launch; a device-side valid
+length below the host's bound trims either form's work.
 
 qkv_rope_cache: q rows and every cache slot written equal the oracle within
 one bf16 unit in the last place (the RMSNorm statistic may round either way;
@@ -64,7 +65,9 @@ def fill_cache(cache, layer, L, seed, dtype=torch.bfloat16):
                                                       (8, 32, 8, 4200, 4224), (9, 32, 8, 700, 736),
                                                       (16, 32, 8, 1000, 1024), (24, 32, 8, 3000, 3040),
                                                       (32, 32, 8, 64, 96), (32, 32, 8, 2000, 2048),
-                                                      (33, 32, 8, 900, 928)])
+                                                      (33, 32, 8, 900, 928), (36, 32, 8, 1024, 1056),
+                                                      (36, 32, 8, 300, 352), (12, 16, 8, 2500, 2528),
+                                                      (36, 32, 8, 4200, 4224), (144, 32, 8, 600, 640)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_block_attention_vs_oracle(M, Hq, Hkv, L_valid, L_total, masked):
     from kernels.attention_fused import BlockKVCache, block_attention
@@ -309,7 +312,8 @@ def test_graph_capture_replays(max_cache, n_ctx):
 @pytest.mark.parametrize("M,Hq,Hkv,L_host,L_dev", [(4, 16, 8, 1500, 700), (16, 16, 8, 1100, 333),
                                                    (4, 16, 8, 3000, 2500), (4, 16, 8, 900, 0),
                                                    (4, 16, 8, 1200, 45), (16, 16, 8, 2000, 100),
-                                                   (4, 16, 8, 5000, 4500), (16, 32, 8, 3000, 1000)])
+                                                   (4, 16, 8, 5000, 4500), (16, 32, 8, 3000, 1000),
+                                                   (36, 32, 8, 1200, 500), (36, 32, 8, 1000, 200)])
 def test_valid_len_dev_lowers_the_range(M, Hq, Hkv, L_host, L_dev):
     """A device-side valid length below the host's bound gives the attention
     over [0, L_dev) (rows see nothing when it is 0), on both the one-launch
@@ -334,29 +338,33 @@ def test_valid_len_dev_lowers_the_range(M, Hq, Hkv, L_host, L_dev):
 def test_split_head_counters_stay_zero_across_forms():
     """Calls of every form share the cache's workspace: the split head form's
     arrival counters are back at zero after each call, and each call repeats
-    its first result bit for bit whatever ran before it."""
+    its first result bit for bit whatever ran before it -- the draft's 4
+    tokens x 2 query heads per KV head (head or chunked form) and the verify's
+    36 x 4 (chunked form)."""
     from kernels.attention_fused import BlockKVCache, block_attention
-    M, Hq, Hkv = 4, 16, 8
+    Hkv = 8
     cache = BlockKVCache(1, Hkv, 4992, 32, DEV)
     k, v = fill_cache(cache, 0, 5024, seed=70)
-    q = rnd(M, Hq, D, seed=71)
+    qs = {4: rnd(4, 16, D, seed=71), 36: rnd(36, 32, D, seed=72)}
     first = {}
     with torch.inference_mode():
         for rep in range(3):
-            for L in (5000, 1000, 2000, 200, 1500, 5024):
-                print(f"split counters rep={rep} L={L}", flush=True)
+            for M, L in ((4, 5000), (36, 1000), (4, 1000), (36, 5000), (4, 2000), (36, 200), (4, 200),
+                         (36, 2100), (4, 1500), (4, 5024)):
+                print(f"split counters rep={rep} M={M} L={L}", flush=True)
+                q = qs[M]
                 out = block_attention(q, cache, 0, valid_len=L).clone()
                 torch.cuda.synchronize()
                 counters = cache._attn_ws[:4 * Hkv].view(torch.int32)
                 assert int(counters.abs().sum()) == 0
-                if L not in first:
-                    first[L] = out
+                if (M, L) not in first:
+                    first[M, L] = out
                     ref = oatt.attention(q.float().cpu().numpy(), k[:, :L].float().cpu().numpy(),
                                          v[:, :L].float().cpu().numpy(), None, D ** -0.5)
-                    got = out.view(M, Hq, D).float().cpu().numpy()
+                    got = out.view(M, q.shape[1], D).float().cpu().numpy()
                     assert float(np.abs(got - ref).max()) <= bound(ref)
                 else:
-                    assert torch.equal(out, first[L])
+                    assert torch.equal(out, first[M, L])
 
 
 def test_errors():
