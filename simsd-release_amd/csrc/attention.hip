@@ -617,14 +617,15 @@ struct HeadShared {
 // Workgroups a KV head's `steps` 32-key steps are dealt to (the caller caps
 // it by the grid): one step a wave up to SIMSD_HEAD_SPW_SWITCH steps, then
 // SIMSD_HEAD_SPW_X2 / 2 steps a wave -- past ~900 slots a partial fewer to
-// merge costs less than a wave's second step.
+// merge costs less than a wave's second step.  The host sizes the grid with
+// the same rule from its bound on the valid length.
 #ifndef SIMSD_HEAD_SPW_X2
 #define SIMSD_HEAD_SPW_X2 3
 #endif
 #ifndef SIMSD_HEAD_SPW_SWITCH
 #define SIMSD_HEAD_SPW_SWITCH 28
 #endif
-SIMSD_DEV int head_split(int steps, int W) {
+__host__ __device__ inline int head_split(int steps, int W) {
   if (steps <= SIMSD_HEAD_SPW_SWITCH) return (steps + W - 1) / W;
   const int per = W * SIMSD_HEAD_SPW_X2;   // twice the steps a workgroup takes
   return (2 * steps + per - 1) / per;
@@ -995,8 +996,14 @@ __global__ __launch_bounds__(64 * W) void attn_head_rope_kernel(const char* __re
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int sp = (int)blockIdx.x;
   const int h = blockIdx.y;
+  // role sp of this workgroup: workgroups go to the XCDs round robin by
+  // linear id, so with an 8-wide grid the same role of every KV head -- the
+  // new keys' owner among them -- would share one XCD; there the roles are
+  // rotated by the head (1400 slots: 10.45 -> 10.06 us a layer; other widths
+  // already spread them, and rotating 9 cost 2048 slots 0.2 us)
+  const int sp = (gridDim.x & 7) == 0 ? (int)((blockIdx.x + gridDim.x - (unsigned)h % gridDim.x) % gridDim.x)
+                                      : (int)blockIdx.x;
 
   // the rows' positions: scalar loads (uniform addresses, in bounds), or the
   // row index into pre-gathered tables
@@ -1350,6 +1357,7 @@ struct AttnPlan {
   int rows, rows_pad, rb, rbw, waves, groups, n_chunks;
   bool ksplit, head;
   int split;                  // head form: workgroups per KV head
+  int fsplit;                 // the same for the fused launch (qkv_rope_attention)
   int64_t chunk, wave_chunk;
   int64_t cnt_bytes, o_bytes, ml_bytes, bytes;
 };
@@ -1406,16 +1414,24 @@ AttnPlan attn_plan(int64_t M, int64_t Hq, int64_t Hkv, int64_t L_valid) {
   // head form: the grid holds the workgroups the bound L could use; the
   // kernel takes as many as the device-side length needs
   p.split = 1;
+  p.fsplit = 1;
   if (p.head && L > (p.rbw == 2 ? kHeadSplitMinSlots2 : kHeadSplitMinSlots1)) {
-    const int64_t per_wg = (p.rbw == 2 ? kHeadW2 : kHeadW1) * (int64_t)kKeyStep;
-    p.split = (int)std::min<int64_t>(kHeadMaxSplit, (L + per_wg - 1) / per_wg);
+    const int W = p.rbw == 2 ? kHeadW2 : kHeadW1;
+    const int steps = (int)((L + kKeyStep - 1) / kKeyStep);
+    // the most any valid length up to L asks for: head_split drops where it
+    // switches to 1.5 steps a wave (28 steps: 7 workgroups, 29: 5)
+    auto most = [&](int n) { return std::max(head_split(n, W), head_split(std::min(n, SIMSD_HEAD_SPW_SWITCH), W)); };
+    p.split = std::min(kHeadMaxSplit, most(steps));
+    // the fused launch: its new keys are one more step after the cached ones
+    // (at most the steps of L, plus one)
+    p.fsplit = std::min(kHeadMaxSplit + 1, most(steps + 1));
   }
   // workspace: [arrival counters][o partials][(max, sum) partials]; the
   // counters come first in every form so that a workspace shared between
   // calls keeps them at zero
-  // the head form's partials: split, or split + 1 in the fused launch (its
-  // new keys take one more workgroup), whichever call uses the workspace
-  const int64_t parts = p.head ? (p.split > 1 ? p.split + 1 : 1) : p.n_chunks;
+  // the head form's partials: split, or fsplit in the fused launch (its new
+  // keys may take one more workgroup), whichever call uses the workspace
+  const int64_t parts = p.head ? std::max(p.split, p.fsplit) : p.n_chunks;
   p.cnt_bytes = up256(Hkv * 4);
   p.o_bytes = up256(Hkv * parts * p.rows_pad * kHeadDim * 4);
   p.ml_bytes = up256(Hkv * parts * p.rows_pad * 8);
@@ -1647,9 +1663,8 @@ extern "C" int simsd_qkv_rope_attention(const void* qkv, int64_t sqkv, const voi
   ra.kcw = static_cast<char*>(k_cache); ra.vcw = static_cast<char*>(v_cache);
   ra.Hq = (int)Hq;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // one more workgroup per KV head than the plain head form when it splits:
-  // the new keys are one more dealt step
-  const dim3 hgrid((unsigned)(pl.split > 1 ? pl.split + 1 : 1), (unsigned)Hkv);
+  // the fused grid: the new keys are one more dealt step
+  const dim3 hgrid((unsigned)pl.fsplit, (unsigned)Hkv);
   const uint32_t head_bytes = (uint32_t)(L_cap * kHeadDim * 2);
   const char* x = static_cast<const char*>(qkv);
   char* o = static_cast<char*>(out);

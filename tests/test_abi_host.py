@@ -111,15 +111,19 @@ def test_workspace_sizes():
     assert w >= 2 * (512 * 512 + 64 * 512 + 512 * 2048 + 64 * 2048)
     # attention: one workgroup per KV head needs none (16 rows up to 256
     # slots, 32 rows up to 384); the split head form needs 256 bytes of
-    # arrival counters, then S + 1 partials (the fused launch's new keys take
-    # one more workgroup) of 16 (32) rows x 128 fp32 and their (max, sum) per
-    # KV head, S = min(8, ceil(slots / (4 waves x 32 keys)))
+    # arrival counters, then P partials of 16 (32) rows x 128 fp32 and their
+    # (max, sum) per KV head: the most workgroups any valid length up to the
+    # bound's n = ceil(slots / 32) key steps takes -- one step a wave (4 waves)
+    # up to 28 steps, 1.5 above, at most 8 -- or n + 1 steps' (the fused
+    # launch's new keys), whichever is more
     assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 200) == 0
     assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 256) == 0
     assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 512) == 256 + 8 * 5 * 16 * 128 * 4 + 8 * 5 * 16 * 8
     assert lib.simsd_block_attention_workspace_bytes(16, 16, 8, 384) == 0      # 32 rows
     assert lib.simsd_block_attention_workspace_bytes(16, 16, 8, 768) == 256 + 8 * 7 * 32 * 128 * 4 + 8 * 7 * 32 * 8
-    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 1200) == 256 + 8 * 9 * 16 * 128 * 4 + 8 * 9 * 16 * 8
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 1200) == 256 + 8 * 7 * 16 * 128 * 4 + 8 * 7 * 16 * 8
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 1024) == 256 + 8 * 7 * 16 * 128 * 4 + 8 * 7 * 16 * 8
+    assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 3000) == 256 + 8 * 9 * 16 * 128 * 4 + 8 * 9 * 16 * 8
     # more than 32 rows per KV head, or past 4096 slots: the chunked form
     assert lib.simsd_block_attention_workspace_bytes(36, 32, 8, 1024) > 256
     assert lib.simsd_block_attention_workspace_bytes(4, 16, 8, 5000) > 256
