@@ -384,7 +384,9 @@ def test_errors():
 
 @pytest.mark.parametrize("M,Hq,Hkv,ctx", [(4, 16, 8, 1020), (8, 16, 8, 500), (4, 16, 8, 100), (8, 32, 8, 700),
                                           (16, 16, 8, 2000), (1, 16, 8, 3000), (5, 10, 5, 63), (4, 16, 8, 4088),
-                                          (2, 16, 8, 0), (7, 8, 8, 384)])
+                                          (2, 16, 8, 0), (7, 8, 8, 384),
+                                          # 8-wide grids, whose roles rotate by the KV head
+                                          (4, 16, 8, 1396), (8, 16, 8, 1300), (8, 32, 8, 1400)])
 @pytest.mark.parametrize("masked", [False, True])
 def test_qkv_rope_attention_vs_oracle(M, Hq, Hkv, ctx, masked):
     """The fused launch (q/k norm + RoPE + cache write + attention, the rows at
