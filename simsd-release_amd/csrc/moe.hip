@@ -107,19 +107,12 @@ SIMSD_DEV void block_exclusive_scan2(int a, int b, int& ea, int& eb, int& ta, in
                                      int* s_wa /* [32] */, int* s_wb /* [32] */) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  int ia = a, ib = b;
-  for (int off = 1; off < 64; off <<= 1) {
-    const int ua = __shfl_up(ia, off), ub = __shfl_up(ib, off);
-    if (lane >= off) { ia += ua; ib += ub; }
-  }
+  const int ia = wave_inclusive_sum(a), ib = wave_inclusive_sum(b);
   if (lane == 63) { s_wa[wv] = ia; s_wb[wv] = ib; }
   __syncthreads();
   if (wv == 0) {
-    int xa = lane < nw ? s_wa[lane] : 0, xb = lane < nw ? s_wb[lane] : 0;
-    for (int off = 1; off < 64; off <<= 1) {
-      const int ua = __shfl_up(xa, off), ub = __shfl_up(xb, off);
-      if (lane >= off) { xa += ua; xb += ub; }
-    }
+    const int xa = wave_inclusive_sum(lane < nw ? s_wa[lane] : 0);
+    const int xb = wave_inclusive_sum(lane < nw ? s_wb[lane] : 0);
     if (lane < nw) { s_wa[lane] = xa; s_wb[lane] = xb; }
   }
   __syncthreads();
@@ -260,37 +253,24 @@ __global__ __launch_bounds__(kAlignThreads) void moe_route_align_kernel(
 }
 
 // Route and align for up to 128 picks (T*k <= 128): the tokens are routed
-// as above, then one wave builds every table with no further barrier -- the
-// picks are 2 keys per lane, the histogram and scans live in that wave's LDS
-// (its LDS operations complete in order), ranks among equal experts come
-// from ballots.  The same tables as align_from_keys.
+// as above, then one wave builds the counts, offsets and permutation with no
+// further barrier -- the picks are 2 keys per lane, the histogram and scans
+// live in that wave's LDS (its LDS operations complete in order), ranks among
+// equal experts come from ballots -- and a tile -> expert table, written by
+// each active expert's lane over its own tiles; after one barrier every
+// thread fills padded rows of the slot table from it.  The same tables as
+// align_from_keys.
 constexpr int kSmallAlignSlots = 128;
+// tiles the picks can fill: min(E, M) + ceil(M / 16) for M <= 128
+constexpr int kSmallAlignTiles = kSmallAlignSlots + kSmallAlignSlots / kTile;
 
-template <int PL>
-__global__ __launch_bounds__(kAlignThreads) void moe_route_align_small_kernel(
-    const float* __restrict__ logits, int T, int E, int64_t stride_t, int k, int scoring, int renorm,
-    float scale, int64_t* __restrict__ ids, float* __restrict__ wout, int num_tiles,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets,
-    int32_t* __restrict__ perm, int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
-  __shared__ int key_sh[kSmallAlignSlots];
-  __shared__ int off_sh[SIMSD_MOE_MAX_EXPERTS + 1];   // counts, then offsets
-  __shared__ int pad_sh[SIMSD_MOE_MAX_EXPERTS + 1];   // padded offsets
-  __shared__ int h0_sh[SIMSD_MOE_MAX_EXPERTS];        // counts among slots 0..63
-  __shared__ int perm_sh[kSmallAlignSlots];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  for (int t = wv; t < T; t += kAlignThreads / 64) {
-    int pick;
-    float weight;
-    route_token<PL>(logits + (int64_t)t * stride_t, E, k, scoring, renorm, scale, pick, weight);
-    if (lane < k) {
-      ids[(int64_t)t * k + lane] = (int64_t)pick;
-      wout[(int64_t)t * k + lane] = weight;
-      key_sh[t * k + lane] = pick;
-    }
-  }
-  __syncthreads();
-  if (wv != 0) return;
-  const int M = T * k;
+// Wave 0's part of moe_route_align_small_kernel: counts, offsets, the stable
+// permutation and the tile -> expert table, from the M keys in key_sh.
+SIMSD_DEV void small_align_wave(const int* key_sh, int* off_sh, int* pad_sh, int* h0_sh, int* perm_sh,
+                                int* tile_sh, int M, int E, int n_tab, int32_t* __restrict__ counts,
+                                int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets,
+                                int32_t* __restrict__ perm) {
+  const int lane = threadIdx.x & 63;
   // lane holds slots lane (key a) and 64 + lane (key b); -1 = no slot
   const int ka = lane < M ? key_sh[lane] : -1;
   const int kb = 64 + lane < M ? key_sh[64 + lane] : -1;
@@ -313,14 +293,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_route_align_small_kernel(
     c_sum += c;
     p_sum += (c + kTile - 1) / kTile * kTile;
   }
-  int c_inc = c_sum, p_inc = p_sum;
-  for (int d = 1; d < 64; d <<= 1) {
-    const int uc = __shfl_up(c_inc, d), up = __shfl_up(p_inc, d);
-    if (lane >= d) {
-      c_inc += uc;
-      p_inc += up;
-    }
-  }
+  const int c_inc = wave_inclusive_sum(c_sum), p_inc = wave_inclusive_sum(p_sum);
   int c_run = c_inc - c_sum, p_run = p_inc - p_sum;
   for (int q = 0; q < EPL; ++q) {
     const int e = lane * EPL + q;
@@ -362,15 +335,57 @@ __global__ __launch_bounds__(kAlignThreads) void moe_route_align_small_kernel(
     perm[p] = 64 + lane;
     perm_sh[p] = 64 + lane;
   }
-  // padded slot table and per-tile experts: tile t is expert e's when
-  // pad[e] <= 16 t < pad[e + 1]
-  for (int t = lane; t < num_tiles; t += 64) {
-    const int e = upper_bound_lds(pad_sh + 1, E, t * kTile);
-    tile_expert[t] = e;
-    const int cnt = e < E ? off_sh[e + 1] - off_sh[e] : 0;
-    const int r0 = e < E ? t * kTile - pad_sh[e] : 0;
-    for (int r = 0; r < kTile; ++r)
-      slots[(int64_t)t * kTile + r] = r0 + r < cnt ? perm_sh[off_sh[e] + r0 + r] : -1;
+  // tile t is expert e's when pad[e] <= 16 t < pad[e + 1]: E everywhere,
+  // then each active expert's lane over its own tiles (after the E writes:
+  // one wave's LDS operations complete in order)
+  for (int t = lane; t < n_tab; t += 64) tile_sh[t] = E;
+  for (int q = 0; q < EPL; ++q) {
+    const int e = lane * EPL + q;
+    if (e < E)
+      for (int t = pad_sh[e] / kTile; t < pad_sh[e + 1] / kTile && t < n_tab; ++t) tile_sh[t] = e;
+  }
+}
+
+template <int PL>
+__global__ __launch_bounds__(kAlignThreads) void moe_route_align_small_kernel(
+    const float* __restrict__ logits, int T, int E, int64_t stride_t, int k, int scoring, int renorm,
+    float scale, int64_t* __restrict__ ids, float* __restrict__ wout, int num_tiles,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ pad_offsets,
+    int32_t* __restrict__ perm, int32_t* __restrict__ slots, int32_t* __restrict__ tile_expert) {
+  __shared__ int key_sh[kSmallAlignSlots];
+  __shared__ int off_sh[SIMSD_MOE_MAX_EXPERTS + 1];   // counts, then offsets
+  __shared__ int pad_sh[SIMSD_MOE_MAX_EXPERTS + 1];   // padded offsets
+  __shared__ int h0_sh[SIMSD_MOE_MAX_EXPERTS];        // counts among slots 0..63
+  __shared__ int perm_sh[kSmallAlignSlots];
+  __shared__ int tile_sh[kSmallAlignTiles];           // expert of each tile, E past the last
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  for (int t = wv; t < T; t += kAlignThreads / 64) {
+    int pick;
+    float weight;
+    route_token<PL>(logits + (int64_t)t * stride_t, E, k, scoring, renorm, scale, pick, weight);
+    if (lane < k) {
+      ids[(int64_t)t * k + lane] = (int64_t)pick;
+      wout[(int64_t)t * k + lane] = weight;
+      key_sh[t * k + lane] = pick;
+    }
+  }
+  __syncthreads();
+  const int M = T * k;
+  const int n_tab = min(num_tiles, kSmallAlignTiles);
+  if (wv == 0) small_align_wave(key_sh, off_sh, pad_sh, h0_sh, perm_sh, tile_sh, M, E, n_tab, counts, offsets,
+                                pad_offsets, perm);
+  __syncthreads();
+  // the padded slot table, a row per thread; tiles past the table's are E's
+  for (int q = threadIdx.x; q < num_tiles * kTile; q += kAlignThreads) {
+    const int t = q / kTile, r = q % kTile;
+    const int e = t < n_tab ? tile_sh[t] : E;
+    int slot = -1;
+    if (e < E) {
+      const int rr = t * kTile - pad_sh[e] + r;
+      if (rr < off_sh[e + 1] - off_sh[e]) slot = perm_sh[off_sh[e] + rr];
+    }
+    slots[q] = slot;
+    if (r == 0) tile_expert[t] = e;
   }
 }
 

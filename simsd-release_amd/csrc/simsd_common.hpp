@@ -602,6 +602,21 @@ SIMSD_DEV float wave_sum(float v) {
   return wave_allreduce(v, [](float a, float b) { return a + b; });
 }
 
+// Inclusive prefix sum over the wave's 64 lanes, in DPP moves (no LDS
+// permutes): shifts by 1, 2, 4 and 8 within each 16-lane row, then the
+// totals of rows 0 and 2 added to rows 1 and 3 (row_bcast:15) and the running
+// total of rows 0-1 to rows 2 and 3 (row_bcast:31).  Lanes outside a move's
+// source or row mask add 0.
+SIMSD_DEV int wave_inclusive_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);   // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);   // row_bcast:31, rows 2 and 3
+  return v;
+}
+
 // Largest 64-bit key over the wave, on every lane.  Route keys are
 // (order-preserving bits of the logit) << 32 | ~index, so the maximum is the
 // largest logit and, among equal logits, the lowest index; 0 marks an entry
