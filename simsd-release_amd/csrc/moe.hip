@@ -123,15 +123,8 @@ SIMSD_DEV void block_exclusive_scan2(int a, int b, int& ea, int& eb, int& ta, in
   tb = s_wb[nw - 1];
 }
 
-// first e in [0, n) with arr[e] > val, or n
-SIMSD_DEV int upper_bound_lds(const int* arr, int n, int val) {
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (arr[mid] > val) hi = mid; else lo = mid + 1;
-  }
-  return lo;
-}
+// tiles the picks can fill: min(E, M) + ceil(M / 16)
+constexpr int kAlignMaxTiles = SIMSD_MOE_MAX_EXPERTS + SIMSD_MOE_MAX_SLOTS / kTile;
 
 // LDS of the align step (one workgroup).
 struct AlignLds {
@@ -140,6 +133,7 @@ struct AlignLds {
   int off[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of counts
   int pad[SIMSD_MOE_MAX_EXPERTS + 1];   // exclusive scan of padded counts
   int perm[SIMSD_MOE_MAX_SLOTS];
+  int tile[kAlignMaxTiles];             // expert of each tile, E past the last
   int wa[32], wb[32];
 };
 
@@ -150,7 +144,9 @@ SIMSD_DEV void align_from_keys(AlignLds& sm, int M, int E, int num_tiles, int32_
                                int32_t* __restrict__ perm, int32_t* __restrict__ slots,
                                int32_t* __restrict__ tile_expert) {
   const int tid = threadIdx.x;
+  const int n_tab = min(num_tiles, kAlignMaxTiles);
   for (int e = tid; e <= E; e += kAlignThreads) sm.pos[e] = 0;
+  for (int t = tid; t < n_tab; t += kAlignThreads) sm.tile[t] = E;
   __syncthreads();
   // 1. histogram; bucket E collects ids outside [0, E) (kept out of every group)
   for (int i = tid; i < M; i += kAlignThreads) atomicAdd(&sm.pos[sm.key[i]], 1);
@@ -166,6 +162,8 @@ SIMSD_DEV void align_from_keys(AlignLds& sm, int M, int E, int num_tiles, int32_
     counts[tid] = c;
     offsets[tid] = ec;
     pad_offsets[tid] = epc;
+    // tile t is expert e's when pad[e] <= 16 t < pad[e + 1]
+    for (int t = epc / kTile; t < (epc + pc) / kTile && t < n_tab; ++t) sm.tile[t] = tid;
   }
   if (tid == 0) {
     sm.off[E] = tc;
@@ -199,20 +197,21 @@ SIMSD_DEV void align_from_keys(AlignLds& sm, int M, int E, int num_tiles, int32_
     }
   }
   __syncthreads();
-  // 4. outputs
+  // 4. outputs: the padded slot table a row per thread from the tile table
+  // (tiles past it are E's)
   for (int p = tid; p < M; p += kAlignThreads) perm[p] = sm.perm[p];
   const int total_rows = num_tiles * kTile;
   for (int q = tid; q < total_rows; q += kAlignThreads) {
-    const int e = upper_bound_lds(sm.pad + 1, E, q);
+    const int t = q / kTile;
+    const int e = t < n_tab ? sm.tile[t] : E;
     int slot = -1;
     if (e < E) {
       const int r = q - sm.pad[e];
       if (r < sm.off[e + 1] - sm.off[e]) slot = sm.perm[sm.off[e] + r];
     }
     slots[q] = slot;
+    if (q % kTile == 0) tile_expert[t] = e;
   }
-  for (int t = tid; t < num_tiles; t += kAlignThreads)
-    tile_expert[t] = upper_bound_lds(sm.pad + 1, E, t * kTile);
 }
 
 __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(
