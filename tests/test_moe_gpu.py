@@ -139,6 +139,23 @@ def test_route_align_fused_equals_two_calls(scoring, renorm, scale):
         _check_align(al2, omoe.align(ids_ref, E))
 
 
+def test_align_more_tiles_than_the_picks_fill():
+    """A tile count above the default (a table sized for a larger bound):
+    every tile past the filled ones is empty (expert E, rows -1), in both the
+    one-launch route + align (up to 128 picks, and past the 136 tiles its
+    table holds) and the general align (past its 1536)."""
+    from kernels.moe_dispatch_fused import _num_tiles, moe_align, moe_route_align
+    g = torch.Generator(device=DEV).manual_seed(23)
+    for T, E, k, extra in [(4, 256, 8, 20), (4, 256, 8, 300), (16, 256, 8, 64), (64, 256, 8, 40),
+                           (1024, 256, 8, 1500)]:
+        logits = torch.randn(T, E, device=DEV, generator=g)
+        nt = _num_tiles(T * k, E) + extra
+        ids, _, al = moe_route_align(logits, k, num_tiles=nt)
+        ref = omoe.align(ids.cpu().numpy(), E, nt)
+        _check_align(al, ref)
+        _check_align(moe_align(ids, E, nt), ref)
+
+
 def test_align_max_slots():
     from kernels.moe_dispatch_fused import moe_align
     rng = np.random.default_rng(12)
