@@ -605,15 +605,6 @@ struct HeadShared {
   int last;
 };
 
-// The last arriver's merge of the NS partials of KV head h, in workgroup
-// order.  The partial rows and the (max, sum) pairs are all loaded before any
-// is used, so the merge waits for one round trip: plain 16-byte loads, ordered
-// after the writers' stores by the arrival's release and the last arriver's
-// acquire (which also drops this CU's stale cache lines).  A pass whose units
-// all lie in the padding rows (rows <= 8 of a 16-row block: the draft's 4
-// tokens x 2 query heads) loads nothing (a workgroup-uniform test); rows past
-// rows in a pass that does load read the workspace's row padding and are
-// dropped.
 // Workgroups a KV head's `steps` 32-key steps are dealt to (the caller caps
 // it by the grid): one step a wave up to SIMSD_HEAD_SPW_SWITCH steps, then
 // SIMSD_HEAD_SPW_X2 / 2 steps a wave -- past ~900 slots a partial fewer to
@@ -631,6 +622,15 @@ __host__ __device__ inline int head_split(int steps, int W) {
   return (2 * steps + per - 1) / per;
 }
 
+// The last arriver's merge of the NS partials of KV head h, in workgroup
+// order.  The partial rows and the (max, sum) pairs are all loaded before any
+// is used, so the merge waits for one round trip: plain 16-byte loads, ordered
+// after the writers' stores by the arrival's release and the last arriver's
+// acquire (which also drops this CU's stale cache lines).  A pass whose units
+// all lie in the padding rows (rows <= 8 of a 16-row block: the draft's 4
+// tokens x 2 query heads) loads nothing (a workgroup-uniform test); rows past
+// rows in a pass that does load read the workspace's row padding and are
+// dropped.
 template <int DT, int RBW, int W, int MAXS, int NS>
 SIMSD_DEV void head_merge(HeadShared<RBW, W, MAXS>& sh, const AttnArgs& a, int h, int rows, int M, int n_rep,
                           char* __restrict__ out, int64_t so_m, int64_t so_h) {
