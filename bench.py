@@ -642,7 +642,7 @@ def run_attn(args, torch, dev):
                 unfused()
                 torch.cuda.synchronize()
                 us_unfused = graph_us_per_call(torch, [unfused], reps=max(5, args.steps // 5))
-        except RuntimeError as e:   # no efficient bf16 kernel with a bool mask on this build
+        except RuntimeError as e:   # no efficient bf16 kernel with a bool mask in this torch
             note = f"reference sequence not timed: {str(e).splitlines()[0][:160]}"
     ms = us_fused / 1e3
     gbs = step_bytes / (ms * 1e-3) / 1e9
@@ -1101,8 +1101,8 @@ def main():
                     help="default workload only: skip the C1/C3/C4/C5 records that ride along")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one MI355X; --gpus must be 1 (the hot path "
-              "needs no communication; multi-GPU sharding is described in DESIGN.md)",
+        print("bench.py: measures one MI355X; --gpus must be 1 (the hot path needs no "
+              "communication between GPUs)",
               file=sys.stderr)
         sys.exit(2)
     import torch

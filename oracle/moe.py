@@ -4,7 +4,7 @@ route_topk      top-k routing; ids by a stable sort of -logits (ties -> lower
                 index), scores softmax/sigmoid, renormalised when k > 1,
                 scaled -- the rule of _routing,
                 kernels/workspace/moe_dispatch/build_oracle.py:71-90, with the
-                softmax option BASELINE's MoE config asks for.
+                softmax option the 256-expert, top-8 MoE step uses.
 align           the integer tables of _align, kernels/moe_dispatch_fused.py:93-132
                 (counts, offsets, stable permutation, 16-padded slot table,
                 per-tile experts), plus the padded offsets.

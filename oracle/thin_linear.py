@@ -86,7 +86,7 @@ def tolerance(ref_absmax: float, dtype: str) -> float:
 
 
 def max_abs_rel(got: np.ndarray, ref: np.ndarray) -> float:
-    """max|got - ref| / max|ref| (the BASELINE bar is <= 1e-2)."""
+    """max|got - ref| / max|ref| (the parity bar of the bf16 linear is <= 1e-2)."""
     ref = np.asarray(ref, dtype=np.float64)
     den = float(np.abs(ref).max()) if ref.size else 0.0
     err = float(np.abs(np.asarray(got, dtype=np.float64) - ref).max()) if ref.size else 0.0

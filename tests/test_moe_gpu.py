@@ -10,7 +10,7 @@
   and random/edge cases (duipai.py:119-147) within the reference's bounds
   against the oracle, plus its fp64 gate (fused error <= 1.5 x the stock
   path's error); graph capture with a routing changed between replays; the
-  BASELINE MoE config (T in {4, 16, 64}, E=256, k=8, H=2048, I=512, shared
+  benchmarked MoE step (T in {4, 16, 64}, E=256, k=8, H=2048, I=512, shared
   expert) end to end.
 """
 from __future__ import annotations
@@ -405,7 +405,7 @@ def test_graph_capture_with_new_routing():
             assert torch.equal(out, eager), r
 
 
-# ───────────────────────────────────────────── the BASELINE MoE config (C4) ───
+# ──────────────────── the benchmarked MoE step (T 4/16/64, E=256, k=8) ───
 @pytest.mark.parametrize("T", [4, 16, 64])
 def test_moe_forward_c4(T):
     from kernels.moe_dispatch_fused import moe_forward, moe_route

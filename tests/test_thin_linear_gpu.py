@@ -8,9 +8,9 @@ toggle), against the same bound: live ``F.linear`` within 2^-7*max|ref|+1e-3
 (bf16) / 1e-5*max(1, max|ref|) (fp32).  On top of that:
 
 * bit-exact golden vectors (small-integer and K=1 cases, tests/golden/);
-* the oracle (exact sum, rounded once) at BASELINE shapes: C1 gate_up, the C2
-  draft set at M=4, the C3 target set at M=16/32, within tolerance and the
-  BASELINE bar max-abs-rel <= 1e-2;
+* the oracle (exact sum, rounded once) at the benchmarked shapes: the draft's
+  gate_up, the draft set at M=4, the target set at M=16/32, within tolerance
+  and the relative bar max-abs-rel <= 1e-2;
 * size-independent properties at full size: bitwise determinism, row
   independence (a batch equals its rows computed alone), exact linearity in
   a power-of-two scale, strided view == contiguous copy.
@@ -357,7 +357,7 @@ def test_golden_k1_bitexact(golden):
     assert np.array_equal(got.float().cpu().numpy().astype(np.float64), d["y"])
 
 
-# ─────────────────────────────────────────── oracle at the BASELINE shapes ───
+# ──────────────────────────────────────── oracle at the benchmarked shapes ───
 def _oracle_check(M, K, N, seed):
     from kernels.thin_linear_fused import thin_linear
     x = rnd(M, K, seed=seed)
