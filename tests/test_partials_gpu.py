@@ -125,23 +125,24 @@ def test_reduce_residual_rmsnorm_rejects_bad_input():
                                 g[:12].contiguous(), 1e-6)
 
 
-@pytest.mark.parametrize("M,split", [(36, 2), (32, 1), (12, 4), (48, 2)])
-def test_reduce_qkv_rope_cache_equals_reduce_then_prologue(M, split):
+@pytest.mark.parametrize("M,split,dtype", [(36, 2, torch.bfloat16), (32, 1, torch.bfloat16), (12, 4, torch.bfloat16),
+                                           (48, 2, torch.bfloat16), (36, 2, torch.float16)])
+def test_reduce_qkv_rope_cache_equals_reduce_then_prologue(M, split, dtype):
     from kernels.attention_fused import (BlockKVCache, default_inv_freq, qkv_rope_cache, reduce_qkv_rope_cache,
                                          rope_tables)
     from kernels.thin_linear_fused import thin_linear, thin_linear_partials
-    print(f"reduce+qkv_rope_cache: M={M} split={split}", flush=True)
+    print(f"reduce+qkv_rope_cache: M={M} split={split} dtype={dtype}", flush=True)
     Hq, Hkv, D, H, eps = 32, 8, 128, 4096, 1e-6
-    x = rnd(M, H, seed=M + 30)
-    w = rnd((Hq + 2 * Hkv) * D, H, scale=0.02, seed=M + 31)
-    qn = (1 + 0.1 * rnd(D, dtype=torch.float32, seed=M + 32)).bfloat16()
-    kn = (1 + 0.1 * rnd(D, dtype=torch.float32, seed=M + 33)).bfloat16()
-    cos, sin = rope_tables(default_inv_freq(device=DEV), 4096, torch.bfloat16)
+    x = rnd(M, H, dtype=dtype, seed=M + 30)
+    w = rnd((Hq + 2 * Hkv) * D, H, dtype=dtype, scale=0.02, seed=M + 31)
+    qn = (1 + 0.1 * rnd(D, dtype=torch.float32, seed=M + 32)).to(dtype)
+    kn = (1 + 0.1 * rnd(D, dtype=torch.float32, seed=M + 33)).to(dtype)
+    cos, sin = rope_tables(default_inv_freq(device=DEV), 4096, dtype)
     pos = torch.arange(500, 500 + M, device=DEV)
     pos[1] = -1                                               # out of range: zero q row, no k write
     slots = torch.arange(900, 900 + M, device=DEV)
     slots2 = torch.arange(600, 600 + M, device=DEV)
-    caches = [BlockKVCache(1, Hkv, 1024, 64, DEV) for _ in range(2)]
+    caches = [BlockKVCache(1, Hkv, 1024, 64, DEV, dtype=dtype) for _ in range(2)]
     cfg = (64, 24, 256, split)
     with torch.inference_mode():
         part = thin_linear_partials(x, w, config=cfg)
